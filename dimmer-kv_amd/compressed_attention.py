@@ -1,0 +1,202 @@
+"""Attention over the compressed cache, without rebuilding the FP16 cache (MI355X HIP path).
+
+Mirror of scripts/compressed_attention.py (SrikanthBalaaji/Dimmer-KV).  The
+maths is the reference's (:1-19): keys are rebuilt one layer at a time from
+coefficients x that layer's basis slice + mean, RoPE'd at their positions,
+scored and discarded; values stay in coefficient space,
+``sum_n p_n v_n = (sum_n p_n c_n) @ B_v + mean_v * sum_n p_n``; one softmax
+spans the compressed tokens and a small exact cache (sinks, recent window,
+new tokens).
+
+What changes is where it runs: every step is a hand-written HIP kernel in
+libdimmerkv_hip.so (include/dimmerkv.h).  The coefficients are read straight
+from the packed bit-plane hot tier (hot_tier.PackedStream): the key codes are
+unpacked into LDS and multiplied on MFMA, so neither the FP16 key cache nor a
+coefficient matrix is materialised.
+
+``CompressedContext.attend`` keeps the reference's contract (:113-137):
+(module, query [B, Hq, q_len, d], key/value [B, Hkv, T_exact, d] exact cache
+after ``update``, additive attention_mask or None, scaling) ->
+(output [B, q_len, Hq, d] contiguous, None).
+"""
+
+from __future__ import annotations
+
+import torch
+
+import dkv_hip
+from hot_tier import PackedStream
+
+
+class ModelTables:
+    """Per-model device tables shared by every conversation (the reference's basis/mean,
+    scripts/compressed_attention.py:45-54): fp16 key/value bases in the kernels' layouts,
+    float32 means [L, Hkv*d] and the RoPE half-tables [P, d/2] (cos/sin of
+    scripts/kvtc.py:32-37; the two halves of HF's emb are equal)."""
+
+    def __init__(self, basis_k: torch.Tensor, basis_v: torch.Tensor, mean_k: torch.Tensor, mean_v: torch.Tensor,
+                 layers: int, kv_heads: int, head_dim: int, cos: torch.Tensor, sin: torch.Tensor):
+        if not basis_k.is_cuda:
+            raise ValueError("ModelTables needs GPU tensors (the HIP path has no CPU fallback)")
+        features, rank = basis_k.shape
+        if features != layers * kv_heads * head_dim or rank % 128:
+            raise ValueError(f"basis [{features}, {rank}] does not match L*Hkv*d = {layers * kv_heads * head_dim}"
+                             " with a rank that is a multiple of 128")
+        self.layers, self.kv_heads, self.head_dim, self.rank = layers, kv_heads, head_dim, rank
+        device = basis_k.device
+        self.key_basis = torch.empty(layers * rank * kv_heads * head_dim, dtype=torch.float16, device=device)
+        self.value_basis = torch.empty_like(self.key_basis)
+        dkv_hip.prepare_key_basis(basis_k.float().contiguous(), layers, kv_heads, head_dim, rank, self.key_basis)
+        dkv_hip.prepare_value_basis(basis_v.float().contiguous(), layers, kv_heads, head_dim, rank,
+                                    self.value_basis)
+        self.mean_k = mean_k.float().reshape(layers, kv_heads * head_dim).contiguous()
+        self.mean_v = mean_v.float().reshape(layers, kv_heads * head_dim).contiguous()
+        half = head_dim // 2
+        self.rope_cos = cos[:, :half].float().contiguous()
+        self.rope_sin = sin[:, :half].float().contiguous()
+
+    def basis_bytes(self) -> int:
+        return (self.key_basis.numel() + self.value_basis.numel()) * 2
+
+
+class CompressedContext:
+    """Compressed middle tokens of one or more conversations, attended to directly.
+
+    ``cu_seqlens`` (int32 [B+1]) splits the packed streams into B
+    conversations for a fused varlen decode; B = 1 is the reference's case.
+    """
+
+    def __init__(self, tables: ModelTables, key: PackedStream, value: PackedStream, positions: torch.Tensor,
+                 q_heads: int, cu_seqlens: torch.Tensor | None = None, exact_cache=None):
+        if key.n != value.n:
+            raise ValueError("key and value streams hold different token counts")
+        self.tables, self.key, self.value = tables, key, value
+        self.q_heads = q_heads
+        device = key.blob.device
+        self.positions = positions.to(device=device, dtype=torch.int32).contiguous()
+        if cu_seqlens is None:
+            cu_seqlens = torch.tensor([0, key.n], dtype=torch.int32)
+        self.cu_host = cu_seqlens.to(torch.int32).cpu().contiguous()
+        self.cu = self.cu_host.to(device)
+        self.batch = self.cu_host.numel() - 1
+        self.exact_cache = exact_cache
+        self._workspace = None
+        self._cu_exact = {}
+
+    # ----- memory accounting (scripts/compressed_attention.py:91-102) -----
+    def code_bytes(self) -> int:
+        """Bytes held for the compressed tokens: the packed hot tiers (reference accounting)."""
+        return self.key.hot_bytes() + self.value.hot_bytes()
+
+    def basis_bytes(self) -> int:
+        return self.tables.basis_bytes()
+
+    def exact_bytes(self) -> int:
+        if self.exact_cache is None:
+            return 0
+        layers = self.exact_cache.layers
+        return sum((l.keys.numel() + l.values.numel()) * l.keys.element_size() for l in layers)
+
+    # ----- attention -----
+    def _exact_offsets(self, lengths: tuple[int, ...]):
+        if lengths not in self._cu_exact:
+            host = torch.zeros(len(lengths) + 1, dtype=torch.int32)
+            host[1:] = torch.cumsum(torch.tensor(lengths, dtype=torch.int32), 0)
+            self._cu_exact[lengths] = (host, host.to(self.key.blob.device))
+        return self._cu_exact[lengths]
+
+    def layer_args(self, layer: int, query: torch.Tensor, out: torch.Tensor, key_exact: torch.Tensor | None = None,
+                   value_exact: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+                   exact_lengths: tuple[int, ...] | None = None, scaling: float | None = None):
+        """Build the C-ABI argument block of one layer.  query [B, Hq, q_len, d] (f32/f16/bf16);
+        out [B, q_len, Hq, d]; key/value_exact float32 [Hkv, E_total, d] (RoPE applied);
+        mask float32 [q_len, E] (B == 1)."""
+        t = self.tables
+        batch, q_heads, q_len, dim = query.shape
+        if batch != self.batch or q_heads != self.q_heads or dim != t.head_dim:
+            raise ValueError(f"query {tuple(query.shape)} does not match the context "
+                             f"(batch {self.batch}, {self.q_heads} heads, head_dim {t.head_dim})")
+        a = dkv_hip.AttendArgs()
+        a.batch, a.q_len = batch, q_len
+        a.layers, a.layer, a.kv_heads, a.head_dim, a.q_heads, a.rank = (t.layers, layer, t.kv_heads, t.head_dim,
+                                                                         q_heads, t.rank)
+        a.scaling = dim ** -0.5 if scaling is None else float(scaling)
+        a.key, a.value = self.key.c_stream(), self.value.c_stream()
+        a.cu_seqlens = self.cu.data_ptr()
+        a.cu_seqlens_host = self.cu_host.data_ptr()
+        a.positions = self.positions.data_ptr()
+        a.key_basis, a.value_basis = t.key_basis.data_ptr(), t.value_basis.data_ptr()
+        a.mean_k, a.mean_v = t.mean_k.data_ptr(), t.mean_v.data_ptr()
+        a.rope_cos, a.rope_sin, a.rope_rows = t.rope_cos.data_ptr(), t.rope_sin.data_ptr(), t.rope_cos.shape[0]
+        a.query, a.query_dtype = dkv_hip.ptr(query), dkv_hip.dtype_code(query.dtype)
+        if key_exact is not None and key_exact.shape[1] > 0:
+            lengths = exact_lengths if exact_lengths is not None else (key_exact.shape[1],)
+            host, dev = self._exact_offsets(tuple(int(x) for x in lengths))
+            a.cu_exact, a.cu_exact_host = dev.data_ptr(), host.data_ptr()
+            a.key_exact, a.value_exact = dkv_hip.ptr(key_exact), dkv_hip.ptr(value_exact)
+            a.mask = dkv_hip.ptr(mask) if mask is not None else None
+        a.out, a.out_dtype = dkv_hip.ptr(out), dkv_hip.dtype_code(out.dtype)
+        return a
+
+    def workspace(self, args) -> torch.Tensor:
+        need = dkv_hip.attend_workspace_bytes(args)
+        if self._workspace is None or self._workspace.numel() < need:
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.key.blob.device)
+        return self._workspace
+
+    def attend(self, module, query, key, value, attention_mask, scaling):
+        """Same contract as an HF attention function: returns (output [B, T, H, D], None)."""
+        layer = module.layer_idx
+        if module.num_key_value_groups * self.tables.kv_heads != query.shape[1]:
+            raise ValueError("module.num_key_value_groups does not match the context's GQA grouping")
+        query = query.contiguous()
+        batch, q_heads, q_len, dim = query.shape
+        out = torch.empty(batch, q_len, q_heads, dim, dtype=query.dtype, device=query.device)
+        key_exact = value_exact = mask = None
+        lengths = None
+        if key is not None and key.shape[2] > 0:
+            if batch != 1:
+                raise ValueError("exact caches with batch > 1 go through layer_args(exact_lengths=...)")
+            key_exact = key[0].float().contiguous()
+            value_exact = value[0].float().contiguous()
+            lengths = (key.shape[2],)
+            if attention_mask is not None:
+                mask = attention_mask[0, 0, :, -key.shape[2]:].float().contiguous()
+        args = self.layer_args(layer, query, out, key_exact, value_exact, mask, lengths, scaling)
+        dkv_hip.attend_layer(args, self.workspace(args))
+        return out, None
+
+
+def greedy_answer(model, tokenizer, context: CompressedContext | None, cache, input_ids: torch.Tensor,
+                  start_position: int, max_new_tokens: int = 12, evicted=None, stop_at_eos: bool = True):
+    """Greedy decoding on top of a prefilled cache (scripts/compressed_attention.py:140-169).
+
+    With ``context`` set, attention runs over the compressed tokens directly and
+    ``cache`` must be ``context.exact_cache``.  Returns (text, first-step logits)."""
+    import dimmer
+
+    device = input_ids.device
+    dimmer.STATE.compressed = context
+    dimmer.set_eviction(evicted)
+    generated, first_logits = [], None
+    try:
+        ids = input_ids
+        position = start_position
+        for _ in range(max_new_tokens):
+            positions = torch.arange(position, position + ids.shape[1], device=device)[None]
+            logits = model(input_ids=ids, past_key_values=cache, position_ids=positions, use_cache=True).logits
+            if first_logits is None:
+                first_logits = logits[0, -1].float()
+            position += ids.shape[1]
+            token = int(logits[0, -1].argmax())
+            if stop_at_eos and (token == tokenizer.eos_token_id or token in tokenizer.all_special_ids):
+                break
+            generated.append(token)
+            ids = torch.tensor([[token]], device=device)
+    finally:
+        dimmer.STATE.compressed = None
+        dimmer.set_eviction(None)
+    return tokenizer.decode(generated, skip_special_tokens=True).strip(), first_logits
+
+
+__all__ = ["ModelTables", "CompressedContext", "greedy_answer"]

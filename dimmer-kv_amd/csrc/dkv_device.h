@@ -1,0 +1,171 @@
+// Device-side helpers shared by the Dimmer-KV HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dimmerkv.h"
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+#define DKV_DEVICE __device__ __forceinline__
+
+// 32-bit rotate right by a compile-time amount.
+DKV_DEVICE uint32_t rotr32(uint32_t x, int s) { return s == 0 ? x : ((x >> s) | (x << (32 - s))); }
+
+DKV_DEVICE float half_bits_to_float(uint16_t h) {
+  half_t v;
+  __builtin_memcpy(&v, &h, 2);
+  return (float)v;
+}
+
+DKV_DEVICE float bf16_bits_to_float(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round-to-nearest-even float -> bf16 bits.
+DKV_DEVICE uint16_t float_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+DKV_DEVICE float load_as_float(const void* p, long idx, int dtype) {
+  if (dtype == DKV_F32) return ((const float*)p)[idx];
+  if (dtype == DKV_F16) return half_bits_to_float(((const uint16_t*)p)[idx]);
+  return bf16_bits_to_float(((const uint16_t*)p)[idx]);
+}
+
+DKV_DEVICE void store_from_float(void* p, long idx, int dtype, float v) {
+  if (dtype == DKV_F32) {
+    ((float*)p)[idx] = v;
+  } else if (dtype == DKV_F16) {
+    half_t h = (half_t)v;
+    uint16_t bits;
+    __builtin_memcpy(&bits, &h, 2);
+    ((uint16_t*)p)[idx] = bits;
+  } else {
+    ((uint16_t*)p)[idx] = float_to_bf16_bits(v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bit-plane unpack.
+//
+// A plane word is two u32 halves; half h holds coefficients 32h..32h+31.
+// Coefficient 32h + 4w + i (w in 0..7, i in 0..3) of plane p is stored at bit
+// (8i + w + 7 - p) mod 32 and carries bit (7 - p) of the coefficient's 8-bit
+// code.  Given the (up to 8) plane halves of one (token, group, half), the
+// code word w (four codes, byte i = coefficient 4w+i, truncated to the
+// present planes with the missing low bits 0) is
+//     rotr( OR_p  plane[p] & (0x01010101 << ((w + 7 - p) & 7)),  w ).
+// Absent planes are passed as 0.
+// ---------------------------------------------------------------------------
+template <int W>
+DKV_DEVICE uint32_t assemble_codes(const uint32_t (&pl)[8]) {
+  uint32_t acc = 0;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) acc |= pl[p] & (0x01010101u << ((W + 7 - p) & 7));
+  return rotr32(acc, W);
+}
+
+// Loads the header and plane halves of one (token, group, half).
+// seg points at the group's hot segment ([low f16][span f16][m words]).
+DKV_DEVICE void load_segment(const uint8_t* seg, int m, int half, uint32_t (&pl)[8], uint32_t& header) {
+  const uint32_t* w = (const uint32_t*)seg;
+  header = (m > 0) ? w[0] : 0u;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) pl[p] = (p < m) ? w[1 + 2 * p + half] : 0u;
+}
+
+// Dequantized value in the reference's exact fp32 operation order
+// (scripts/progressive.py:53): low + ((idx + 0.5) * span) / 2^m, every
+// product and sum rounded on its own; m == 0 gives 0.
+DKV_DEVICE float dequant_exact(uint32_t code8, int m, float low, float span, float inv_bins) {
+#pragma clang fp contract(off)
+  if (m == 0) return 0.0f;
+  const uint32_t idx = code8 >> (8 - m);
+  const float prod = ((float)idx + 0.5f) * span;
+  return low + prod * inv_bins;  // * 2^-m is exact, equal to / 2^m
+}
+
+// Per-(token, group) affine form used to feed MFMA operands:
+// value = code8 * scale + offset  with scale = span/256, offset = low + span*2^-(m+1)
+// (equal to the exact form up to one fp32 rounding; the result is then
+// rounded to fp16 anyway).
+struct AffineDq {
+  float scale, offset;
+};
+
+DKV_DEVICE AffineDq affine_from_header(uint32_t header, int m) {
+  AffineDq a;
+  if (m == 0) {
+    a.scale = 0.0f;
+    a.offset = 0.0f;
+  } else {
+    const float low = half_bits_to_float((uint16_t)(header & 0xffffu));
+    const float span = half_bits_to_float((uint16_t)(header >> 16));
+    a.scale = span * (1.0f / 256.0f);
+    a.offset = low + span * __builtin_ldexpf(1.0f, -(m + 1));
+  }
+  return a;
+}
+
+// 32 codes of one (token, group, half) -> 32 fp16 values (affine form),
+// stored as 16 packed half2 words in out[0..15] (element j = coefficient j).
+DKV_DEVICE void unpack_half_f16(const uint32_t (&pl)[8], AffineDq a, uint32_t (&out)[16]) {
+  uint32_t cw[8];
+  cw[0] = assemble_codes<0>(pl);
+  cw[1] = assemble_codes<1>(pl);
+  cw[2] = assemble_codes<2>(pl);
+  cw[3] = assemble_codes<3>(pl);
+  cw[4] = assemble_codes<4>(pl);
+  cw[5] = assemble_codes<5>(pl);
+  cw[6] = assemble_codes<6>(pl);
+  cw[7] = assemble_codes<7>(pl);
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const uint32_t c = cw[w];
+    const float v0 = __builtin_fmaf((float)(c & 0xffu), a.scale, a.offset);
+    const float v1 = __builtin_fmaf((float)((c >> 8) & 0xffu), a.scale, a.offset);
+    const float v2 = __builtin_fmaf((float)((c >> 16) & 0xffu), a.scale, a.offset);
+    const float v3 = __builtin_fmaf((float)(c >> 24), a.scale, a.offset);
+    half_t h0 = (half_t)v0, h1 = (half_t)v1, h2 = (half_t)v2, h3 = (half_t)v3;
+    uint16_t b0, b1, b2, b3;
+    __builtin_memcpy(&b0, &h0, 2);
+    __builtin_memcpy(&b1, &h1, 2);
+    __builtin_memcpy(&b2, &h2, 2);
+    __builtin_memcpy(&b3, &h3, 2);
+    out[2 * w] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+    out[2 * w + 1] = (uint32_t)b2 | ((uint32_t)b3 << 16);
+  }
+}
+
+// Sequence/tile lookup from cu_seqlens without a host-built table: returns
+// the sequence b and the tile index inside it for a global tile id, where
+// sequence b has ceil(len_b / tile) tiles.
+DKV_DEVICE int2 find_tile(const int32_t* cu, int batch, int tile, int gid) {
+  int base = 0;
+  for (int b = 0; b < batch; ++b) {
+    const int len = cu[b + 1] - cu[b];
+    const int nt = (len + tile - 1) / tile;
+    if (gid < base + nt) return make_int2(b, gid - base);
+    base += nt;
+  }
+  return make_int2(-1, 0);
+}
+
+DKV_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+DKV_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}

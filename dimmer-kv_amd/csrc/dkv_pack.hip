@@ -1,0 +1,326 @@
+// Packing, K1 unpack/dequantize, cold-plane gather (K4c) and basis layouts.
+//
+// Reference behaviour replaced here (SrikanthBalaaji/Dimmer-KV):
+//   scripts/progressive.py:47-55   dequantize
+//   scripts/progressive.py:103-110 TokenStore (codes kept unpacked; only counted)
+//   scripts/progressive.py:185-194 hot/cold byte accounting
+//   scripts/progressive.py:224-236 ProgressiveCache.refine (cold pieces of the top tokens)
+#include <string>
+
+#include "dkv_device.h"
+#include "dkv_host.h"
+
+namespace dkv {
+static thread_local std::string g_error;
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+}  // namespace dkv
+
+extern "C" int dkv_abi_version(void) { return DKV_ABI_VERSION; }
+extern "C" const char* dkv_last_error(void) { return dkv::g_error.c_str(); }
+
+// ---------------------------------------------------------------------------
+// Pack: one wave per (token, group).  Lane L owns bit position L of each
+// plane word; it fetches (by cross-lane shuffle) the code of the coefficient
+// that the layout puts at that position and the wave ballots the bit.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_kernel(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ low,
+                                                   const uint16_t* __restrict__ span,
+                                                   const int16_t* __restrict__ pieces, int n, dkv_order_t order,
+                                                   uint8_t* __restrict__ hot, const int64_t* __restrict__ hot_off,
+                                                   uint8_t* __restrict__ cold,
+                                                   const int64_t* __restrict__ cold_tok_off) {
+  const int G = order.groups;
+  const long gw = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (gw >= (long)n * G) return;
+  const int t = (int)(gw / G), g = (int)(gw % G);
+  const int k = pieces[t];
+  const int m = order.planes[(long)k * G + g];
+  const int m_full = order.planes[(long)order.pieces * G + g];
+  const uint32_t code = codes[gw * 64 + lane];
+  uint64_t words[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int jj = ((lane & 31) + 25 + p) & 31;  // (q - 7 + p) mod 32
+    const int coef = (lane & 32) + 4 * (jj & 7) + (jj >> 3);
+    const uint32_t c = (uint32_t)__shfl((int)code, coef, 64);
+    words[p] = __ballot((c >> (7 - p)) & 1u);
+  }
+  const uint32_t header = (uint32_t)low[gw] | ((uint32_t)span[gw] << 16);
+  if (m > 0) {
+    uint32_t* dst = (uint32_t*)(hot + hot_off[t] + order.seg_off[(long)k * G + g]);
+    if (lane == 0) dst[0] = header;
+    if (lane < m) {
+      uint64_t wv = 0;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) wv = (p == lane) ? words[p] : wv;
+      dst[1 + 2 * lane] = (uint32_t)wv;
+      dst[2 + 2 * lane] = (uint32_t)(wv >> 32);
+    }
+  }
+  if (cold != nullptr && m < m_full) {
+    uint32_t* dst = (uint32_t*)(cold + cold_tok_off[t] + order.cold_off[(long)k * G + g]);
+    if (m == 0) {
+      if (lane == 0) dst[0] = header;
+      dst += 1;
+    }
+    if (lane >= m && lane < m_full) {
+      uint64_t wv = 0;
+#pragma unroll
+      for (int p = 0; p < 8; ++p) wv = (p == lane) ? words[p] : wv;
+      dst[2 * (lane - m)] = (uint32_t)wv;
+      dst[2 * (lane - m) + 1] = (uint32_t)(wv >> 32);
+    }
+  }
+}
+
+extern "C" int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const uint16_t* span, const int16_t* pieces,
+                               int32_t n, dkv_order_t order, uint8_t* hot, const int64_t* hot_off, uint8_t* cold,
+                               const int64_t* cold_off, void* stream) {
+  DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_pack_planes: n < 0");
+  int rc = dkv::check_order(order, "dkv_pack_planes");
+  if (rc) return rc;
+  DKV_REQUIRE(codes && low && span && pieces && hot && hot_off, DKV_EINVAL, "dkv_pack_planes: null pointer");
+  DKV_REQUIRE(!cold || (cold_off && order.cold_off), DKV_EINVAL, "dkv_pack_planes: cold needs cold offsets");
+  if (n == 0) return DKV_OK;
+  const long waves = (long)n * order.groups;
+  const long blocks = (waves + 3) / 4;
+  DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_pack_planes: too many tokens");
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), codes, low, span,
+                     pieces, n, order, hot, hot_off, cold, cold_off);
+  return dkv::check_launch("dkv_pack_planes");
+}
+
+// ---------------------------------------------------------------------------
+// K1: one thread per (token, group, half): 32 coefficients.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void unpack_dequant_kernel(dkv_stream_t s, int t0, int nt, void* __restrict__ out) {
+  const int G = s.order.groups;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)nt * G * 2) return;
+  const int h = (int)(id & 1);
+  const long tg = id >> 1;
+  const int tt = (int)(tg / G), g = (int)(tg % G);
+  const int t = t0 + tt;
+  const int k = s.pieces[t];
+  const int m = s.order.planes[(long)k * G + g];
+  const uint8_t* seg = s.blob + s.tok_off[t] + s.order.seg_off[(long)k * G + g];
+  uint32_t pl[8], header;
+  load_segment(seg, m, h, pl, header);
+  const float low = half_bits_to_float((uint16_t)(header & 0xffffu));
+  const float span = half_bits_to_float((uint16_t)(header >> 16));
+  const float inv_bins = __builtin_ldexpf(1.0f, -m);
+  uint32_t cw[8];
+  cw[0] = assemble_codes<0>(pl);
+  cw[1] = assemble_codes<1>(pl);
+  cw[2] = assemble_codes<2>(pl);
+  cw[3] = assemble_codes<3>(pl);
+  cw[4] = assemble_codes<4>(pl);
+  cw[5] = assemble_codes<5>(pl);
+  cw[6] = assemble_codes<6>(pl);
+  cw[7] = assemble_codes<7>(pl);
+  const long base = (long)tt * (64L * G) + g * 64 + h * 32;
+  if (DT == DKV_F32) {
+    float4* o = (float4*)((float*)out + base);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      float4 v;
+      v.x = dequant_exact(cw[w] & 0xffu, m, low, span, inv_bins);
+      v.y = dequant_exact((cw[w] >> 8) & 0xffu, m, low, span, inv_bins);
+      v.z = dequant_exact((cw[w] >> 16) & 0xffu, m, low, span, inv_bins);
+      v.w = dequant_exact(cw[w] >> 24, m, low, span, inv_bins);
+      o[w] = v;
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        store_from_float(out, base + 4 * w + i, DT, dequant_exact((cw[w] >> (8 * i)) & 0xffu, m, low, span, inv_bins));
+    }
+  }
+}
+
+extern "C" int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt, void* out, int32_t out_dtype,
+                                  void* stream) {
+  int rc = dkv::check_stream(s, "dkv_unpack_dequant");
+  if (rc) return rc;
+  DKV_REQUIRE(out, DKV_EINVAL, "dkv_unpack_dequant: out is null");
+  DKV_REQUIRE(t0 >= 0 && nt >= 0, DKV_ESHAPE, "dkv_unpack_dequant: bad token range");
+  DKV_REQUIRE(out_dtype == DKV_F32 || out_dtype == DKV_F16 || out_dtype == DKV_BF16, DKV_EINVAL,
+              "dkv_unpack_dequant: bad dtype %d", out_dtype);
+  if (nt == 0) return DKV_OK;
+  const long threads = (long)nt * s->order.groups * 2;
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  hipStream_t st = dkv::as_stream(stream);
+  if (out_dtype == DKV_F32)
+    hipLaunchKernelGGL(unpack_dequant_kernel<DKV_F32>, dim3(blocks), dim3(256), 0, st, *s, t0, nt, out);
+  else if (out_dtype == DKV_F16)
+    hipLaunchKernelGGL(unpack_dequant_kernel<DKV_F16>, dim3(blocks), dim3(256), 0, st, *s, t0, nt, out);
+  else
+    hipLaunchKernelGGL(unpack_dequant_kernel<DKV_BF16>, dim3(blocks), dim3(256), 0, st, *s, t0, nt, out);
+  return dkv::check_launch("dkv_unpack_dequant");
+}
+
+// Reference dequantize on unpacked codes (progressive.py:47-55).
+__global__ __launch_bounds__(256) void dequantize_codes_kernel(const uint8_t* __restrict__ codes,
+                                                               const uint16_t* __restrict__ low,
+                                                               const uint16_t* __restrict__ span,
+                                                               const uint8_t* __restrict__ planes, int planes_rows,
+                                                               int n, int G, float* __restrict__ out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)n * G * 64) return;
+  const long tg = id >> 6;
+  const int t = (int)(tg / G), g = (int)(tg % G);
+  const int m = planes[(long)(planes_rows == 1 ? 0 : t) * G + g];
+  const float lo = half_bits_to_float(low[tg]);
+  const float sp = half_bits_to_float(span[tg]);
+  out[id] = dequant_exact(codes[id], m, lo, sp, __builtin_ldexpf(1.0f, -m));
+}
+
+extern "C" int dkv_dequantize_codes(const uint8_t* codes, const uint16_t* low, const uint16_t* span,
+                                    const uint8_t* planes, int32_t planes_rows, int32_t n, int32_t groups, float* out,
+                                    void* stream) {
+  DKV_REQUIRE(codes && low && span && planes && out, DKV_EINVAL, "dkv_dequantize_codes: null pointer");
+  DKV_REQUIRE(n >= 0 && groups > 0 && (planes_rows == 1 || planes_rows == n), DKV_ESHAPE,
+              "dkv_dequantize_codes: bad shape (n=%d groups=%d planes_rows=%d)", n, groups, planes_rows);
+  if (n == 0) return DKV_OK;
+  const long total = (long)n * groups * 64;
+  hipLaunchKernelGGL(dequantize_codes_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     dkv::as_stream(stream), codes, low, span, planes, planes_rows, n, groups, out);
+  return dkv::check_launch("dkv_dequantize_codes");
+}
+
+// ---------------------------------------------------------------------------
+// K4c: merge hot + cold segments of selected tokens into full blobs.
+// One workgroup per selected token; one thread per group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const uint8_t* __restrict__ cold,
+                                                         const int64_t* __restrict__ cold_tok_off,
+                                                         const int32_t* __restrict__ idx, uint8_t* __restrict__ refined,
+                                                         int64_t refined_base_off, int64_t* tok_off,
+                                                         int16_t* pieces) {
+  const int G = s.order.groups, K = s.order.pieces;
+  const int r = blockIdx.x;
+  const int t = idx[r];
+  const int k = pieces[t];
+  const int64_t off = tok_off[t];
+  const int full_bytes = s.order.prefix_bytes[K];
+  uint8_t* dst_tok = refined + (long)r * full_bytes;
+  for (int g = threadIdx.x; g < G; g += blockDim.x) {
+    const int m_hot = s.order.planes[(long)k * G + g];
+    const int m_full = s.order.planes[(long)K * G + g];
+    if (m_full == 0) continue;
+    uint32_t* dst = (uint32_t*)(dst_tok + s.order.seg_off[(long)K * G + g]);
+    const uint32_t* hseg = (const uint32_t*)(s.blob + off + s.order.seg_off[(long)k * G + g]);
+    const uint32_t* cseg = (const uint32_t*)(cold + cold_tok_off[t] + s.order.cold_off[(long)k * G + g]);
+    if (m_hot > 0) {
+      dst[0] = hseg[0];
+    } else {
+      dst[0] = cseg[0];
+      cseg += 1;
+    }
+    for (int p = 0; p < m_full; ++p) {
+      const uint32_t* src = (p < m_hot) ? (hseg + 1 + 2 * p) : (cseg + 2 * (p - m_hot));
+      dst[1 + 2 * p] = src[0];
+      dst[2 + 2 * p] = src[1];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    tok_off[t] = refined_base_off + (int64_t)r * full_bytes;
+    pieces[t] = (int16_t)K;
+  }
+}
+
+extern "C" int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const int64_t* cold_tok_off,
+                               const int32_t* idx, int32_t k, uint8_t* refined, int64_t refined_base_off,
+                               int64_t* tok_off, int16_t* pieces, void* stream) {
+  int rc = dkv::check_stream(s, "dkv_gather_cold");
+  if (rc) return rc;
+  DKV_REQUIRE(cold && cold_tok_off && idx && refined && tok_off && pieces && s->order.cold_off, DKV_EINVAL,
+              "dkv_gather_cold: null pointer");
+  DKV_REQUIRE(k >= 0 && refined_base_off >= 0, DKV_ESHAPE, "dkv_gather_cold: bad k / offset");
+  if (k == 0) return DKV_OK;
+  dkv_stream_t view = *s;
+  hipLaunchKernelGGL(gather_cold_kernel, dim3(k), dim3(64), 0, dkv::as_stream(stream), view, cold, cold_tok_off, idx,
+                     refined, refined_base_off, tok_off, pieces);
+  return dkv::check_launch("dkv_gather_cold");
+}
+
+// ---------------------------------------------------------------------------
+// Basis layouts.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void key_basis_kernel(const float* __restrict__ basis, int L, int H, int D, int R,
+                                                        uint16_t* __restrict__ out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)L * H * D * R;
+  if (id >= total) return;
+  // out index = (((l*G + g)*H + h)*D + dd)*64 + kk
+  const int G = R / 64;
+  const int kk = (int)(id & 63);
+  long rest = id >> 6;
+  const int dd = (int)(rest % D);
+  rest /= D;
+  const int h = (int)(rest % H);
+  rest /= H;
+  const int g = (int)(rest % G);
+  const int l = (int)(rest / G);
+  const float v = basis[((long)(l * H + h) * D + dd) * R + g * 64 + kk];
+  half_t hv = (half_t)v;
+  uint16_t bits;
+  __builtin_memcpy(&bits, &hv, 2);
+  out[id] = bits;
+}
+
+__global__ __launch_bounds__(256) void value_basis_kernel(const float* __restrict__ basis, int L, int H, int D, int R,
+                                                          uint16_t* __restrict__ out) {
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)L * H * D * R;
+  if (id >= total) return;
+  // out index = ((l*H + h)*R + k)*D + dd
+  const int dd = (int)(id % D);
+  long rest = id / D;
+  const int k = (int)(rest % R);
+  const long lh = rest / R;
+  const float v = basis[(lh * D + dd) * R + k];
+  half_t hv = (half_t)v;
+  uint16_t bits;
+  __builtin_memcpy(&bits, &hv, 2);
+  out[id] = bits;
+}
+
+static int check_basis_args(const float* basis, int L, int H, int D, int R, const uint16_t* out, const char* what) {
+  DKV_REQUIRE(basis && out, DKV_EINVAL, "%s: null pointer", what);
+  DKV_REQUIRE(L > 0 && H > 0 && D > 0 && R > 0 && R % 64 == 0, DKV_ESHAPE, "%s: bad shape L=%d H=%d D=%d R=%d", what,
+              L, H, D, R);
+  return DKV_OK;
+}
+
+extern "C" int dkv_prepare_key_basis(const float* basis, int32_t layers, int32_t kv_heads, int32_t head_dim,
+                                     int32_t rank, uint16_t* out, void* stream) {
+  int rc = check_basis_args(basis, layers, kv_heads, head_dim, rank, out, "dkv_prepare_key_basis");
+  if (rc) return rc;
+  const long total = (long)layers * kv_heads * head_dim * rank;
+  hipLaunchKernelGGL(key_basis_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, dkv::as_stream(stream),
+                     basis, layers, kv_heads, head_dim, rank, out);
+  return dkv::check_launch("dkv_prepare_key_basis");
+}
+
+extern "C" int dkv_prepare_value_basis(const float* basis, int32_t layers, int32_t kv_heads, int32_t head_dim,
+                                       int32_t rank, uint16_t* out, void* stream) {
+  int rc = check_basis_args(basis, layers, kv_heads, head_dim, rank, out, "dkv_prepare_value_basis");
+  if (rc) return rc;
+  const long total = (long)layers * kv_heads * head_dim * rank;
+  hipLaunchKernelGGL(value_basis_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, dkv::as_stream(stream),
+                     basis, layers, kv_heads, head_dim, rank, out);
+  return dkv::check_launch("dkv_prepare_value_basis");
+}

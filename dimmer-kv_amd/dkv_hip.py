@@ -1,0 +1,189 @@
+"""ctypes binding of libdimmerkv_hip.so (the C ABI declared in include/dimmerkv.h).
+
+The library is loaded from this directory.  There is no fallback: if the
+library is missing, or a tensor is not on a GPU, the call raises.  Return
+codes map to the reference's exception types (scripts/kvtc.py:226-227,
+289-290 ValueError; scripts/progressive.py:189-190 AssertionError;
+scripts/methods.py:136-137 RuntimeError).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libdimmerkv_hip.so"
+ABI_VERSION = 1
+
+DKV_F32, DKV_F16, DKV_BF16 = 0, 1, 2
+_DTYPE = {torch.float32: DKV_F32, torch.float16: DKV_F16, torch.bfloat16: DKV_BF16}
+
+EXPORTS = [
+    "dkv_abi_version", "dkv_last_error", "dkv_pack_planes", "dkv_unpack_dequant", "dkv_dequantize_codes",
+    "dkv_prepare_key_basis", "dkv_prepare_value_basis", "dkv_attend_workspace_bytes", "dkv_attend_layer",
+    "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
+    "dkv_gather_cold",
+]
+
+c_i32, c_i64, c_f32, c_vp, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+
+class Order(ctypes.Structure):
+    _fields_ = [("groups", c_i32), ("pieces", c_i32), ("planes", c_vp), ("seg_off", c_vp), ("cold_off", c_vp),
+                ("prefix_bytes", c_vp)]
+
+
+class Stream(ctypes.Structure):
+    _fields_ = [("blob", c_vp), ("tok_off", c_vp), ("pieces", c_vp), ("order", Order)]
+
+
+class AttendArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("q_len", c_i32),
+        ("layers", c_i32), ("layer", c_i32), ("kv_heads", c_i32), ("head_dim", c_i32), ("q_heads", c_i32),
+        ("rank", c_i32),
+        ("scaling", c_f32),
+        ("key", Stream), ("value", Stream),
+        ("cu_seqlens", c_vp), ("cu_seqlens_host", c_vp), ("positions", c_vp),
+        ("key_basis", c_vp), ("value_basis", c_vp), ("mean_k", c_vp), ("mean_v", c_vp),
+        ("rope_cos", c_vp), ("rope_sin", c_vp), ("rope_rows", c_i32),
+        ("query", c_vp), ("query_dtype", c_i32),
+        ("cu_exact", c_vp), ("cu_exact_host", c_vp), ("key_exact", c_vp), ("value_exact", c_vp), ("mask", c_vp),
+        ("out", c_vp), ("out_dtype", c_i32),
+    ]
+
+
+class DkvError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library once; raise loudly if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                               "(python dimmer-kv_amd/build_lib.py); there is no CPU fallback")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        handle.dkv_abi_version.restype = c_i32
+        handle.dkv_last_error.restype = ctypes.c_char_p
+        for name in ("dkv_attend_workspace_bytes", "dkv_score_workspace_bytes", "dkv_topk_workspace_bytes"):
+            getattr(handle, name).restype = c_sz
+        handle.dkv_topk_workspace_bytes.argtypes = [c_i32]
+        if handle.dkv_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {handle.dkv_abi_version()}, expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    msg = f"{what}: {lib().dkv_last_error().decode()} (code {rc})"
+    if rc in (-1, -2):
+        raise ValueError(msg)
+    if rc == -5:
+        raise AssertionError(msg)
+    raise DkvError(msg)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("dimmer-kv HIP kernels need GPU tensors (no CPU path)")
+    if not t.is_contiguous():
+        raise ValueError("dimmer-kv HIP kernels need contiguous tensors")
+    return t.data_ptr()
+
+
+def stream_handle() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype not in _DTYPE:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return _DTYPE[dtype]
+
+
+# ----------------------------------------------------------------- wrappers
+
+def pack_planes(codes, low, span, pieces, order: Order, hot, hot_off, cold=None, cold_off=None) -> None:
+    n = codes.shape[0]
+    _check(lib().dkv_pack_planes(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(span)), c_vp(ptr(pieces)), c_i32(n),
+                                 order, c_vp(ptr(hot)), c_vp(ptr(hot_off)), c_vp(ptr(cold)), c_vp(ptr(cold_off)),
+                                 c_vp(stream_handle())), "dkv_pack_planes")
+
+
+def unpack_dequant(stream: Stream, t0: int, nt: int, out: torch.Tensor) -> None:
+    _check(lib().dkv_unpack_dequant(ctypes.byref(stream), c_i32(t0), c_i32(nt), c_vp(ptr(out)),
+                                    c_i32(dtype_code(out.dtype)), c_vp(stream_handle())), "dkv_unpack_dequant")
+
+
+def dequantize_codes(codes, low, span, planes, out) -> None:
+    n, groups = codes.shape[0], codes.shape[1]
+    _check(lib().dkv_dequantize_codes(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(span)), c_vp(ptr(planes)),
+                                      c_i32(planes.shape[0]), c_i32(n), c_i32(groups), c_vp(ptr(out)),
+                                      c_vp(stream_handle())), "dkv_dequantize_codes")
+
+
+def prepare_key_basis(basis, layers, kv_heads, head_dim, rank, out) -> None:
+    _check(lib().dkv_prepare_key_basis(c_vp(ptr(basis)), c_i32(layers), c_i32(kv_heads), c_i32(head_dim),
+                                       c_i32(rank), c_vp(ptr(out)), c_vp(stream_handle())), "dkv_prepare_key_basis")
+
+
+def prepare_value_basis(basis, layers, kv_heads, head_dim, rank, out) -> None:
+    _check(lib().dkv_prepare_value_basis(c_vp(ptr(basis)), c_i32(layers), c_i32(kv_heads), c_i32(head_dim),
+                                         c_i32(rank), c_vp(ptr(out)), c_vp(stream_handle())),
+           "dkv_prepare_value_basis")
+
+
+def attend_workspace_bytes(args: AttendArgs) -> int:
+    n = lib().dkv_attend_workspace_bytes(ctypes.byref(args))
+    if n == 0:
+        _check(-2, "dkv_attend_workspace_bytes")
+    return n
+
+
+def attend_layer(args: AttendArgs, workspace: torch.Tensor) -> None:
+    _check(lib().dkv_attend_layer(ctypes.byref(args), c_vp(ptr(workspace)), c_sz(workspace.numel()),
+                                  c_vp(stream_handle())), "dkv_attend_layer")
+
+
+def score_workspace_bytes(args: AttendArgs) -> int:
+    n = lib().dkv_score_workspace_bytes(ctypes.byref(args))
+    if n == 0:
+        _check(-2, "dkv_score_workspace_bytes")
+    return n
+
+
+def score_begin(importance: torch.Tensor) -> None:
+    _check(lib().dkv_score_begin(c_vp(ptr(importance)), c_i32(importance.numel()), c_vp(stream_handle())),
+           "dkv_score_begin")
+
+
+def score_layer(args: AttendArgs, key_question: torch.Tensor, importance: torch.Tensor,
+                workspace: torch.Tensor) -> None:
+    _check(lib().dkv_score_layer(ctypes.byref(args), c_vp(ptr(key_question)), c_vp(ptr(importance)),
+                                 c_vp(ptr(workspace)), c_sz(workspace.numel()), c_vp(stream_handle())),
+           "dkv_score_layer")
+
+
+def topk(scores: torch.Tensor, k: int, out: torch.Tensor) -> None:
+    _check(lib().dkv_topk(c_vp(ptr(scores)), c_i32(scores.numel()), c_i32(k), c_vp(ptr(out)), c_vp(None), c_sz(0),
+                          c_vp(stream_handle())), "dkv_topk")
+
+
+def gather_cold(stream: Stream, cold, cold_tok_off, idx, refined_base_off: int, blob, tok_off, pieces) -> None:
+    k = idx.numel()
+    refined_ptr = ptr(blob) + refined_base_off
+    _check(lib().dkv_gather_cold(ctypes.byref(stream), c_vp(ptr(cold)), c_vp(ptr(cold_tok_off)), c_vp(ptr(idx)),
+                                 c_i32(k), c_vp(refined_ptr), c_i64(refined_base_off), c_vp(ptr(tok_off)),
+                                 c_vp(ptr(pieces)), c_vp(stream_handle())), "dkv_gather_cold")

@@ -1,0 +1,143 @@
+"""Packed hot/cold bit-plane tiers of one stream on the GPU.
+
+The reference keeps progressive codes unpacked in a ``TokenStore``
+(scripts/progressive.py:103-110) and only counts their bytes
+(:185-194).  Here the bytes exist: a token's hot blob holds, for every group
+with m > 0 planes, ``[low f16][span f16][m plane words]`` and is exactly
+``order.prefix_bytes[pieces[t]]`` bytes; its cold blob holds the remaining
+pieces (``prefix_bytes[-1] - prefix_bytes[pieces[t]]`` bytes, the
+reference's ``fetched``, :232).  The plane-word bit order is fixed by
+include/dimmerkv.h / oracle/packing_ref.py.
+
+``PackedStream.refine`` is the cold-plane gather (K4c): selected tokens get
+full blobs in a refine area at the end of the hot allocation, and their
+offsets/piece counts are redirected there, so the attention kernels see the
+refined tokens with no other change.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import dkv_hip
+
+HEADER_BYTES = 4
+PIECE_BYTES = 8
+RUNG_ID_BYTES = 1
+
+
+class OrderTables:
+    """Device copies of one stream's order plus the derived segment-offset tables."""
+
+    def __init__(self, planes, prefix_bytes, device):
+        planes = np.asarray(torch.as_tensor(planes).cpu(), dtype=np.int64)
+        prefix = np.asarray(torch.as_tensor(prefix_bytes).cpu(), dtype=np.int64)
+        self.groups = planes.shape[1]
+        self.pieces = planes.shape[0] - 1
+        m = planes
+        m_full = planes[-1][None, :]
+        seg = np.where(m > 0, HEADER_BYTES + PIECE_BYTES * m, 0)
+        seg_off = np.zeros_like(seg)
+        seg_off[:, 1:] = np.cumsum(seg[:, :-1], axis=1)
+        cold = np.where((m == 0) & (m_full > 0), HEADER_BYTES, 0) + PIECE_BYTES * np.maximum(m_full - m, 0)
+        cold_off = np.zeros_like(cold)
+        cold_off[:, 1:] = np.cumsum(cold[:, :-1], axis=1)
+        if not np.array_equal(seg.sum(axis=1), prefix):
+            raise ValueError("order prefix_bytes do not match its plane table (8 B/piece + 4 B/first plane)")
+        self.prefix_np = prefix
+        self.planes = torch.as_tensor(planes.astype(np.uint8)).to(device)
+        self.seg_off = torch.as_tensor(seg_off.astype(np.int32)).to(device)
+        self.cold_off = torch.as_tensor(cold_off.astype(np.int32)).to(device)
+        self.prefix = torch.as_tensor(prefix.astype(np.int32)).to(device)
+        self.prefix64 = torch.as_tensor(prefix).to(device)
+        self.full_bytes = int(prefix[-1])
+
+    def c_order(self) -> dkv_hip.Order:
+        return dkv_hip.Order(self.groups, self.pieces, self.planes.data_ptr(), self.seg_off.data_ptr(),
+                             self.cold_off.data_ptr(), self.prefix.data_ptr())
+
+
+def _exclusive_cumsum(sizes: torch.Tensor) -> tuple[torch.Tensor, int]:
+    off = torch.zeros(sizes.numel(), dtype=torch.int64, device=sizes.device)
+    if sizes.numel() > 1:
+        off[1:] = torch.cumsum(sizes[:-1], 0)
+    total = int(sizes.sum()) if sizes.numel() else 0
+    return off, total
+
+
+class PackedStream:
+    """Hot + cold tiers of one stream (keys or values) for n tokens."""
+
+    def __init__(self, tables: OrderTables, blob, tok_off, pieces, cold, cold_off, hot_used: int, refine_capacity: int):
+        self.tables = tables
+        self.blob, self.tok_off, self.pieces = blob, tok_off, pieces
+        self.cold, self.cold_off = cold, cold_off
+        self.hot_used = hot_used
+        self.refine_capacity = refine_capacity
+        self.refined = 0
+        self.initial_pieces = pieces.clone()
+
+    @property
+    def n(self) -> int:
+        return self.pieces.numel()
+
+    @classmethod
+    def pack(cls, codes: torch.Tensor, low: torch.Tensor, span: torch.Tensor, pieces: torch.Tensor,
+             tables: OrderTables, refine_capacity: int = 0, with_cold: bool = True) -> "PackedStream":
+        """codes u8 [n, G, 64], low/span f16 [n, G], pieces [n] -> packed tiers (GPU pack kernel)."""
+        device = codes.device
+        n = codes.shape[0]
+        pieces = pieces.to(device=device, dtype=torch.int16).contiguous()
+        p64 = pieces.long()
+        hot_sizes = tables.prefix64[p64] if n else torch.zeros(0, dtype=torch.int64, device=device)
+        tok_off, hot_total = _exclusive_cumsum(hot_sizes)
+        capacity = hot_total + refine_capacity * tables.full_bytes
+        blob = torch.zeros(max(capacity, 16), dtype=torch.uint8, device=device)
+        cold = cold_off = None
+        if with_cold:
+            cold_sizes = tables.full_bytes - hot_sizes
+            cold_off, cold_total = _exclusive_cumsum(cold_sizes)
+            cold = torch.zeros(max(cold_total, 16), dtype=torch.uint8, device=device)
+        if n:
+            dkv_hip.pack_planes(codes.contiguous(), low.contiguous().view(torch.int16),
+                                span.contiguous().view(torch.int16), pieces, tables.c_order(), blob, tok_off,
+                                cold, cold_off)
+        return cls(tables, blob, tok_off, pieces, cold, cold_off, hot_total, refine_capacity)
+
+    def c_stream(self) -> dkv_hip.Stream:
+        return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(),
+                              self.tables.c_order())
+
+    def dequantize(self, t0: int = 0, nt: int | None = None, dtype=torch.float32) -> torch.Tensor:
+        """K1: coefficients [nt, 64G] of tokens t0.. at their hot prefix (bit-exact in float32)."""
+        nt = self.n - t0 if nt is None else nt
+        out = torch.empty(nt, 64 * self.tables.groups, dtype=dtype, device=self.blob.device)
+        if nt:
+            dkv_hip.unpack_dequant(self.c_stream(), t0, nt, out)
+        return out
+
+    def hot_bytes(self) -> int:
+        """Reference accounting of this stream's hot tier (progressive.py:185-188, without exact tokens)."""
+        return int(self.tables.prefix64[self.pieces.long()].sum()) + RUNG_ID_BYTES * self.n
+
+    def cold_bytes(self) -> int:
+        return int((self.tables.full_bytes - self.tables.prefix64[self.pieces.long()]).sum())
+
+    def refine(self, rows: torch.Tensor) -> int:
+        """K4c: fetch the cold pieces of ``rows`` (stream-local, unique) -> bytes fetched (progressive.py:232)."""
+        rows = rows.to(device=self.blob.device, dtype=torch.int64)
+        rows = rows[self.pieces[rows].long() < self.tables.pieces].to(torch.int32).contiguous()
+        k = rows.numel()
+        if k == 0:
+            return 0
+        if self.cold is None:
+            raise ValueError("this stream was packed without a cold tier")
+        if self.refined + k > self.refine_capacity:
+            raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
+        fetched = int((self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum())
+        base = self.hot_used + self.refined * self.tables.full_bytes
+        dkv_hip.gather_cold(self.c_stream(), self.cold, self.cold_off, rows, base, self.blob, self.tok_off,
+                            self.pieces)
+        self.refined += k
+        return fetched

@@ -1,0 +1,189 @@
+/*
+ * dimmerkv.h - C ABI of libdimmerkv_hip.so, the MI355X (gfx950) kernels for
+ * Dimmer-KV's answer-time path: decode attention run directly over a
+ * per-token variable-precision, bit-plane-coded, cross-layer-PCA KV cache.
+ *
+ * The reference (SrikanthBalaaji/Dimmer-KV) is pure Python on PyTorch; its
+ * "interface" for this path is a set of Python functions.  Each entry point
+ * below names the reference function whose work it replaces.  The Python
+ * modules in dimmer-kv_amd/ (progressive.py, compressed_attention.py,
+ * methods.py, dimmer.py) keep the reference's API and call these through
+ * ctypes.
+ *
+ * Conventions
+ * - Every pointer in a struct or argument is a device pointer unless its
+ *   comment says "host".
+ * - The library never allocates or frees memory.  Kernels that need scratch
+ *   memory take a caller-provided workspace sized by the matching
+ *   *_workspace_bytes() query.
+ * - Calls are asynchronous on the given stream (hipStream_t passed as void*;
+ *   NULL = the default stream) and never synchronise the host.
+ * - Every entry point validates its arguments before launching anything and
+ *   returns 0 on success or a negative DKV_E* code; dkv_last_error() then
+ *   holds a message (thread-local).
+ */
+#ifndef DIMMERKV_H
+#define DIMMERKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DKV_ABI_VERSION 1
+
+/* Status codes.  The Python wrapper maps them to the reference's exception
+ * types: DKV_EINVAL/DKV_ESHAPE -> ValueError, DKV_EBUDGET -> AssertionError,
+ * DKV_ELAUNCH/DKV_EWORKSPACE -> RuntimeError. */
+#define DKV_OK 0
+#define DKV_EINVAL (-1)     /* null pointer or bad enum */
+#define DKV_ESHAPE (-2)     /* inconsistent sizes */
+#define DKV_EWORKSPACE (-3) /* workspace too small */
+#define DKV_ELAUNCH (-4)    /* hipGetLastError after launch */
+#define DKV_EBUDGET (-5)    /* byte budget exceeded */
+
+/* Element types of query / output / dequantized coefficients. */
+#define DKV_F32 0
+#define DKV_F16 1
+#define DKV_BF16 2
+
+/* Progressive order of one stream (scripts/progressive.py:58-64 Order):
+ * the per-token plane map is planes[pieces[t]].  seg_off / cold_off are
+ * derived tables (byte offset of group g's segment in a hot / cold token blob
+ * whose hot prefix is k pieces); prefix_bytes[k] is the hot blob size. */
+typedef struct dkv_order {
+  int32_t groups;              /* G = rank / 64 */
+  int32_t pieces;              /* K = number of (group, plane) pieces, <= 8G */
+  const uint8_t* planes;       /* [K+1][G] */
+  const int32_t* seg_off;      /* [K+1][G] */
+  const int32_t* cold_off;     /* [K+1][G] */
+  const int32_t* prefix_bytes; /* [K+1] */
+} dkv_order_t;
+
+/* One stream (keys or values) of a packed hot tier.  Token t's hot blob
+ * starts at blob + tok_off[t] and holds pieces[t] pieces
+ * (prefix_bytes[pieces[t]] bytes).  Layout: for every group with m > 0
+ * planes, [low f16][span f16][m plane words of 8 B]; plane-word bit order is
+ * documented in oracle/packing_ref.py and DESIGN.md. */
+typedef struct dkv_stream {
+  const uint8_t* blob;
+  const int64_t* tok_off; /* [n] */
+  const int16_t* pieces;  /* [n] */
+  dkv_order_t order;
+} dkv_stream_t;
+
+int dkv_abi_version(void);
+const char* dkv_last_error(void);
+
+/* ---- packing (encoder side; scripts/progressive.py:103-110 TokenStore,
+ *      byte accounting :185-194) ------------------------------------------ */
+
+/* codes u8 [n][G][64], low/span f16 [n][G], pieces [n] -> hot blob at
+ * hot_off[t] and cold blob at cold_off[t] (both int64 [n], byte offsets).
+ * The cold blob of a token is [low,span if m==0][planes m..7] per group. */
+int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const uint16_t* span, const int16_t* pieces,
+                    int32_t n, dkv_order_t order, uint8_t* hot, const int64_t* hot_off, uint8_t* cold,
+                    const int64_t* cold_off, void* stream);
+
+/* ---- K1: unpack + dequantize (replaces scripts/progressive.py:47-55
+ *      dequantize applied to TokenStore rows at their hot prefix, :196-201) -
+ * Tokens t0..t0+nt-1 of the stream -> out [nt][64G] in out_dtype.  With
+ * DKV_F32 the values are bit-identical to the reference's fp32 dequantize. */
+int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt, void* out, int32_t out_dtype,
+                       void* stream);
+
+/* Reference dequantize on unpacked codes (scripts/progressive.py:47-55):
+ * codes u8 [n][G][64], low/span f16 [n][G], planes u8 [n or 1][G] -> f32 [n][64G]. */
+int dkv_dequantize_codes(const uint8_t* codes, const uint16_t* low, const uint16_t* span, const uint8_t* planes,
+                         int32_t planes_rows, int32_t n, int32_t groups, float* out, void* stream);
+
+/* ---- bases ----------------------------------------------------------------
+ * basis f32 [F][r] (columns = components, F = L*Hkv*d, row f = (l*Hkv+h)*d+dd;
+ * scripts/kvtc.py:100-105, :88-97) -> the fp16 layouts the attention kernels
+ * read:  key basis  [L][G][Hkv][d][64]  (per layer and 64-component group,
+ *        every head's d x 64 block, components contiguous);
+ *        value basis [L][Hkv][r][d]. */
+int dkv_prepare_key_basis(const float* basis, int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t rank,
+                          uint16_t* out, void* stream);
+int dkv_prepare_value_basis(const float* basis, int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t rank,
+                            uint16_t* out, void* stream);
+
+/* ---- K2 + K3: one layer of attention over the codes ---------------------
+ * Replaces scripts/compressed_attention.py:105-137 (CompressedContext._keys
+ * and .attend): keys of the layer are rebuilt from the key codes on MFMA,
+ * RoPE'd and scored without being written to memory; one softmax covers the
+ * compressed tokens and the exact tokens; values are weighted in coefficient
+ * space and the value basis is applied once per KV head.
+ *
+ * Sequences: `batch` conversations share the packed streams; sequence b owns
+ * compressed tokens [cu_seqlens[b], cu_seqlens[b+1]) and exact tokens
+ * [cu_exact[b], cu_exact[b+1]) (both int32 device arrays, batch+1 entries;
+ * cu_seqlens_host mirrors cu_seqlens on the host to size the launch). */
+typedef struct dkv_attend_args {
+  int32_t batch, q_len;
+  int32_t layers, layer, kv_heads, head_dim, q_heads, rank;
+  float scaling;
+  dkv_stream_t key, value;
+  const int32_t* cu_seqlens;      /* [batch+1] */
+  const int32_t* cu_seqlens_host; /* host [batch+1] */
+  const int32_t* positions;       /* [n_total] RoPE position of each compressed token */
+  const uint16_t* key_basis;      /* fp16, dkv_prepare_key_basis layout */
+  const uint16_t* value_basis;    /* fp16, dkv_prepare_value_basis layout */
+  const float* mean_k;            /* [L][Hkv*d] */
+  const float* mean_v;            /* [L][Hkv*d] */
+  const float* rope_cos;          /* [P][d/2] f32 (first half of HF emb) */
+  const float* rope_sin;          /* [P][d/2] */
+  int32_t rope_rows;              /* P */
+  const void* query;              /* [batch][Hq][q_len][d], query_dtype */
+  int32_t query_dtype;
+  const int32_t* cu_exact;        /* [batch+1] or NULL (no exact tokens) */
+  const int32_t* cu_exact_host;   /* host mirror of cu_exact (<= 1024 exact tokens per sequence) */
+  const float* key_exact;         /* [Hkv][E_total][d] f32, RoPE applied */
+  const float* value_exact;       /* [Hkv][E_total][d] f32 */
+  const float* mask;              /* [q_len][E] additive (batch == 1 only) or NULL */
+  void* out;                      /* [batch][q_len][Hq][d], out_dtype */
+  int32_t out_dtype;
+} dkv_attend_args_t;
+
+size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);
+int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- K4a: question scoring over the hot tier ----------------------------
+ * Replaces scripts/progressive.py:239-254 question_importance with
+ * scripts/dimmer.py:52-66 scoring: for every layer, the attention each
+ * compressed token receives from the q_len question tokens, summed over
+ * query positions, the GQA group and the KV heads; the softmax spans the
+ * compressed tokens, the exact tokens and the question's own keys (causal).
+ * Uses the attend arguments (batch must be 1; out/value fields unused);
+ * key_question is [Hkv][q_len][d] f32 (RoPE applied).  Adds this layer's
+ * contribution into importance [n] (f32) in a fixed order; call
+ * dkv_score_begin once before the first layer. */
+size_t dkv_score_workspace_bytes(const dkv_attend_args_t* a);
+int dkv_score_begin(float* importance, int32_t n, void* stream);
+int dkv_score_layer(const dkv_attend_args_t* a, const float* key_question, float* importance, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* ---- K4b: top-k (scripts/methods.py:246-247 importance[start:end].topk) --
+ * Indices of the k largest values of scores [n] (ties: lower index first),
+ * written in ascending index order to idx_out [k]. */
+size_t dkv_topk_workspace_bytes(int32_t n);
+int dkv_topk(const float* scores, int32_t n, int32_t k, int32_t* idx_out, void* workspace, size_t workspace_bytes,
+             void* stream);
+
+/* ---- K4c: cold-plane gather (scripts/progressive.py:224-236 refine) ------
+ * For the k selected tokens idx [k] (stream-local), merge each token's hot
+ * blob with its cold blob (cold + cold_tok_off[t]) into a full blob written
+ * at refined + r*full_bytes (r = 0..k-1), then point the stream at it:
+ * tok_off[t] = refined_base_off + r*full_bytes, pieces[t] = order.pieces.
+ * `tok_off`/`pieces` are the stream's (mutable) arrays; `refined` must lie
+ * inside the stream's blob allocation at byte offset refined_base_off. */
+int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const int64_t* cold_tok_off, const int32_t* idx,
+                    int32_t k, uint8_t* refined, int64_t refined_base_off, int64_t* tok_off, int16_t* pieces,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DIMMERKV_H */

@@ -1,0 +1,28 @@
+"""CPU oracle for the compressed-cache decode path (test infrastructure only).
+
+This package restates, in numpy, the reference algorithm of Dimmer-KV's
+answer-time path so that the HIP kernels can be checked against it:
+
+- ``rope_ref``      RoPE tables / rotate_half / rerotate   (scripts/kvtc.py:27-47,
+                    transformers/modeling_rope_utils.py:621-662)
+- ``progressive_ref`` quantize8 / dequantize / order and byte accounting
+                    (scripts/progressive.py:32-236)
+- ``kvtc_ref``      allocate_rungs / quantize_groups (scripts/kvtc.py:62-79, 277-298)
+- ``attention_ref`` CompressedContext.attend math and an independent fp64
+                    decode-then-attend (scripts/compressed_attention.py:105-137)
+- ``scoring_ref``   question_importance + top-k selection
+                    (scripts/progressive.py:239-254, scripts/dimmer.py:45-77,
+                    scripts/methods.py:244-248)
+- ``packing_ref``   the packed hot/cold bit-plane layout this build defines
+                    (its byte totals follow scripts/progressive.py:185-194, 232)
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this package, and only as the checker. The product
+path (the HIP library and its Python wrappers) never calls it.
+
+Parity pins: every function here is checked in ``tests/test_oracle_*.py``
+against closed forms, library routines (transformers' RoPE, torch.topk /
+stable sort), brute force on tiny inputs or invariants.  Functions whose
+bit-exact behaviour only the reference itself could fix are marked
+"parity unpinned" in their docstring.
+"""
