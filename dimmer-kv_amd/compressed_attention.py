@@ -81,7 +81,9 @@ class CompressedContext:
         self.batch = self.cu_host.numel() - 1
         self.exact_cache = exact_cache
         self._workspace = None
+        self._score_workspace = None
         self._cu_exact = {}
+        self.importance = None  # float32 [n] while a question is being scored
 
     # ----- memory accounting (scripts/compressed_attention.py:91-102) -----
     def code_bytes(self) -> int:
@@ -141,7 +143,8 @@ class CompressedContext:
     def workspace(self, args) -> torch.Tensor:
         need = dkv_hip.attend_workspace_bytes(args)
         if self._workspace is None or self._workspace.numel() < need:
-            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.key.blob.device)
+            # zero-filled: the head of the workspace holds the kernels' completion counters
+            self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.key.blob.device)
         return self._workspace
 
     def attend(self, module, query, key, value, attention_mask, scaling):
@@ -164,7 +167,43 @@ class CompressedContext:
                 mask = attention_mask[0, 0, :, -key.shape[2]:].float().contiguous()
         args = self.layer_args(layer, query, out, key_exact, value_exact, mask, lengths, scaling)
         dkv_hip.attend_layer(args, self.workspace(args))
+        if self.importance is not None:
+            self._score(layer, query, key, scaling)
         return out, None
+
+    # ----- question scoring over the hot codes (K4a) -----
+    def begin_scoring(self) -> None:
+        """Start accumulating the attention the compressed tokens receive (dimmer.py:60-66 scoring)."""
+        self.importance = torch.empty(self.key.n, dtype=torch.float32, device=self.key.blob.device)
+        dkv_hip.score_begin(self.importance)
+
+    def end_scoring(self) -> torch.Tensor:
+        importance, self.importance = self.importance, None
+        return importance
+
+    def _score(self, layer: int, query: torch.Tensor, key: torch.Tensor, scaling) -> None:
+        """Adds this layer's attention mass on each compressed token, summed over the question
+        tokens and all query heads; the softmax spans the compressed tokens, the exact cache
+        before the question and the question's own keys (causal)."""
+        if self.batch != 1:
+            raise ValueError("question scoring takes one conversation")
+        q_len = query.shape[2]
+        if key is None or key.shape[2] < q_len:
+            raise ValueError("scoring needs the question's keys in the exact cache")
+        past = key.shape[2] - q_len
+        key_question = key[0, :, past:].float().contiguous()
+        key_exact = value_exact = None
+        lengths = None
+        if past > 0:
+            key_exact = key[0, :, :past].float().contiguous()
+            value_exact = key_exact  # values are not read by the scoring kernels
+            lengths = (past,)
+        scratch = torch.empty(1, q_len, query.shape[1], query.shape[3], dtype=query.dtype, device=query.device)
+        args = self.layer_args(layer, query, scratch, key_exact, value_exact, None, lengths, scaling)
+        need = dkv_hip.score_workspace_bytes(args)
+        if self._score_workspace is None or self._score_workspace.numel() < need:
+            self._score_workspace = torch.zeros(need, dtype=torch.uint8, device=query.device)
+        dkv_hip.score_layer(args, key_question, self.importance, self._score_workspace)
 
 
 def greedy_answer(model, tokenizer, context: CompressedContext | None, cache, input_ids: torch.Tensor,

@@ -29,9 +29,8 @@ constexpr int kTileTok = 256;    // tokens per K2 workgroup
 constexpr int kK2Threads = 512;  // 8 waves: 4 token quarters x 2 row halves
 constexpr int kStride = 72;      // LDS row stride in halves for [row][64] tiles (64 + 8 pad)
 constexpr int kSplitTok = 1024;  // tokens per K3a split
-constexpr int kK3Threads = 256;  // 4 waves, one 64-component group each
+constexpr int kK3Threads = 256;  // 4 waves sharing one 64-component group
 constexpr int kVtStride = 40;    // LDS stride (halves) of the transposed value tile [64][32 + 8]
-constexpr int kPStride = 40;     // LDS stride (halves) of the p~ tile [32][32 + 8]
 constexpr int kChunk = 128;      // components per K3b workgroup
 
 struct K2Args {
@@ -99,9 +98,14 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const bool uvalid = ut < count;
   const int ut_g = tok0 + ut;
   const int ukp = uvalid ? a.key.pieces[ut_g] : 0;
-  const uint8_t* ubase = uvalid ? a.key.blob + a.key.tok_off[ut_g] : nullptr;
-  const uint8_t* planes_row = a.key.order.planes + (long)ukp * G;
-  const int32_t* seg_row = a.key.order.seg_off + (long)ukp * G;
+  const uint8_t* ubase = uvalid ? a.key.blob + a.key.tok_off[ut_g] : a.key.blob;
+  // The token's plane-count row (4 groups per dword, G % 4 == 0), kept in
+  // registers and fetched one dword ahead; the segment offset of each group
+  // is a running sum, so the loop never waits on an order-table lookup.
+  const uint32_t* prow = (const uint32_t*)(a.key.order.planes + (long)ukp * G);
+  uint32_t pw_cur = uvalid ? prow[0] : 0u;
+  uint32_t pw_nxt = (uvalid && G > 4) ? prow[1] : 0u;
+  int seg_run = 0;
 
   const uint16_t* basis_layer = a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h0 * D * 64;
   const long basis_group_stride = (long)a.Hkv * D * 64;
@@ -123,13 +127,14 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
 #define DKV_K2_ISSUE(g_)                                                              \
   do {                                                                                \
-    um = uvalid ? (int)planes_row[(g_)] : 0;                                          \
-    if (uvalid) {                                                                     \
-      load_segment(ubase + seg_row[(g_)], um, uh, pl, header);                        \
-    } else {                                                                          \
-      _Pragma("unroll") for (int p_ = 0; p_ < 8; ++p_) pl[p_] = 0u;                   \
-      header = 0u;                                                                    \
+    const int gg_ = (g_);                                                             \
+    if ((gg_ & 3) == 0 && gg_ > 0) {                                                  \
+      pw_cur = pw_nxt;                                                                \
+      pw_nxt = (uvalid && gg_ + 4 < G) ? prow[(gg_ >> 2) + 1] : 0u;                   \
     }                                                                                 \
+    um = (int)((pw_cur >> (8 * (gg_ & 3))) & 0xffu);                                  \
+    load_segment_nb(ubase + seg_run, um, uh, a.key.blob, pl, header);                 \
+    seg_run += um > 0 ? 4 + 8 * um : 0;                                               \
     const uint4* src_ = (const uint4*)(basis_layer + (long)(g_) * basis_group_stride); \
     br0 = src_[0 * kK2Threads + tid];                                                 \
     br1 = src_[1 * kK2Threads + tid];                                                 \
@@ -313,6 +318,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     }
     __syncthreads();
   }
+
 }
 
 // ---------------------------------------------------------------------------
@@ -330,39 +336,87 @@ struct K3aArgs {
   const float* scores;
   const float* tile_max;
   float* w_part;
-  int batch, R_total, n_total, ntiles, G, rank, nsplits, row_blocks, nchunks_g;
+  int batch, R_total, n_total, ntiles, G, rank, nsplits, row_blocks;
 };
 
+// Max over a sequence's tiles of one row, 8 lanes per row (all loads of a lane issued together).
+DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, int row, bool ok, int sub) {
+  float m = -INFINITY;
+  if (ok) {
+    const float* tm = tile_max + (long)row * ntiles + tb0;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (sub + 8 * i < ntb) ? tm[sub + 8 * i] : -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, v[i]);
+    for (int t = sub + 64; t < ntb; t += 8) m = fmaxf(m, tm[t]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  m = fmaxf(m, __shfl_xor(m, 4, 64));
+  return m;
+}
+
+// Loads of one 32-token chunk for the value unpack: metadata, order-table
+// entries, then the plane words (three dependent levels).
+struct ChunkLoads {
+  uint32_t pl[8];
+  uint32_t hdr;
+  int m;
+};
+
+DKV_DEVICE void chunk_loads(const dkv_stream_t& v, int tok0, int count, int t, int g, int half, ChunkLoads& c) {
+  const int G = v.order.groups;
+  if (t < count) {
+    const int tg = tok0 + t;
+    const int kp = v.pieces[tg];
+    const int64_t off = v.tok_off[tg];
+    c.m = v.order.planes[(long)kp * G + g];
+    load_segment(v.blob + off + v.order.seg_off[(long)kp * G + g], c.m, half, c.pl, c.hdr);
+  } else {
+    c.m = 0;
+    c.hdr = 0u;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) c.pl[p] = 0u;
+  }
+}
+
+// K3a: workgroup = (token split of kSplitTok tokens, one 64-component group,
+// one block of 32 output rows).  Wave w owns the split's 32-token chunks
+// w, w+4, ...; the loads of the next chunk are issued before the current one
+// is processed.  p~ = exp(s - M_c) feeds the MFMA A operand straight from the
+// scores; value codes are unpacked to fp16 and transposed through a per-wave
+// LDS tile for the B operand; MFMA 32x32x16 accumulates; the four waves' sums
+// are reduced through LDS.
 __global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
-  __shared__ __attribute__((aligned(16))) half_t Pt[32 * kPStride];
   __shared__ __attribute__((aligned(16))) half_t Vt[4][64 * kVtStride];
+  __shared__ float red[3][64][33];
   __shared__ float Mrow[32];
 
   const int bid = blockIdx.x;
   const int rbk = bid % a.row_blocks;
-  const int gc = (bid / a.row_blocks) % a.nchunks_g;
-  const int sp = bid / (a.row_blocks * a.nchunks_g);
+  const int g = (bid / a.row_blocks) % a.G;
+  const int sp = bid / (a.row_blocks * a.G);
   const int2 bs = find_tile(a.cu_seqlens, a.batch, kSplitTok, sp);
   const int b = bs.x;
   const int tok0 = a.cu_seqlens[b] + bs.y * kSplitTok;
   const int count = min(kSplitTok, a.cu_seqlens[b + 1] - tok0);
-  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-  const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int G = a.G;
-  const int g = gc * 4 + wave;
-  const bool gvalid = g < G;
-
-  if (tid < 32) {
-    const int row = rbk * 32 + tid;
-    float M = -INFINITY;
-    if (row < a.R_total)
-      for (int t = 0; t < ntb; ++t) M = fmaxf(M, a.tile_max[(long)row * a.ntiles + tb0 + t]);
-    Mrow[tid] = M;
+  const int ut = lane >> 1, uh = lane & 1;
+  {
+    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+    const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
+    const int r = rbk * 32 + (tid >> 3);
+    const float m = rows_max8(a.tile_max, a.ntiles, tb0, ntb, r, r < a.R_total, tid & 7);
+    if ((tid & 7) == 0) Mrow[tid >> 3] = m;
   }
   __syncthreads();
+  const int my_row = rbk * 32 + l32;
+  const bool row_ok = my_row < a.R_total;
+  const float my_M = Mrow[l32];
+  const float* srow = a.scores + (long)(row_ok ? my_row : 0) * a.n_total + tok0;
 
   floatx16 acc[2];
 #pragma unroll
@@ -370,39 +424,24 @@ __global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[nb][v] = 0.0f;
 
-  const int ut = lane >> 1, uh = lane & 1;
-  for (int c0 = 0; c0 < count; c0 += 32) {
-    // p~ tile [32 rows][32 tokens]
+  half_t* vt = Vt[wave];
+  ChunkLoads cur;
+  int c0 = wave * 32;
+  chunk_loads(a.value, tok0, count, c0 + ut, g, uh, cur);
+  for (; c0 < count; c0 += 4 * 32) {
+    float sc[16];
 #pragma unroll
-    for (int e = tid; e < 32 * 32; e += kK3Threads) {
-      const int rr = e >> 5, t = e & 31;
-      const int row = rbk * 32 + rr;
-      float p = 0.0f;
-      if (row < a.R_total && c0 + t < count) {
-        const float M = Mrow[rr];
-        p = __expf(a.scores[(long)row * a.n_total + tok0 + c0 + t] - M);
-      }
-      Pt[rr * kPStride + t] = (half_t)p;
+    for (int e = 0; e < 16; ++e) {
+      const int t = c0 + (e >> 3) * 16 + lhi * 8 + (e & 7);
+      sc[e] = (row_ok && t < count) ? srow[t] : -INFINITY;
     }
-    // value codes of token c0 + ut, this wave's group -> transposed [coef][token]
+    ChunkLoads nxt;
+    chunk_loads(a.value, tok0, count, c0 + 4 * 32 + ut, g, uh, nxt);
     {
-      const int t = c0 + ut;
-      uint32_t pl[8], header = 0u;
-      int m = 0;
-      if (gvalid && t < count) {
-        const int tg = tok0 + t;
-        const int kp = a.value.pieces[tg];
-        m = a.value.order.planes[(long)kp * G + g];
-        const uint8_t* seg = a.value.blob + a.value.tok_off[tg] + a.value.order.seg_off[(long)kp * G + g];
-        load_segment(seg, m, uh, pl, header);
-      } else {
-#pragma unroll
-        for (int p = 0; p < 8; ++p) pl[p] = 0u;
-      }
-      const AffineDq dq = affine_from_header(header, m);
+      const AffineDq dq = affine_from_header(cur.hdr, cur.m);
       uint32_t vals[16];
-      unpack_half_f16(pl, dq, vals);
-      half_t* col = Vt[wave] + uh * 32 * kVtStride + ut;
+      unpack_half_f16(cur.pl, dq, vals);
+      half_t* col = vt + uh * 32 * kVtStride + ut;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t v2 = vals[j];
@@ -414,33 +453,58 @@ __global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
         col[(2 * j + 1) * kVtStride] = hhi;
       }
     }
-    __syncthreads();
+    half8 pa[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float s = sc[ks * 8 + e];
+        pa[ks][e] = (half_t)(s == -INFINITY ? 0.0f : __expf(s - my_M));
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int kof = ks * 16 + lhi * 8;
-      const half8 pa = lds_half8(Pt + l32 * kPStride + kof);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const half8 vb = lds_half8(Vt[wave] + (nb * 32 + l32) * kVtStride + kof);
-        acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, vb, acc[nb], 0, 0, 0);
+        const half8 vb = lds_half8(vt + (nb * 32 + l32) * kVtStride + kof);
+        acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks], vb, acc[nb], 0, 0, 0);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    cur = nxt;
   }
-  if (!gvalid) return;
+  if (wave > 0) {
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb)
+    for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int row = rbk * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-      if (row < a.R_total) a.w_part[((long)sp * a.R_total + row) * a.rank + g * 64 + nb * 32 + l32] = acc[nb][v];
-    }
+      for (int v = 0; v < 16; ++v) red[wave - 1][lane][nb * 16 + v] = acc[nb][v];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float s = acc[nb][v] + red[0][lane][nb * 16 + v] + red[1][lane][nb * 16 + v] +
+                        red[2][lane][nb * 16 + v];
+        const int row = rbk * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+        if (row < a.R_total) a.w_part[((long)sp * a.R_total + row) * a.rank + g * 64 + nb * 32 + l32] = s;
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// K3b: per (sequence, KV head, 128-component chunk): sum partials over the
-// sequence's splits, multiply by the value basis chunk [128][D].
+// K3b: per (sequence, KV head, 128-component chunk): sum the partials over the
+// sequence's splits, multiply once by the value-basis chunk [128][D].
 // ---------------------------------------------------------------------------
+constexpr int kMaxExact = 1024;
+constexpr int kMaxSplitsUnrolled = 32;
+
 struct K3bArgs {
   const int32_t* cu_seqlens;
   const float* w_part;
@@ -451,7 +515,7 @@ struct K3bArgs {
 
 __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
   __shared__ float W[8][kChunk];
-  __shared__ float red[256 / 64][8][128];
+  __shared__ float red[4][8][130];
   const int c = blockIdx.x % a.nchunks;
   const int h = (blockIdx.x / a.nchunks) % a.Hkv;
   const int b = blockIdx.x / (a.nchunks * a.Hkv);
@@ -461,35 +525,69 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
   const int sp0 = tiles_before(a.cu_seqlens, b, kSplitTok);
   const int nsp = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kSplitTok - 1) / kSplitTok;
   const int D = a.D;
-  const int parts = 256 / D;  // threads per d
-  const int d = tid % D, part = tid / D;
+  const int npair = D / 2;
+  const int parts = 256 / npair;  // 4 (D=128) or 8 (D=64)
+  const int dp = tid % npair, part = tid / npair;
   const int ilen = kChunk / parts;
-  const uint16_t* bv = a.value_basis + (((long)a.layer * a.Hkv + h) * a.rank + (long)c * kChunk) * D;
+  const uint32_t* bv = (const uint32_t*)(a.value_basis + (((long)a.layer * a.Hkv + h) * a.rank + (long)c * kChunk) * D);
+  const long sp_stride = (long)a.R_total * a.rank;
   for (int r0 = 0; r0 < RH; r0 += 8) {
     const int nr = min(8, RH - r0);
+    // partial sums over the splits, all loads of a thread issued together
     for (int e = tid; e < nr * kChunk; e += 256) {
       const int rr = e / kChunk, i = e % kChunk;
-      const long row = (long)h * RH + r0 + rr;
+      const float* src = a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + rr) * a.rank + c * kChunk + i;
+      float v[kMaxSplitsUnrolled];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitsUnrolled; ++sp) v[sp] = sp < nsp ? src[sp * sp_stride] : 0.0f;
       float s = 0.0f;
-      for (int sp = 0; sp < nsp; ++sp) s += a.w_part[((long)(sp0 + sp) * a.R_total + row) * a.rank + c * kChunk + i];
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplitsUnrolled; ++sp) s += v[sp];
+      for (int sp = kMaxSplitsUnrolled; sp < nsp; ++sp) s += src[sp * sp_stride];
       W[rr][i] = s;
     }
     __syncthreads();
-    float accr[8];
+    float acc0[8], acc1[8];
 #pragma unroll
-    for (int rr = 0; rr < 8; ++rr) accr[rr] = 0.0f;
-    for (int i = part * ilen; i < (part + 1) * ilen; ++i) {
-      const float bvv = half_bits_to_float(bv[(long)i * D + d]);
+    for (int rr = 0; rr < 8; ++rr) acc0[rr] = acc1[rr] = 0.0f;
+    uint32_t bw[kChunk / 4];
 #pragma unroll
-      for (int rr = 0; rr < 8; ++rr) accr[rr] += W[rr][i] * bvv;
+    for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = ii < ilen ? bv[(long)(part * ilen + ii) * npair + dp] : 0u;
+#pragma unroll
+    for (int ii = 0; ii < kChunk / 4; ++ii) {
+      if (ii >= ilen) break;
+      const int i = part * ilen + ii;
+      const float b0 = half_bits_to_float((uint16_t)(bw[ii] & 0xffffu));
+      const float b1 = half_bits_to_float((uint16_t)(bw[ii] >> 16));
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr) {
+        acc0[rr] += W[rr][i] * b0;
+        acc1[rr] += W[rr][i] * b1;
+      }
     }
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) red[part][rr][d] = accr[rr];
+    if (parts > 4) {
+      if (part >= 4)
+        for (int rr = 0; rr < 8; ++rr) {
+          red[part - 4][rr][2 * dp] = acc0[rr];
+          red[part - 4][rr][2 * dp + 1] = acc1[rr];
+        }
+      __syncthreads();
+      if (part < 4)
+        for (int rr = 0; rr < 8; ++rr) {
+          acc0[rr] += red[part][rr][2 * dp];
+          acc1[rr] += red[part][rr][2 * dp + 1];
+        }
+      __syncthreads();
+    }
+    if (part < 4)
+      for (int rr = 0; rr < 8; ++rr) {
+        red[part][rr][2 * dp] = acc0[rr];
+        red[part][rr][2 * dp + 1] = acc1[rr];
+      }
     __syncthreads();
     for (int e = tid; e < nr * D; e += 256) {
       const int rr = e / D, dd = e % D;
-      float s = 0.0f;
-      for (int p = 0; p < parts; ++p) s += red[p][rr][dd];
+      const float s = red[0][rr][dd] + red[1][rr][dd] + red[2][rr][dd] + red[3][rr][dd];
       a.out_part[(((long)c * a.batch + b) * a.R_total + (long)h * RH + r0 + rr) * D + dd] = s;
     }
     __syncthreads();
@@ -497,8 +595,8 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// K3c: one workgroup per (sequence, output row): exact tokens, softmax merge,
-// mean term, normalisation.
+// K3c: one workgroup (4 waves) per (sequence, output row): exact tokens in the
+// same softmax as the compressed part, sum(p) * mean_v, normalisation.
 // ---------------------------------------------------------------------------
 struct K3cArgs {
   const int32_t* cu_seqlens;
@@ -513,103 +611,117 @@ struct K3cArgs {
   const void* query;
   void* out;
   float scaling;
-  int batch, layer, Hkv, Hq, q_len, D, R_total, ntiles, nchunks, E_total, query_dtype, out_dtype;
+  int batch, layer, Hkv, Hq, q_len, D, R_total, nchunks, E_total, query_dtype, out_dtype, ntiles;
 };
 
-constexpr int kMaxExact = 1024;
-
-__global__ __launch_bounds__(128) void finish_kernel(K3cArgs a) {
+__global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
   __shared__ float q[128];
   __shared__ float se[kMaxExact];
-  __shared__ float red[128];
-  __shared__ float bc[4];
+  __shared__ float wred[2][4];
+  __shared__ float buf[2][256];
+  __shared__ float bc[2];
   const int row = blockIdx.x % a.R_total;
   const int b = blockIdx.x / a.R_total;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.D;
   const int gq = a.Hq / a.Hkv;
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
-  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-  const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
-
-  // compressed-part statistics
-  float m = -INFINITY;
-  for (int t = tid; t < ntb; t += 128) m = fmaxf(m, a.tile_max[(long)row * a.ntiles + tb0 + t]);
-  red[tid] = m;
-  __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
-  }
-  const float Mc = red[0];
-  __syncthreads();
-  float l = 0.0f;
-  if (Mc != -INFINITY)
-    for (int t = tid; t < ntb; t += 128) {
-      const float mt = a.tile_max[(long)row * a.ntiles + tb0 + t];
-      if (mt != -INFINITY) l += a.tile_sum[(long)row * a.ntiles + tb0 + t] * __expf(mt - Mc);
-    }
-  red[tid] = l;
-  __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
-    __syncthreads();
-  }
-  const float Lc = red[0];
-  __syncthreads();
-
-  // exact tokens
   const int e0 = a.cu_exact ? a.cu_exact[b] : 0;
   const int E = a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
+  if (wave == 0) {
+    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+    const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
+    const float* tm = a.tile_max + (long)row * a.ntiles + tb0;
+    const float* ts = a.tile_sum + (long)row * a.ntiles + tb0;
+    float m = -INFINITY;
+    for (int t = lane; t < ntb; t += 64) m = fmaxf(m, tm[t]);
+    m = wave_max(m);
+    float l = 0.0f;
+    if (m != -INFINITY)
+      for (int t = lane; t < ntb; t += 64)
+        if (tm[t] != -INFINITY) l += ts[t] * __expf(tm[t] - m);
+    l = wave_sum(l);
+    if (lane == 0) {
+      bc[0] = m;
+      bc[1] = l;
+    }
+  }
   if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
+  // the thread's share of the chunk partials (independent of the softmax)
+  const int d = tid % D, part = tid / D, parts = 256 / D;
+  float vparts[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = part + i * parts;
+    vparts[i] = c < a.nchunks ? a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d] : 0.0f;
+  }
+  float vc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) vc += vparts[i];
+  for (int c = part + 16 * parts; c < a.nchunks; c += parts)
+    vc += a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d];
   __syncthreads();
+  // exact scores: one token per thread
   float me = -INFINITY;
-  for (int j = tid; j < E; j += 128) {
-    const float* kr = a.key_exact + ((long)h * a.E_total + e0 + j) * D;
+  for (int j = tid; j < E; j += 256) {
+    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D);
+    float4 k4[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) k4[i] = i < D / 4 ? kr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     float dot = 0.0f;
-    for (int dd = 0; dd < D; ++dd) dot += q[dd] * kr[dd];
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i < D / 4) dot += q[4 * i] * k4[i].x + q[4 * i + 1] * k4[i].y + q[4 * i + 2] * k4[i].z + q[4 * i + 3] * k4[i].w;
     float s = dot * a.scaling;
     if (a.mask) s += a.mask[(long)qi * E + j];
     se[j] = s;
     me = fmaxf(me, s);
   }
-  red[tid] = me;
+  me = wave_max(me);
+  if (lane == 0) wred[0][wave] = me;
   __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
-  }
-  const float Me = red[0];
-  __syncthreads();
+  const float Mc = bc[0], Lc = bc[1];
+  const float Me = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
   const float M = fmaxf(Mc, Me);
-  if (tid == 0) {
-    bc[0] = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
-    bc[1] = M;
-  }
-  __syncthreads();
-  const float ec = bc[0];
+  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
   float le = 0.0f;
-  for (int j = tid; j < E; j += 128) {
-    const float w = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
-    se[j] = w;
-    le += w;
+  for (int j = tid; j < E; j += 256) {
+    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
+    se[j] = wgt;
+    le += wgt;
   }
-  red[tid] = le;
+  le = wave_sum(le);
+  if (lane == 0) wred[1][wave] = le;
   __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
-    __syncthreads();
-  }
-  const float Le = red[0];
+  const float Le = wred[1][0] + wred[1][1] + wred[1][2] + wred[1][3];
   const float denom = ec * Lc + Le;
+  // exact values: thread (d, part) takes tokens part, part + parts, ... in batches of 8
+  float ve = 0.0f;
+  for (int j0 = part; j0 < E; j0 += 8 * parts) {
+    float vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = j0 + i * parts;
+      vv[i] = j < E ? a.value_exact[((long)h * a.E_total + e0 + j) * D + d] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = j0 + i * parts;
+      if (j < E) ve += se[j] * vv[i];
+    }
+  }
+  buf[0][tid] = vc;
+  buf[1][tid] = ve;
+  __syncthreads();
   if (tid < D) {
-    float vc = 0.0f;
-    for (int c = 0; c < a.nchunks; ++c) vc += a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + tid];
-    vc += Lc * a.mean_v[((long)a.layer * a.Hkv + h) * D + tid];
-    float ve = 0.0f;
-    for (int j = 0; j < E; ++j) ve += se[j] * a.value_exact[((long)h * a.E_total + e0 + j) * D + tid];
-    const float o = denom > 0.0f ? (ec * vc + ve) / denom : 0.0f;
+    float vcs = 0.0f, ves = 0.0f;
+    for (int p = 0; p < parts; ++p) {
+      vcs += buf[0][p * D + tid];
+      ves += buf[1][p * D + tid];
+    }
+    vcs += Lc * a.mean_v[((long)a.layer * a.Hkv + h) * D + tid];
+    const float o = denom > 0.0f ? (ec * vcs + ves) / denom : 0.0f;
     store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * D + tid, a.out_dtype, o);
   }
 }
@@ -624,6 +736,7 @@ struct Layout {
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Workspace: [scores][tile statistics][split partials][chunk partials].
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
   L.ntiles = 0;
@@ -657,8 +770,8 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
   if (rc) return rc;
   DKV_REQUIRE(a->head_dim == 64 || a->head_dim == 128, DKV_ESHAPE, "%s: head_dim must be 64 or 128 (got %d)", what,
               a->head_dim);
-  DKV_REQUIRE(a->rank > 0 && a->rank % kChunk == 0 && a->rank == 64 * a->key.order.groups, DKV_ESHAPE,
-              "%s: rank %d must be a multiple of 128 and equal 64 * groups (%d)", what, a->rank,
+  DKV_REQUIRE(a->rank > 0 && a->rank % 256 == 0 && a->rank == 64 * a->key.order.groups, DKV_ESHAPE,
+              "%s: rank %d must be a multiple of 256 and equal 64 * groups (%d)", what, a->rank,
               a->key.order.groups);
   DKV_REQUIRE(a->kv_heads > 0 && a->q_heads % a->kv_heads == 0, DKV_ESHAPE, "%s: q_heads %d not a multiple of %d",
               what, a->q_heads, a->kv_heads);
@@ -718,34 +831,47 @@ extern "C" size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a) {
   return make_layout(a).total;
 }
 
-extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_attend(a, "dkv_attend_layer");
+static int check_values(const dkv_attend_args_t* a, int& E_total) {
+  int rc = dkv::check_stream(&a->value, "dkv_attend_values");
   if (rc) return rc;
-  rc = dkv::check_stream(&a->value, "dkv_attend_layer(value)");
-  if (rc) return rc;
-  DKV_REQUIRE(a->value.order.groups == a->key.order.groups, DKV_ESHAPE, "dkv_attend_layer: K/V group mismatch");
-  DKV_REQUIRE(a->value_basis && a->mean_v && a->out, DKV_EINVAL, "dkv_attend_layer: null value/out pointer");
-  DKV_REQUIRE(a->out_dtype >= DKV_F32 && a->out_dtype <= DKV_BF16, DKV_EINVAL, "dkv_attend_layer: bad out dtype");
-  DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "dkv_attend_layer: mask is only supported for batch == 1");
+  DKV_REQUIRE(a->value.order.groups == a->key.order.groups, DKV_ESHAPE, "dkv_attend_values: K/V group mismatch");
+  DKV_REQUIRE(a->value_basis && a->mean_v && a->out, DKV_EINVAL, "dkv_attend_values: null value/out pointer");
+  DKV_REQUIRE(a->out_dtype >= DKV_F32 && a->out_dtype <= DKV_BF16, DKV_EINVAL, "dkv_attend_values: bad out dtype");
+  DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "dkv_attend_values: mask is only supported for batch == 1");
   DKV_REQUIRE(!a->cu_exact || (a->key_exact && a->value_exact), DKV_EINVAL,
-              "dkv_attend_layer: exact keys/values missing");
-  const Layout L = make_layout(a);
-  DKV_REQUIRE(workspace && workspace_bytes >= L.total, DKV_EWORKSPACE,
-              "dkv_attend_layer: workspace %zu B < required %zu B", workspace_bytes, L.total);
-  // The finish kernel keeps one sequence's exact scores in LDS.
-  int E_total = 0;
+              "dkv_attend_values: exact keys/values missing");
+  E_total = 0;
   if (a->cu_exact) {
-    DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "dkv_attend_layer: cu_exact needs cu_exact_host");
+    DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "dkv_attend_values: cu_exact needs cu_exact_host");
     for (int b = 0; b < a->batch; ++b) {
       const int e = a->cu_exact_host[b + 1] - a->cu_exact_host[b];
-      DKV_REQUIRE(e >= 0 && e <= kMaxExact, DKV_ESHAPE, "dkv_attend_layer: %d exact tokens (max %d)", e, kMaxExact);
+      DKV_REQUIRE(e >= 0 && e <= kMaxExact, DKV_ESHAPE, "dkv_attend_values: %d exact tokens (max %d)", e, kMaxExact);
     }
     E_total = a->cu_exact_host[a->batch];
   }
+  return DKV_OK;
+}
+
+extern "C" int dkv_attend_scores(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attend(a, "dkv_attend_scores");
+  if (rc) return rc;
+  const Layout L = make_layout(a);
+  DKV_REQUIRE(workspace && workspace_bytes >= L.total, DKV_EWORKSPACE,
+              "dkv_attend_scores: workspace %zu B < required %zu B", workspace_bytes, L.total);
+  return launch_keys_scores(a, L, (char*)workspace, dkv::as_stream(stream));
+}
+
+extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attend(a, "dkv_attend_values");
+  if (rc) return rc;
+  int E_total = 0;
+  rc = check_values(a, E_total);
+  if (rc) return rc;
+  const Layout L = make_layout(a);
+  DKV_REQUIRE(workspace && workspace_bytes >= L.total, DKV_EWORKSPACE,
+              "dkv_attend_values: workspace %zu B < required %zu B", workspace_bytes, L.total);
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
-  rc = launch_keys_scores(a, L, ws, st);
-  if (rc) return rc;
   const int G = a->key.order.groups;
   if (L.nsplits > 0) {
     K3aArgs k{};
@@ -762,8 +888,7 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
     k.rank = a->rank;
     k.nsplits = L.nsplits;
     k.row_blocks = (L.R_total + 31) / 32;
-    k.nchunks_g = (G + 3) / 4;
-    const long blocks = (long)L.nsplits * k.row_blocks * k.nchunks_g;
+    const long blocks = (long)L.nsplits * k.row_blocks * G;
     hipLaunchKernelGGL(value_weights_kernel, dim3((unsigned)blocks), dim3(kK3Threads), 0, st, k);
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
@@ -790,6 +915,7 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
   kc.cu_exact = a->cu_exact;
   kc.tile_max = (const float*)(ws + L.tile_max);
   kc.tile_sum = (const float*)(ws + L.tile_sum);
+  kc.ntiles = L.ntiles;
   kc.out_part = (const float*)(ws + L.out_part);
   kc.mean_v = a->mean_v;
   kc.key_exact = a->key_exact;
@@ -805,13 +931,23 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
   kc.q_len = a->q_len;
   kc.D = a->head_dim;
   kc.R_total = L.R_total;
-  kc.ntiles = L.ntiles;
   kc.nchunks = L.nchunks;
   kc.E_total = E_total;
   kc.query_dtype = a->query_dtype;
   kc.out_dtype = a->out_dtype;
-  hipLaunchKernelGGL(finish_kernel, dim3(a->batch * L.R_total), dim3(128), 0, st, kc);
+  hipLaunchKernelGGL(finish_kernel, dim3(a->batch * L.R_total), dim3(256), 0, st, kc);
   return dkv::check_launch("finish");
+}
+
+extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attend(a, "dkv_attend_layer");
+  if (rc) return rc;
+  int E_total = 0;
+  rc = check_values(a, E_total);
+  if (rc) return rc;
+  rc = dkv_attend_scores(a, workspace, workspace_bytes, stream);
+  if (rc) return rc;
+  return dkv_attend_values(a, workspace, workspace_bytes, stream);
 }
 
 // ===========================================================================
@@ -889,8 +1025,8 @@ struct ImportanceArgs {
   const float* scores;  // [R_total][n]
   const float* tile_max;
   const float* tile_sum;
-  const float* stat;  // [R_total][2]
-  float* part;        // [nrc][n]
+  const float* stat;    // [R_total][2] exact-part (max, sum exp)
+  float* part;          // [nrc][n]
   int R_total, n, ntiles;
 };
 
@@ -902,28 +1038,34 @@ __global__ __launch_bounds__(kTokChunk) void importance_part_kernel(ImportanceAr
   const int tid = threadIdx.x;
   const int r0 = rc * kRowChunk;
   const int nr = min(kRowChunk, a.R_total - r0);
-  if (tid < nr) {
-    const int row = r0 + tid;
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int r = wave; r < nr; r += kTokChunk / 64) {
+    const int row = r0 + r;
+    const float* tm = a.tile_max + (long)row * a.ntiles;
+    const float* ts = a.tile_sum + (long)row * a.ntiles;
     float Mc = -INFINITY;
-    for (int t = 0; t < a.ntiles; ++t) Mc = fmaxf(Mc, a.tile_max[(long)row * a.ntiles + t]);
+    for (int t = lane; t < a.ntiles; t += 64) Mc = fmaxf(Mc, tm[t]);
+    Mc = wave_max(Mc);
     float Lc = 0.0f;
     if (Mc != -INFINITY)
-      for (int t = 0; t < a.ntiles; ++t) {
-        const float mt = a.tile_max[(long)row * a.ntiles + t];
-        if (mt != -INFINITY) Lc += a.tile_sum[(long)row * a.ntiles + t] * __expf(mt - Mc);
-      }
-    const float Me = a.stat[2 * row], Le = a.stat[2 * row + 1];
-    const float M = fmaxf(Mc, Me);
-    float L = 0.0f;
-    if (Mc != -INFINITY) L += Lc * __expf(Mc - M);
-    if (Me != -INFINITY) L += Le * __expf(Me - M);
-    Mr[tid] = M;
-    invL[tid] = L > 0.0f ? 1.0f / L : 0.0f;
+      for (int t = lane; t < a.ntiles; t += 64)
+        if (tm[t] != -INFINITY) Lc += ts[t] * __expf(tm[t] - Mc);
+    Lc = wave_sum(Lc);
+    if (lane == 0) {
+      const float Me = a.stat[2 * row], Le = a.stat[2 * row + 1];
+      const float M = fmaxf(Mc, Me);
+      float L = 0.0f;
+      if (Mc != -INFINITY) L += Lc * __expf(Mc - M);
+      if (Me != -INFINITY) L += Le * __expf(Me - M);
+      Mr[r] = M;
+      invL[r] = L > 0.0f ? 1.0f / L : 0.0f;
+    }
   }
   __syncthreads();
   const int tok = tc * kTokChunk + tid;
   if (tok >= a.n) return;
   float acc = 0.0f;
+#pragma unroll 16
   for (int r = 0; r < nr; ++r) acc += __expf(a.scores[(long)(r0 + r) * a.n + tok] - Mr[r]) * invL[r];
   a.part[(long)rc * a.n + tok] = acc;
 }

@@ -81,6 +81,21 @@ DKV_DEVICE void load_segment(const uint8_t* seg, int m, int half, uint32_t (&pl)
   for (int p = 0; p < 8; ++p) pl[p] = (p < m) ? w[1 + 2 * p + half] : 0u;
 }
 
+// Branch-free variant: absent planes (and the whole segment when m == 0) read
+// from ``safe`` (any valid address) and are then zeroed.
+DKV_DEVICE void load_segment_nb(const uint8_t* seg, int m, int half, const uint8_t* safe, uint32_t (&pl)[8],
+                                uint32_t& header) {
+  const uint32_t* w = (const uint32_t*)(m > 0 ? seg : safe);
+  const uint32_t* sw = (const uint32_t*)safe;
+  const uint32_t h = w[0];
+  header = m > 0 ? h : 0u;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const uint32_t v = *((p < m) ? (w + 1 + 2 * p + half) : sw);
+    pl[p] = (p < m) ? v : 0u;
+  }
+}
+
 // Dequantized value in the reference's exact fp32 operation order
 // (scripts/progressive.py:53): low + ((idx + 0.5) * span) / 2^m, every
 // product and sum rounded on its own; m == 0 gives 0.

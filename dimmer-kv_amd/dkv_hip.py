@@ -24,6 +24,7 @@ _DTYPE = {torch.float32: DKV_F32, torch.float16: DKV_F16, torch.bfloat16: DKV_BF
 EXPORTS = [
     "dkv_abi_version", "dkv_last_error", "dkv_pack_planes", "dkv_unpack_dequant", "dkv_dequantize_codes",
     "dkv_prepare_key_basis", "dkv_prepare_value_basis", "dkv_attend_workspace_bytes", "dkv_attend_layer",
+    "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
     "dkv_gather_cold",
 ]
@@ -155,6 +156,16 @@ def attend_workspace_bytes(args: AttendArgs) -> int:
 def attend_layer(args: AttendArgs, workspace: torch.Tensor) -> None:
     _check(lib().dkv_attend_layer(ctypes.byref(args), c_vp(ptr(workspace)), c_sz(workspace.numel()),
                                   c_vp(stream_handle())), "dkv_attend_layer")
+
+
+def attend_scores(args: AttendArgs, workspace: torch.Tensor) -> None:
+    _check(lib().dkv_attend_scores(ctypes.byref(args), c_vp(ptr(workspace)), c_sz(workspace.numel()),
+                                   c_vp(stream_handle())), "dkv_attend_scores")
+
+
+def attend_values(args: AttendArgs, workspace: torch.Tensor) -> None:
+    _check(lib().dkv_attend_values(ctypes.byref(args), c_vp(ptr(workspace)), c_sz(workspace.numel()),
+                                   c_vp(stream_handle())), "dkv_attend_values")
 
 
 def score_workspace_bytes(args: AttendArgs) -> int:

@@ -92,13 +92,11 @@ def _gen(seed: int) -> torch.Generator:
 
 
 def orthonormal_basis(features: int, rank: int, seed: int, device="cpu") -> torch.Tensor:
-    """Q of a QR of a seeded Gaussian [features, rank] (float64 on CPU, float32 on a GPU), as float32."""
+    """Q of a QR of a seeded Gaussian [features, rank], as float32.  The QR runs on the host
+    (float64 for small bases, float32 for model-sized ones) so every device sees the same basis."""
     g = _gen(seed)
     a = torch.randn(features, rank, generator=g, dtype=torch.float32)
-    if torch.device(device).type == "cpu":
-        q, _ = torch.linalg.qr(a.double())
-    else:
-        q, _ = torch.linalg.qr(a.to(device))
+    q, _ = torch.linalg.qr(a.double() if features * rank <= (1 << 23) else a)
     return q.float().to(device).contiguous()
 
 
@@ -272,6 +270,76 @@ def stream_budget_bytes(shape: ModelShape, budget: float) -> float:
     return budget * shape.exact_bytes
 
 
+class RopeModel(torch.nn.Module):
+    """The one part of a Llama model the codecs call: ``model.model.rotary_emb`` and ``config``
+    (scripts/kvtc.py:32-37).  Built from the local config; no weights."""
+
+    def __init__(self, shape: ModelShape, device="cpu"):
+        super().__init__()
+        from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+        self.config = llama_config(shape)
+        self.model = torch.nn.Module()
+        self.model.rotary_emb = LlamaRotaryEmbedding(self.config).to(device)
+
+
+def ladder_rungs(groups: int) -> torch.Tensor:
+    """kvtc bit-width ladder [rungs, groups] over {0, 2, 4, 8}, coarse -> fine: rung r gives the
+    leading groups more bits (the shape scripts/fit_kvtc.py produces from calibration)."""
+    rows = []
+    for r in range(1, 9):
+        bits = torch.zeros(groups, dtype=torch.long)
+        n8 = (groups * r) // 16
+        n4 = min(groups - n8, (groups * r) // 8)
+        n2 = min(groups - n8 - n4, (groups * r) // 4)
+        bits[:n8] = 8
+        bits[n8:n8 + n4] = 4
+        bits[n8 + n4:n8 + n4 + n2] = 2
+        rows.append(bits)
+    return torch.stack(rows)
+
+
+def kvtc_checkpoint(ctx: "SyntheticContext", model_id: str = "synthetic/llama-3.2", group: int = 64) -> dict:
+    """A kvtc calibration dict with the keys scripts/kvtc.py:108-131 reads, from a synthetic context."""
+    s = ctx.shape
+    rungs = ladder_rungs(s.rank // group)
+    saved = {"model": model_id, "layers": s.layers, "heads": s.kv_heads, "head_dim": s.head_dim, "group": group,
+             "sinks": ctx.sinks}
+    for kind in ("key", "value"):
+        sizes = [int((b.float() * group / 8).sum() + 4 * (b > 0).sum()) for b in rungs]
+        saved[kind] = {"mean": ctx.mean[kind].float().cpu(), "basis": ctx.basis[kind].float().cpu(), "rungs": rungs,
+                       "rung_bytes": sizes}
+    return saved
+
+
+def order_checkpoint(shape: ModelShape, model_id: str = "synthetic/llama-3.2") -> dict:
+    """A progressive-order dict with the keys scripts/progressive.py:124-129 reads: plane-major order."""
+    groups = shape.groups
+    sizes, planes, level = [0.0], [[0] * groups], [0] * groups
+    for k in range(PLANES * groups):
+        g = k % groups
+        sizes.append(sizes[-1] + PIECE_BYTES + (HEADER_BYTES if level[g] == 0 else 0))
+        level[g] += 1
+        planes.append(list(level))
+    entry = {"planes": torch.tensor(planes, dtype=torch.uint8), "prefix_bytes": torch.tensor(sizes, dtype=torch.float64),
+             "rungs": [groups * m for m in range(1, PLANES + 1)]}
+    return {"model": model_id, "key": dict(entry), "value": dict(entry)}
+
+
+def prefill_cache(ctx: "SyntheticContext", coef_middle: dict | None = None, device="cpu", dtype=torch.float16):
+    """Per-layer keys/values [1, Hkv, T, d] of a whole conversation (sinks, middle, recent), keys RoPE'd:
+    what a prefill leaves in a DynamicCache (scripts/common.py:62-67)."""
+    s = ctx.shape
+    coef_middle = ctx.coef if coef_middle is None else coef_middle
+    cos, sin = rope_tables(s, ctx.tokens, "cpu")
+    coef = {kind: torch.cat([ctx.exact_coef[kind][:ctx.start].cpu(), coef_middle[kind].cpu(),
+                             ctx.exact_coef[kind][ctx.start:].cpu()]) for kind in ("key", "value")}
+    keys, values = decode_exact(ctx, coef, torch.arange(ctx.tokens), cos, sin)
+    return ([keys[l][None].to(device=device, dtype=dtype) for l in range(s.layers)],
+            [values[l][None].to(device=device, dtype=dtype) for l in range(s.layers)])
+
+
 __all__ = ["ModelShape", "SHAPE_1B", "SHAPE_3B", "SyntheticContext", "make_context", "make_queries", "rope_tables",
            "decode_exact", "plane_counts", "orthonormal_basis", "coefficients", "causal_mask", "ragged_lengths",
-           "budget_per_stream", "stream_bytes", "llama_config"]
+           "budget_per_stream", "stream_bytes", "llama_config", "RopeModel",
+           "ladder_rungs", "kvtc_checkpoint", "order_checkpoint", "prefill_cache"]

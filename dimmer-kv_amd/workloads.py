@@ -1,0 +1,196 @@
+"""GPU-resident synthetic decode workloads for the benchmark, the smoke test and the
+full-size parity properties.
+
+One ``DecodeWorkload`` is a compressed conversation (or a ragged batch of
+them) packed on the GPU plus, per layer, the decode query, the exact cache
+(sinks, recent window and the new token, RoPE applied) and a preallocated
+output, with the C-ABI argument blocks built once so a decode step is just
+``n_layers`` calls of ``dkv_attend_layer``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+import dkv_hip
+import synth
+from compressed_attention import CompressedContext, ModelTables
+from hot_tier import OrderTables, PackedStream
+from progressive import plane_major_order, quantize8
+
+CONFIGS = {
+    # name: (shape, tokens, budget, query dtype)
+    "cfg0": (synth.SHAPE_1B, 1500, None, torch.float32),
+    "cfg1": (synth.SHAPE_1B, 8192, 0.02, torch.bfloat16),
+    "cfg2": (synth.SHAPE_3B, 16384, 0.03, torch.bfloat16),
+}
+
+
+@dataclass
+class DecodeWorkload:
+    name: str
+    shape: synth.ModelShape
+    context: CompressedContext
+    tables: ModelTables
+    streams: dict
+    queries: torch.Tensor        # [L, B, Hq, q_len, d]
+    key_exact: torch.Tensor      # [L, Hkv, E_total, d] f32
+    value_exact: torch.Tensor
+    outs: torch.Tensor           # [L, B, q_len, Hq, d]
+    args: list = field(default_factory=list)
+    workspace: torch.Tensor | None = None
+    tokens: int = 0
+    middle: int = 0
+    exact_lengths: tuple = ()
+    batch: int = 1
+    q_len: int = 1
+
+    def step(self) -> None:
+        """One decode step: every layer of compressed attention, in layer order."""
+        for a in self.args:
+            dkv_hip.attend_layer(a, self.workspace)
+
+    def step_split(self, starts=None, ends=None) -> None:
+        """Same work as ``step`` with K2 and K3 launched separately and optional timing
+        events recorded around each K2 launch (on the launch stream)."""
+        for i, a in enumerate(self.args):
+            if starts is not None:
+                starts[i].record()
+            dkv_hip.attend_scores(a, self.workspace)
+            if ends is not None:
+                ends[i].record()
+            dkv_hip.attend_values(a, self.workspace)
+
+    # ---- algorithmic work of one decode step (all layers) ----
+    def hot_code_bytes(self) -> int:
+        return sum(int(s.tables.prefix64[s.pieces.long()].sum()) for s in self.streams.values())
+
+    def bytes_per_layer(self) -> int:
+        s = self.shape
+        basis = 2 * s.rank * s.kv_heads * s.head_dim * 2  # fp16 key + value basis slices
+        return self.hot_code_bytes() + basis
+
+    def k2_flops_per_layer(self) -> int:
+        s = self.shape
+        n = self.middle_total
+        return 2 * n * s.rank * s.kv_heads * s.head_dim + 2 * n * s.q_heads * self.q_len * s.head_dim
+
+    def flops_per_layer(self) -> int:
+        s = self.shape
+        n = self.middle_total
+        rows = s.q_heads * self.q_len
+        return (self.k2_flops_per_layer() + 2 * rows * n * s.rank + 2 * rows * self.batch * s.rank * s.head_dim)
+
+    @property
+    def middle_total(self) -> int:
+        return self.context.key.n
+
+
+def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device) -> dict:
+    order = plane_major_order(shape.groups)
+    otab = OrderTables(order.planes, order.prefix_bytes, device)
+    streams = {}
+    for kind in ("key", "value"):
+        codes, low, span = quantize8(coefs[kind].to(device), 64)
+        pieces = torch.from_numpy(planes[kind] * shape.groups).to(device)
+        streams[kind] = PackedStream.pack(codes, low, span, pieces, otab, refine_capacity=0, with_cold=False)
+        del codes, low, span
+    return streams
+
+
+def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
+                 shape: synth.ModelShape | None = None, tokens: int | None = None, budget: float | None = None,
+                 query_dtype: torch.dtype | None = None, keep_host_basis: bool = False) -> DecodeWorkload:
+    """A single-conversation decode workload (configs 0-2).  ``keep_host_basis`` keeps float32
+    host copies of the bases (for the CPU baseline)."""
+    if name in CONFIGS:
+        s0, t0, b0, qd0 = CONFIGS[name]
+        shape, tokens = shape or s0, tokens or t0
+        budget = b0 if budget is None else budget
+        query_dtype = query_dtype or qd0
+    ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device)
+    streams = _pack_streams(ctx.coef, ctx.planes, shape, device)
+    cos, sin = synth.rope_tables(shape, tokens + q_len, device)
+    tables = ModelTables(ctx.basis["key"], ctx.basis["value"], ctx.mean["key"], ctx.mean["value"], shape.layers,
+                         shape.kv_heads, shape.head_dim, cos, sin)
+    positions = torch.arange(ctx.start, ctx.end, dtype=torch.int32)
+    context = CompressedContext(tables, streams["key"], streams["value"], positions, shape.q_heads)
+    new_coef = {kind: synth.coefficients(q_len, shape.rank, seed + 50 + i, device)
+                for i, kind in enumerate(("key", "value"))}
+    exact_coef = {kind: torch.cat([ctx.exact_coef[kind], new_coef[kind]]) for kind in ("key", "value")}
+    exact_pos = torch.cat([ctx.exact_positions(), torch.arange(tokens, tokens + q_len)]).to(device)
+    key_exact, value_exact = synth.decode_exact(ctx, exact_coef, exact_pos, cos, sin)
+    queries = synth.make_queries(shape, q_len, seed + 60, device, query_dtype, query_scale)
+    outs = torch.empty(shape.layers, 1, q_len, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
+    mask = None
+    if q_len > 1:
+        mask = synth.causal_mask(q_len, tokens - ctx.middle, device)[0, 0].contiguous()
+    w = DecodeWorkload(name, shape, context, tables, streams, queries, key_exact, value_exact, outs,
+                       tokens=tokens, middle=ctx.middle, exact_lengths=(key_exact.shape[2],), q_len=q_len)
+    w.args = [context.layer_args(l, queries[l], outs[l], key_exact[l], value_exact[l], mask) for l in range(shape.layers)]
+    w.workspace = context.workspace(w.args[0])
+    if keep_host_basis:
+        w.synthetic_basis_host = {k: v.cpu().numpy() for k, v in ctx.basis.items()}
+    # drop the float32 device bases now that the fp16 kernel layouts exist
+    ctx.basis.clear()
+    w.synthetic = ctx
+    return w
+
+
+def build_ragged(count: int = 32, lo: int = 2048, hi: int = 16384, budget: float = 0.03, seed: int = 3033,
+                 device="cuda", shape: synth.ModelShape = synth.SHAPE_3B,
+                 query_dtype: torch.dtype = torch.bfloat16) -> DecodeWorkload:
+    """Config 3: ``count`` conversations with lengths U[lo, hi], independent plane maps, one packed
+    buffer per stream and cu_seqlens offsets; one fused varlen decode step covers all of them."""
+    lengths = synth.ragged_lengths(count, lo, hi, seed)
+    basis = {"key": synth.orthonormal_basis(shape.features, shape.rank, seed + 1, device),
+             "value": synth.orthonormal_basis(shape.features, shape.rank, seed + 2, device)}
+    coefs = {"key": [], "value": []}
+    planes = {"key": [], "value": []}
+    positions, cu, exact_k, exact_v, exact_len = [], [0], [], [], []
+    cos, sin = synth.rope_tables(shape, max(lengths) + 1, device)
+    mean = None
+    for b, tokens in enumerate(lengths):
+        ctx = synth.make_context(shape, tokens, seed + 100 * (b + 1), budget=budget, device=device, basis=basis)
+        if mean is None:
+            mean = ctx.mean
+        ctx.mean = mean
+        for kind in ("key", "value"):
+            coefs[kind].append(ctx.coef[kind])
+            planes[kind].append(ctx.planes[kind])
+        positions.append(torch.arange(ctx.start, ctx.end, dtype=torch.int32))
+        cu.append(cu[-1] + ctx.middle)
+        new_coef = {kind: synth.coefficients(1, shape.rank, seed + 100 * (b + 1) + 50 + i, device)
+                    for i, kind in enumerate(("key", "value"))}
+        exact_coef = {kind: torch.cat([ctx.exact_coef[kind], new_coef[kind]]) for kind in ("key", "value")}
+        exact_pos = torch.cat([ctx.exact_positions(), torch.tensor([tokens])]).to(device)
+        ke, ve = synth.decode_exact(ctx, exact_coef, exact_pos, cos, sin)
+        exact_k.append(ke)
+        exact_v.append(ve)
+        exact_len.append(ke.shape[2])
+    coefs = {kind: torch.cat(v) for kind, v in coefs.items()}
+    planes = {kind: np.concatenate(v) for kind, v in planes.items()}
+    streams = _pack_streams(coefs, planes, shape, device)
+    del coefs
+    tables = ModelTables(basis["key"], basis["value"], mean["key"], mean["value"], shape.layers, shape.kv_heads,
+                         shape.head_dim, cos, sin)
+    basis.clear()
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    context = CompressedContext(tables, streams["key"], streams["value"], torch.cat(positions), shape.q_heads,
+                                cu_seqlens=cu_t)
+    key_exact = torch.cat(exact_k, dim=2).contiguous()  # [L, Hkv, E_total, d]
+    value_exact = torch.cat(exact_v, dim=2).contiguous()
+    queries = synth.make_queries(shape, 1, seed + 7, device, query_dtype).expand(-1, count, -1, -1, -1)
+    queries = (queries * torch.linspace(0.5, 1.5, count, device=device).to(query_dtype)[None, :, None, None, None])
+    queries = queries.contiguous()
+    outs = torch.empty(shape.layers, count, 1, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
+    w = DecodeWorkload("cfg3", shape, context, tables, streams, queries, key_exact, value_exact, outs,
+                       tokens=sum(lengths), middle=cu[-1], exact_lengths=tuple(exact_len), batch=count)
+    w.args = [context.layer_args(l, queries[l], outs[l], key_exact[l], value_exact[l], None, tuple(exact_len))
+              for l in range(shape.layers)]
+    w.workspace = context.workspace(w.args[0])
+    w.lengths = lengths
+    return w

@@ -15,7 +15,8 @@
  *   comment says "host".
  * - The library never allocates or frees memory.  Kernels that need scratch
  *   memory take a caller-provided workspace sized by the matching
- *   *_workspace_bytes() query.
+ *   *_workspace_bytes() query.  Calls that overlap on different streams
+ *   need separate workspaces.
  * - Calls are asynchronous on the given stream (hipStream_t passed as void*;
  *   NULL = the default stream) and never synchronise the host.
  * - Every entry point validates its arguments before launching anything and
@@ -149,6 +150,15 @@ typedef struct dkv_attend_args {
 
 size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);
 int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two halves of dkv_attend_layer, in this order on one stream with the
+ * same workspace: K2 (rebuild keys on MFMA, RoPE, score, per-tile softmax
+ * statistics; replaces compressed_attention.py:105-126) and K3 (value
+ * weighting in coefficient space, value basis once per KV head, exact-token
+ * merge and normalisation; replaces :127-137).  Exposed so callers can time
+ * or overlap them separately. */
+int dkv_attend_scores(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
+int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- K4a: question scoring over the hot tier ----------------------------
  * Replaces scripts/progressive.py:239-254 question_importance with

@@ -1,0 +1,65 @@
+"""The C-ABI library loads, exports every entry point include/dimmerkv.h declares, and its
+argument validation fails with the reference's exception types before touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import dkv_hip
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "dimmerkv.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dkv_[a-z_]+)\s*\(", text)))
+
+
+def test_header_declares_the_python_exports():
+    assert set(declared_symbols()) == set(dkv_hip.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = dkv_hip.lib()
+    missing = [name for name in declared_symbols() if not hasattr(lib, name)]
+    assert not missing, missing
+    assert lib.dkv_abi_version() == dkv_hip.ABI_VERSION
+
+
+def test_validation_errors_map_to_reference_exceptions():
+    lib = dkv_hip.lib()
+    order = dkv_hip.Order(0, 0, None, None, None, None)
+    rc = lib.dkv_pack_planes(None, None, None, None, ctypes.c_int32(4), order, None, None, None, None, None)
+    assert rc == -2  # DKV_ESHAPE: bad order checked before anything runs
+    assert b"bad order" in lib.dkv_last_error()
+    with pytest.raises(ValueError):
+        dkv_hip._check(rc, "dkv_pack_planes")
+    rc = lib.dkv_topk(None, ctypes.c_int32(10), ctypes.c_int32(3), None, None, ctypes.c_size_t(0), None)
+    assert rc == -1  # DKV_EINVAL: null pointer
+    rc = lib.dkv_dequantize_codes(ctypes.c_void_p(8), ctypes.c_void_p(8), ctypes.c_void_p(8), ctypes.c_void_p(8),
+                                  ctypes.c_int32(3), ctypes.c_int32(5), ctypes.c_int32(2), ctypes.c_void_p(8), None)
+    assert rc == -2  # planes_rows must be 1 or n
+    with pytest.raises(AssertionError):
+        dkv_hip._check(-5, "budget")
+    with pytest.raises(RuntimeError):
+        dkv_hip._check(-4, "launch")
+
+
+def test_attend_argument_checks():
+    lib = dkv_hip.lib()
+    a = dkv_hip.AttendArgs()
+    assert lib.dkv_attend_workspace_bytes(ctypes.byref(a)) == 0  # invalid -> 0 and an error message
+    assert b"dkv_attend_workspace_bytes" in lib.dkv_last_error()
+    assert lib.dkv_attend_layer(ctypes.byref(a), None, ctypes.c_size_t(0), None) in (-1, -2)
+
+
+def test_cpu_tensors_are_refused():
+    import torch
+
+    with pytest.raises(ValueError, match="GPU"):
+        dkv_hip.ptr(torch.zeros(3))
