@@ -42,7 +42,22 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "keys_scores_cfg2_traffic.txt"))
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
+                        "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     return p.parse_args()
+
+
+def copy_calibration(mib: int) -> None:
+    import torch
+
+    n = mib * 2**20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 5}), flush=True)
 
 
 def read_traffic(path: str):
@@ -98,6 +113,9 @@ def cpu_baseline(w, seconds: float):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); the multi-GPU design is described "
               "in DESIGN.md and is not run.", file=sys.stderr)

@@ -81,7 +81,9 @@ class CompressedContext:
         self.batch = self.cu_host.numel() - 1
         self.exact_cache = exact_cache
         self._workspace = None
+        self._prepared = None  # (plane_cap, key stream version) decoded into the workspace
         self._score_workspace = None
+        self._score_prepared = None
         self._cu_exact = {}
         self.importance = None  # float32 [n] while a question is being scored
 
@@ -143,9 +145,22 @@ class CompressedContext:
     def workspace(self, args) -> torch.Tensor:
         need = dkv_hip.attend_workspace_bytes(args)
         if self._workspace is None or self._workspace.numel() < need:
-            # zero-filled: the head of the workspace holds the kernels' completion counters
             self._workspace = torch.zeros(need, dtype=torch.uint8, device=self.key.blob.device)
+            self._prepared = None
         return self._workspace
+
+    def prepare(self, args, plane_cap: int = 8) -> None:
+        """K1: decode the key codes into the workspace (once per decode step; the layers reuse it)."""
+        dkv_hip.attend_prepare(args, self.workspace(args), plane_cap)
+        self._prepared = (plane_cap, self.key.version)
+
+    def run_layer(self, args) -> None:
+        """One layer through the C ABI; the key codes are decoded again at layer 0 (the start of
+        every forward) and whenever the key stream changed since the last decode."""
+        workspace = self.workspace(args)
+        if args.layer == 0 or self._prepared != (8, self.key.version):
+            self.prepare(args)
+        dkv_hip.attend_layer(args, workspace)
 
     def attend(self, module, query, key, value, attention_mask, scaling):
         """Same contract as an HF attention function: returns (output [B, T, H, D], None)."""
@@ -166,15 +181,18 @@ class CompressedContext:
             if attention_mask is not None:
                 mask = attention_mask[0, 0, :, -key.shape[2]:].float().contiguous()
         args = self.layer_args(layer, query, out, key_exact, value_exact, mask, lengths, scaling)
-        dkv_hip.attend_layer(args, self.workspace(args))
+        self.run_layer(args)
         if self.importance is not None:
             self._score(layer, query, key, scaling)
         return out, None
 
     # ----- question scoring over the hot codes (K4a) -----
-    def begin_scoring(self) -> None:
-        """Start accumulating the attention the compressed tokens receive (dimmer.py:60-66 scoring)."""
+    def begin_scoring(self, plane_cap: int = 8) -> None:
+        """Start accumulating the attention the compressed tokens receive (dimmer.py:60-66 scoring);
+        the question's keys are rebuilt from the first ``plane_cap`` planes of each group."""
         self.importance = torch.empty(self.key.n, dtype=torch.float32, device=self.key.blob.device)
+        self.score_plane_cap = plane_cap
+        self._score_prepared = None
         dkv_hip.score_begin(self.importance)
 
     def end_scoring(self) -> torch.Tensor:
@@ -203,6 +221,11 @@ class CompressedContext:
         need = dkv_hip.score_workspace_bytes(args)
         if self._score_workspace is None or self._score_workspace.numel() < need:
             self._score_workspace = torch.zeros(need, dtype=torch.uint8, device=query.device)
+            self._score_prepared = None
+        state = (self.score_plane_cap, self.key.version)
+        if self._score_prepared != state:
+            dkv_hip.attend_prepare(args, self._score_workspace, self.score_plane_cap)
+            self._score_prepared = state
         dkv_hip.score_layer(args, key_question, self.importance, self._score_workspace)
 
 

@@ -29,12 +29,10 @@ constexpr int kTileTok = 256;    // tokens per K2 workgroup
 constexpr int kK2Threads = 512;  // 8 waves: 4 token quarters x 2 row halves
 constexpr int kStride = 72;      // LDS row stride in halves for [row][64] tiles (64 + 8 pad)
 constexpr int kSplitTok = 1024;  // tokens per K3a split
-constexpr int kK3Threads = 256;  // 4 waves sharing one 64-component group
-constexpr int kVtStride = 40;    // LDS stride (halves) of the transposed value tile [64][32 + 8]
 constexpr int kChunk = 128;      // components per K3b workgroup
 
 struct K2Args {
-  dkv_stream_t key;
+  const uint16_t* coef;  // decoded key coefficients, fp16 [G][n_pad][64]
   const int32_t* cu_seqlens;
   const int32_t* positions;
   const uint16_t* key_basis;
@@ -46,7 +44,7 @@ struct K2Args {
   float* tile_max;
   float* tile_sum;
   float scaling;
-  int batch, layer, Hkv, Hq, q_len, G, n_total, ntiles, total_wg, per_xcd, query_dtype;
+  int batch, layer, Hkv, Hq, q_len, G, n_total, n_pad, ntiles, total_wg, per_xcd, query_dtype;
 };
 
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
@@ -63,9 +61,206 @@ DKV_DEVICE half8 load_query8(const void* q, long idx, int dtype) {
 }
 
 // ---------------------------------------------------------------------------
-// K2.  D = head_dim (64 or 128).  The workgroup covers HPW = 256 / D heads
-// (256 basis rows); wave w takes tokens (w & 3) * 64 .. +64 and basis rows
-// (w >> 2) * 128 .. +128 of the tile.
+// K1 (fp16 operand form): decode the hot key codes of every token into the
+// MFMA operand layout coef[g][t][64] (fp16, affine dequantization of the
+// codes truncated to min(m, plane_cap) planes).  One thread per (token,
+// group, half); rows t >= n_total (the padding every tile may over-read) are
+// written as zeros.  The coefficients depend on the stream only, so one
+// decode serves every layer.
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  dkv_stream_t s;
+  uint16_t* coef;
+  int n_total, n_pad, G, plane_cap;
+};
+
+constexpr int kDecodeTok = 128;
+
+// Block -> (token block, group) with the group fastest and consecutive ids on
+// one XCD, so the blocks reading the same tokens' blobs share that XCD's L2.
+DKV_DEVICE int2 decode_block(int G, int nblocks) {
+  const int per_xcd = (nblocks + 7) / 8;
+  const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  return make_int2(lin / G, lin % G);  // (token block, group); token block may be out of range
+}
+
+__global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs a) {
+  const int2 bg = decode_block(a.G, (a.n_pad / kDecodeTok) * a.G);
+  const int tb = bg.x, g = bg.y;
+  if (tb >= a.n_pad / kDecodeTok) return;
+  const int t = tb * kDecodeTok + (threadIdx.x >> 1);
+  const int half = threadIdx.x & 1;
+  uint32_t vals[16];
+  if (t < a.n_total) {
+    const int G = a.G;
+    const int kp = a.s.pieces[t];
+    const int m = a.s.order.planes[(long)kp * G + g];
+    const int mu = min(m, a.plane_cap);
+    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + a.s.order.seg_off[(long)kp * G + g];
+    uint32_t pl[8], header;
+    load_segment(seg, mu, half, pl, header);
+    if (m > 0 && mu == 0) header = 0u;
+    unpack_half_f16(pl, affine_from_header(header, mu), vals);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vals[j] = 0u;
+  }
+  uint4* dst = (uint4*)(a.coef + ((long)g * a.n_pad + t) * 64 + half * 32);
+  dst[0] = make_uint4(vals[0], vals[1], vals[2], vals[3]);
+  dst[1] = make_uint4(vals[4], vals[5], vals[6], vals[7]);
+  dst[2] = make_uint4(vals[8], vals[9], vals[10], vals[11]);
+  dst[3] = make_uint4(vals[12], vals[13], vals[14], vals[15]);
+}
+
+// ---------------------------------------------------------------------------
+// K2 epilogue for few query rows per KV head (decode: RH = (Hq/Hkv) * q_len
+// <= kSmallRows).  The keys never leave registers: the tile's RoPE rows are
+// staged in LDS (coalesced), each lane rotates the dimension pairs it holds
+// (d and d + D/2 sit in the same lane) and dots them with the query rows in
+// fp32; the two lanes holding the two halves of a token's dimensions combine
+// with one shuffle.  Scores and per-tile softmax statistics are written as in
+// the MFMA epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kSmallRows = 4;
+
+template <int D>
+DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
+                                           float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
+                                           int tile, int h0, int b, int RH) {
+  constexpr int HPW = 256 / D;
+  constexpr int DB = D / 32;
+  constexpr int HALF_BLK = DB / 2;
+  constexpr int HALF_D = D / 2;
+  constexpr int CSTR = HALF_D + 4;  // floats per staged RoPE row (keeps b128 reads conflict-free)
+  float* cs = (float*)lds_h;                 // [256][CSTR] cos
+  float* sn = cs + kTileTok * CSTR;          // [256][CSTR] sin
+  float* qs = sn + kTileTok * CSTR;          // [HPW][kSmallRows][D] query rows
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tq = wave & 3, hs = wave >> 2;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int gq = a.Hq / a.Hkv;
+
+  // stage RoPE rows of the tile's tokens and the query rows of the workgroup's heads
+  constexpr int V4_PER_ROW = HALF_D / 4;
+  for (int e = tid; e < kTileTok * V4_PER_ROW; e += kK2Threads) {
+    const int n = e / V4_PER_ROW, c = e % V4_PER_ROW;
+    float4 cv = make_float4(1.f, 1.f, 1.f, 1.f), sv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (n < count) {
+      const long pos = a.positions[tok0 + n];
+      cv = *(const float4*)(a.rope_cos + pos * HALF_D + 4 * c);
+      sv = *(const float4*)(a.rope_sin + pos * HALF_D + 4 * c);
+    }
+    *(float4*)(cs + n * CSTR + 4 * c) = cv;
+    *(float4*)(sn + n * CSTR + 4 * c) = sv;
+  }
+  for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
+    const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
+    const int qh = (h0 + hl) * gq + r / a.q_len, qi = r % a.q_len;
+    qs[(hl * kSmallRows + r) * D + d] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + d,
+                                                      a.query_dtype);
+  }
+  __syncthreads();
+
+  // part[hw][r][tb]: partial q . k over this lane's dimensions, head hw of the wave
+  constexpr int HPWAVE = HPW / 2;
+  float part[HPWAVE][kSmallRows][2];
+#pragma unroll
+  for (int hw = 0; hw < HPWAVE; ++hw)
+#pragma unroll
+    for (int r = 0; r < kSmallRows; ++r) part[hw][r][0] = part[hw][r][1] = 0.0f;
+#pragma unroll
+  for (int tb = 0; tb < 2; ++tb) {
+    const int n = tq * 64 + tb * 32 + l32;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      if ((rb % DB) >= HALF_BLK) continue;
+      const int rb2 = rb + HALF_BLK;
+      const int hw = rb / DB;
+      const int hl = hs * HPWAVE + hw;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int j = (rb % DB) * 32 + 8 * v4 + 4 * lhi;  // pair index, 0 .. D/2-1
+        const float4 c4 = *(const float4*)(cs + n * CSTR + j);
+        const float4 s4 = *(const float4*)(sn + n * CSTR + j);
+        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+        const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+        float rlo[4], rhi[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float klo = acc[tb][rb][v4 * 4 + e];
+          const float khi = acc[tb][rb2][v4 * 4 + e];
+          rlo[e] = klo * cv[e] - khi * sv[e];
+          rhi[e] = khi * cv[e] + klo * sv[e];
+        }
+#pragma unroll
+        for (int r = 0; r < kSmallRows; ++r) {
+          if (r >= RH) break;
+          const float4 qlo = *(const float4*)(qs + (hl * kSmallRows + r) * D + j);
+          const float4 qhi = *(const float4*)(qs + (hl * kSmallRows + r) * D + j + HALF_D);
+          part[hw][r][tb] += qlo.x * rlo[0] + qlo.y * rlo[1] + qlo.z * rlo[2] + qlo.w * rlo[3] + qhi.x * rhi[0] +
+                             qhi.y * rhi[1] + qhi.z * rhi[2] + qhi.w * rhi[3];
+        }
+      }
+    }
+  }
+  // combine the two dimension halves (lanes l32 and l32 + 32), write scores, tile statistics
+#pragma unroll
+  for (int hw = 0; hw < HPWAVE; ++hw) {
+    const int hl = hs * HPWAVE + hw;
+    const int h = h0 + hl;
+#pragma unroll
+    for (int r = 0; r < kSmallRows; ++r) {
+      if (r >= RH) break;
+      float x[2];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const float full = part[hw][r][tb] + __shfl_xor(part[hw][r][tb], 32, 64);
+        const int n = tq * 64 + tb * 32 + l32;
+        x[tb] = n < count ? full * a.scaling : -INFINITY;
+        if (tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
+      }
+      float mx = fmaxf(x[0], x[1]);
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      float sm = 0.0f;
+      if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+      if (lane == 0) {
+        stat_m[hl][tq][r] = mx;
+        stat_s[hl][tq][r] = sm;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < HPW * kSmallRows) {
+    const int hl = tid / kSmallRows, r = tid % kSmallRows;
+    if (r < RH) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][r]);
+      float S = 0.0f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float mq = stat_m[hl][q][r];
+          if (mq != -INFINITY) S += stat_s[hl][q][r] * __expf(mq - M);
+        }
+      }
+      const long o = (long)((h0 + hl) * RH + r) * a.ntiles + tile;
+      a.tile_max[o] = M;
+      a.tile_sum[o] = S;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K2.  D = head_dim (64 or 128).  The workgroup covers 256 tokens x HPW =
+// 256 / D heads (256 basis rows); wave w takes tokens (w & 3) * 64 .. +64
+// and basis rows (w >> 2) * 128 .. +128 of the tile.  Per 64-component
+// group: the decoded coefficient block [256][64] and the basis block
+// [256][64] are fetched into registers one group ahead and stored into a
+// double-buffered, padded LDS tile; 32x32x16 fp16 MFMAs accumulate the keys.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
@@ -93,48 +288,47 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int tq = wave & 3, hs = wave >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  // Unpack role: token ut, half uh.
-  const int ut = tid >> 1, uh = tid & 1;
-  const bool uvalid = ut < count;
-  const int ut_g = tok0 + ut;
-  const int ukp = uvalid ? a.key.pieces[ut_g] : 0;
-  const uint8_t* ubase = uvalid ? a.key.blob + a.key.tok_off[ut_g] : a.key.blob;
-  // The token's plane-count row (4 groups per dword, G % 4 == 0), kept in
-  // registers and fetched one dword ahead; the segment offset of each group
-  // is a running sum, so the loop never waits on an order-table lookup.
-  const uint32_t* prow = (const uint32_t*)(a.key.order.planes + (long)ukp * G);
-  uint32_t pw_cur = uvalid ? prow[0] : 0u;
-  uint32_t pw_nxt = (uvalid && G > 4) ? prow[1] : 0u;
-  int seg_run = 0;
-
+  const uint16_t* coef_tile = a.coef + (long)tok0 * 64;
+  const long coef_group_stride = (long)a.n_pad * 64;
   const uint16_t* basis_layer = a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h0 * D * 64;
   const long basis_group_stride = (long)a.Hkv * D * 64;
 
-  half_t* A0 = lds;                          // codes   [2][256][72]
-  half_t* B0 = lds + 2 * kTileTok * kStride;  // basis   [2][256][72]
+  half_t* A0 = lds;                          // coefficients [2][256][72]
+  half_t* B0 = lds + 2 * kTileTok * kStride;  // basis        [2][256][72]
 
+  // The accumulators start at the layer's key mean: key = mean + basis . coefficients.
+  // acc[tb][rb][v] holds token tq*64 + tb*32 + l32 and basis row
+  // hs*128 + rb*32 + 8*(v/4) + 4*lhi + (v&3) of the workgroup's 256 rows.
+  const float* mean_rows = a.mean_k + ((long)a.layer * a.Hkv + h0) * D + hs * 128 + 4 * lhi;
   floatx16 acc[2][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float4 m4 = *(const float4*)(mean_rows + j * 32 + 8 * v4);
+      acc[0][j][4 * v4 + 0] = acc[1][j][4 * v4 + 0] = m4.x;
+      acc[0][j][4 * v4 + 1] = acc[1][j][4 * v4 + 1] = m4.y;
+      acc[0][j][4 * v4 + 2] = acc[1][j][4 * v4 + 2] = m4.z;
+      acc[0][j][4 * v4 + 3] = acc[1][j][4 * v4 + 3] = m4.w;
+    }
 
-  uint32_t pl[8], header = 0u;
-  int um = 0;
-  uint4 br0, br1, br2, br3;
+  // Coefficient blocks are fetched two groups ahead (two register sets), basis
+  // blocks one group ahead; the basis loads of group g+1 are issued before the
+  // coefficient loads of group g+2 so that waiting for the former leaves the
+  // latter in flight.
+  uint4 a00, a01, a02, a03, a10, a11, a12, a13, br0, br1, br2, br3;
 
-#define DKV_K2_ISSUE(g_)                                                              \
+#define DKV_K2_ISSUE_A(g_, x0, x1, x2, x3)                                           \
   do {                                                                                \
-    const int gg_ = (g_);                                                             \
-    if ((gg_ & 3) == 0 && gg_ > 0) {                                                  \
-      pw_cur = pw_nxt;                                                                \
-      pw_nxt = (uvalid && gg_ + 4 < G) ? prow[(gg_ >> 2) + 1] : 0u;                   \
-    }                                                                                 \
-    um = (int)((pw_cur >> (8 * (gg_ & 3))) & 0xffu);                                  \
-    load_segment_nb(ubase + seg_run, um, uh, a.key.blob, pl, header);                 \
-    seg_run += um > 0 ? 4 + 8 * um : 0;                                               \
+    const uint4* asrc_ = (const uint4*)(coef_tile + (long)(g_) * coef_group_stride);  \
+    x0 = asrc_[0 * kK2Threads + tid];                                                 \
+    x1 = asrc_[1 * kK2Threads + tid];                                                 \
+    x2 = asrc_[2 * kK2Threads + tid];                                                 \
+    x3 = asrc_[3 * kK2Threads + tid];                                                 \
+  } while (0)
+
+#define DKV_K2_ISSUE_B(g_)                                                            \
+  do {                                                                                \
     const uint4* src_ = (const uint4*)(basis_layer + (long)(g_) * basis_group_stride); \
     br0 = src_[0 * kK2Threads + tid];                                                 \
     br1 = src_[1 * kK2Threads + tid];                                                 \
@@ -142,55 +336,85 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     br3 = src_[3 * kK2Threads + tid];                                                 \
   } while (0)
 
-#define DKV_K2_FINISH(buf_)                                                            \
-  do {                                                                                 \
-    const AffineDq dq_ = affine_from_header(header, um);                               \
-    uint32_t vals_[16];                                                                \
-    unpack_half_f16(pl, dq_, vals_);                                                   \
-    uint4* dstA_ = (uint4*)(A0 + ((buf_) * kTileTok + ut) * kStride + uh * 32);        \
-    dstA_[0] = make_uint4(vals_[0], vals_[1], vals_[2], vals_[3]);                     \
-    dstA_[1] = make_uint4(vals_[4], vals_[5], vals_[6], vals_[7]);                     \
-    dstA_[2] = make_uint4(vals_[8], vals_[9], vals_[10], vals_[11]);                   \
-    dstA_[3] = make_uint4(vals_[12], vals_[13], vals_[14], vals_[15]);                 \
-    half_t* bdst_ = B0 + (buf_) * kTileTok * kStride;                                  \
-    *(uint4*)(bdst_ + ((0 * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = br0;  \
-    *(uint4*)(bdst_ + ((1 * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = br1;  \
-    *(uint4*)(bdst_ + ((2 * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = br2;  \
-    *(uint4*)(bdst_ + ((3 * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = br3;  \
+#define DKV_K2_STORE(dst_, j_, v_) \
+  *(uint4*)((dst_) + (((j_) * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = (v_)
+
+#define DKV_K2_FINISH(buf_, x0, x1, x2, x3)                \
+  do {                                                     \
+    half_t* adst_ = A0 + (buf_) * kTileTok * kStride;      \
+    half_t* bdst_ = B0 + (buf_) * kTileTok * kStride;      \
+    DKV_K2_STORE(adst_, 0, x0);                            \
+    DKV_K2_STORE(adst_, 1, x1);                            \
+    DKV_K2_STORE(adst_, 2, x2);                            \
+    DKV_K2_STORE(adst_, 3, x3);                            \
+    DKV_K2_STORE(bdst_, 0, br0);                           \
+    DKV_K2_STORE(bdst_, 1, br1);                           \
+    DKV_K2_STORE(bdst_, 2, br2);                           \
+    DKV_K2_STORE(bdst_, 3, br3);                           \
   } while (0)
 
-  DKV_K2_ISSUE(0);
-  DKV_K2_FINISH(0);
-  for (int g = 0; g < G; ++g) {
-    const int buf = g & 1;
+#define DKV_K2_MFMA(buf_)                                                              \
+  do {                                                                                 \
+    const half_t* At = A0 + (buf_) * kTileTok * kStride;                               \
+    const half_t* Bt = B0 + (buf_) * kTileTok * kStride;                               \
+    _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                 \
+      const int kof = ks * 16 + lhi * 8;                                               \
+      half8 bop[2], aop[4];                                                            \
+      _Pragma("unroll") for (int tb = 0; tb < 2; ++tb)                                 \
+        bop[tb] = lds_half8(At + (tq * 64 + tb * 32 + l32) * kStride + kof);           \
+      _Pragma("unroll") for (int rb = 0; rb < 4; ++rb)                                 \
+        aop[rb] = lds_half8(Bt + (hs * 128 + rb * 32 + l32) * kStride + kof);          \
+      _Pragma("unroll") for (int tb = 0; tb < 2; ++tb)                                 \
+        _Pragma("unroll") for (int rb = 0; rb < 4; ++rb)                               \
+          acc[tb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[tb], acc[tb][rb], 0, 0, 0); \
+    }                                                                                  \
+  } while (0)
+
+  // Step g (even): MFMA on LDS buffer 0 while group g+1 (registers a1x) is
+  // stored into buffer 1 and group g+2 is fetched into a0x; odd steps swap.
+  // The loop body is branch-free (group indices past the end are clamped and
+  // the surplus blocks land in a buffer nobody reads) so that every wait on
+  // the loads is exact.
+  DKV_K2_ISSUE_A(0, a00, a01, a02, a03);
+  DKV_K2_ISSUE_B(0);
+  DKV_K2_ISSUE_A(1, a10, a11, a12, a13);
+  DKV_K2_FINISH(0, a00, a01, a02, a03);
+  for (int g = 0; g < G; g += 2) {  // G is a multiple of 4 (rank is a multiple of 256)
+    const int g2 = min(g + 2, G - 1), g3 = min(g + 3, G - 1);
+    // sched_barrier keeps the compiler from sinking the loads below the MFMAs
+    // (which would expose their latency) or hoisting the stores above them.
     __syncthreads();
-    if (g + 1 < G) DKV_K2_ISSUE(g + 1);
-    const half_t* At = A0 + buf * kTileTok * kStride;
-    const half_t* Bt = B0 + buf * kTileTok * kStride;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int kof = ks * 16 + lhi * 8;
-      half8 bop[2], aop[4];
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb) bop[tb] = lds_half8(At + (tq * 64 + tb * 32 + l32) * kStride + kof);
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) aop[rb] = lds_half8(Bt + (hs * 128 + rb * 32 + l32) * kStride + kof);
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-          acc[tb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[tb], acc[tb][rb], 0, 0, 0);
-    }
-    if (g + 1 < G) DKV_K2_FINISH(buf ^ 1);
+    DKV_K2_ISSUE_B(g + 1);
+    DKV_K2_ISSUE_A(g2, a00, a01, a02, a03);
+    __builtin_amdgcn_sched_barrier(0);
+    DKV_K2_MFMA(0);
+    __builtin_amdgcn_sched_barrier(0);
+    DKV_K2_FINISH(1, a10, a11, a12, a13);
+    __syncthreads();
+    DKV_K2_ISSUE_B(g2);
+    DKV_K2_ISSUE_A(g3, a10, a11, a12, a13);
+    __builtin_amdgcn_sched_barrier(0);
+    DKV_K2_MFMA(1);
+    __builtin_amdgcn_sched_barrier(0);
+    DKV_K2_FINISH(0, a00, a01, a02, a03);
   }
-#undef DKV_K2_ISSUE
+#undef DKV_K2_ISSUE_A
+#undef DKV_K2_ISSUE_B
+#undef DKV_K2_MFMA
+#undef DKV_K2_STORE
 #undef DKV_K2_FINISH
   __syncthreads();
 
-  // ---- epilogue 1: + mean, RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8]
-  half_t* Kl = lds;
-  const float* mean_layer = a.mean_k + (long)a.layer * a.Hkv * D;
+  const int gq = a.Hq / a.Hkv;
+  const int RH = gq * a.q_len;
   const int half_d = D / 2;
+  if (RH <= kSmallRows) {
+    keys_scores_small_epilogue<D>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH);
+    return;
+  }
+
+  // ---- epilogue 1 (many query rows): RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8]
+  half_t* Kl = lds;
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
     const int n = tq * 64 + tb * 32 + l32;
@@ -203,26 +427,21 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
       if ((rb % DB) >= HALF_BLK) continue;
       const int rb2 = rb + HALF_BLK;
       const int hl = hs * (128 / D) + rb / DB;
-      const float* mh = mean_layer + (long)(h0 + hl) * D;
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
         const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
-        const float4 mlo = *(const float4*)(mh + d0);
-        const float4 mhi = *(const float4*)(mh + d0 + half_d);
         float4 c = make_float4(1.f, 1.f, 1.f, 1.f), s = make_float4(0.f, 0.f, 0.f, 0.f);
         if (valid) {
           c = *(const float4*)(cosr + d0);
           s = *(const float4*)(sinr + d0);
         }
-        const float ml[4] = {mlo.x, mlo.y, mlo.z, mlo.w};
-        const float mhv[4] = {mhi.x, mhi.y, mhi.z, mhi.w};
         const float cv[4] = {c.x, c.y, c.z, c.w};
         const float sv[4] = {s.x, s.y, s.z, s.w};
         half4 lo, hi;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float klo = acc[tb][rb][v4 * 4 + e] + ml[e];
-          const float khi = acc[tb][rb2][v4 * 4 + e] + mhv[e];
+          const float klo = acc[tb][rb][v4 * 4 + e];
+          const float khi = acc[tb][rb2][v4 * 4 + e];
           lo[e] = (half_t)(klo * cv[e] - khi * sv[e]);
           hi[e] = (half_t)(khi * cv[e] + klo * sv[e]);
         }
@@ -234,8 +453,6 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __syncthreads();
 
   // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block.
-  const int gq = a.Hq / a.Hkv;
-  const int RH = gq * a.q_len;
   const int mblocks = (RH + 31) / 32;
   constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in this phase
   for (int mb = 0; mb < mblocks; ++mb) {
@@ -331,12 +548,13 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 }
 
 struct K3aArgs {
-  dkv_stream_t value;
+  const uint8_t* vcodes;  // decoded value codes, u8 [G][64][n_pad] (token-contiguous per component)
+  const float2* vaff;     // (scale, offset) per (group, token): value = code * scale + offset
   const int32_t* cu_seqlens;
   const float* scores;
   const float* tile_max;
   float* w_part;
-  int batch, R_total, n_total, ntiles, G, rank, nsplits, row_blocks;
+  int batch, R_total, n_total, n_pad, ntiles, G, rank, nsplits, row_blocks;
 };
 
 // Max over a sequence's tiles of one row, 8 lanes per row (all loads of a lane issued together).
@@ -357,40 +575,108 @@ DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, 
   return m;
 }
 
-// Loads of one 32-token chunk for the value unpack: metadata, order-table
-// entries, then the plane words (three dependent levels).
-struct ChunkLoads {
-  uint32_t pl[8];
-  uint32_t hdr;
-  int m;
-};
-
-DKV_DEVICE void chunk_loads(const dkv_stream_t& v, int tok0, int count, int t, int g, int half, ChunkLoads& c) {
-  const int G = v.order.groups;
-  if (t < count) {
-    const int tg = tok0 + t;
-    const int kp = v.pieces[tg];
-    const int64_t off = v.tok_off[tg];
-    c.m = v.order.planes[(long)kp * G + g];
-    load_segment(v.blob + off + v.order.seg_off[(long)kp * G + g], c.m, half, c.pl, c.hdr);
+// ---------------------------------------------------------------------------
+// K1 for the value side: every token's value codes (all hot planes) as 8-bit
+// codes, transposed to [G][64][n_pad] so that an MFMA operand (one component,
+// 8 consecutive tokens) is one 8-byte load, plus the per-(group, token) affine
+// form (scale = span / 256, offset = low + span * 2^-(m+1); 0 and 0 for a
+// group without planes).  One block = 128 tokens x one group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
+  __shared__ uint32_t tile[64][kDecodeTok / 4 + 1];  // [component][token / 4], bytes of 4 tokens per word
+  const int2 bg = decode_block(a.G, (a.n_pad / kDecodeTok) * a.G);
+  const int tb = bg.x, g = bg.y;
+  if (tb >= a.n_pad / kDecodeTok) return;
+  const int tl = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int t = tb * kDecodeTok + tl;
+  uint32_t cw[8];
+  float2 aff = make_float2(0.0f, 0.0f);
+  if (t < a.n_total) {
+    const int G = a.G;
+    const int kp = a.s.pieces[t];
+    const int m = a.s.order.planes[(long)kp * G + g];
+    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + a.s.order.seg_off[(long)kp * G + g];
+    uint32_t pl[8], header;
+    load_segment(seg, m, half, pl, header);
+    cw[0] = assemble_codes<0>(pl);
+    cw[1] = assemble_codes<1>(pl);
+    cw[2] = assemble_codes<2>(pl);
+    cw[3] = assemble_codes<3>(pl);
+    cw[4] = assemble_codes<4>(pl);
+    cw[5] = assemble_codes<5>(pl);
+    cw[6] = assemble_codes<6>(pl);
+    cw[7] = assemble_codes<7>(pl);
+    const AffineDq dq = affine_from_header(header, m);
+    aff = make_float2(dq.scale, dq.offset);
   } else {
-    c.m = 0;
-    c.hdr = 0u;
 #pragma unroll
-    for (int p = 0; p < 8; ++p) c.pl[p] = 0u;
+    for (int w = 0; w < 8; ++w) cw[w] = 0u;
   }
+  if (half == 0) vaff[(long)g * a.n_pad + t] = aff;
+  // byte i of cw[w] is component half*32 + 4w + i of token t
+  uint8_t* tb8 = (uint8_t*)&tile[0][0];
+  constexpr int ROWB = (kDecodeTok / 4 + 1) * 4;
+#pragma unroll
+  for (int w = 0; w < 8; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tb8[(half * 32 + 4 * w + i) * ROWB + tl] = (uint8_t)(cw[w] >> (8 * i));
+  __syncthreads();
+  // 64 components x 128 tokens: thread -> component c, 32 tokens
+  const int c = threadIdx.x >> 2, q = threadIdx.x & 3;
+  uint4 v;
+  v.x = tile[c][q * 8 + 0];
+  v.y = tile[c][q * 8 + 1];
+  v.z = tile[c][q * 8 + 2];
+  v.w = tile[c][q * 8 + 3];
+  uint4 v2;
+  v2.x = tile[c][q * 8 + 4];
+  v2.y = tile[c][q * 8 + 5];
+  v2.z = tile[c][q * 8 + 6];
+  v2.w = tile[c][q * 8 + 7];
+  uint4* dst = (uint4*)(vcodes + ((long)g * 64 + c) * a.n_pad + tb * kDecodeTok + q * 32);
+  dst[0] = v;
+  dst[1] = v2;
 }
 
-// K3a: workgroup = (token split of kSplitTok tokens, one 64-component group,
-// one block of 32 output rows).  Wave w owns the split's 32-token chunks
-// w, w+4, ...; the loads of the next chunk are issued before the current one
-// is processed.  p~ = exp(s - M_c) feeds the MFMA A operand straight from the
-// scores; value codes are unpacked to fp16 and transposed through a per-wave
-// LDS tile for the B operand; MFMA 32x32x16 accumulates; the four waves' sums
-// are reduced through LDS.
-__global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
-  __shared__ __attribute__((aligned(16))) half_t Vt[4][64 * kVtStride];
-  __shared__ float red[3][64][33];
+// 8 codes (bytes of lo, hi) -> 8 fp16 values equal to the codes.  (0x6400 | c)
+// is the fp16 number 1024 + c; subtracting 1024 is exact.
+DKV_DEVICE half8 codes_to_half8(uint32_t lo, uint32_t hi) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const uint32_t w0 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+  const uint32_t w1 = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+  const uint32_t w2 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+  const uint32_t w3 = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+  const half2_t bias = {(half_t)1024.0f, (half_t)1024.0f};
+  half2_t h0, h1, h2, h3;
+  __builtin_memcpy(&h0, &w0, 4);
+  __builtin_memcpy(&h1, &w1, 4);
+  __builtin_memcpy(&h2, &w2, 4);
+  __builtin_memcpy(&h3, &w3, 4);
+  h0 -= bias;
+  h1 -= bias;
+  h2 -= bias;
+  h3 -= bias;
+  half8 r;
+  r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+  r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// K3a: w[row][k] = sum_t p[row][t] * value[t][k] for one token split, one
+// 64-component group and one block of 32 rows, with p = exp(s - M_row).
+// value = code * scale + offset, so
+//   w = sum_t (p * scale)[row][t] * code[t][k]  +  sum_t p[row][t] * offset[t]:
+// the first term is a 32x32x16 fp16 MFMA with A = p * scale and B = the codes
+// (exact in fp16), the second a per-row scalar.  Wave w of the 8 takes tokens
+// w*128 .. +128 of the split in 16-token steps; the waves' sums meet in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kK3Waves = 8;
+constexpr int kK3WaveTok = kSplitTok / kK3Waves;  // 128
+
+__global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a) {
+  __shared__ float red[kK3Waves][32][65];
+  __shared__ float ored[kK3Waves][32];
   __shared__ float Mrow[32];
 
   const int bid = blockIdx.x;
@@ -404,8 +690,7 @@ __global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int ut = lane >> 1, uh = lane & 1;
-  {
+  if (tid < 256) {
     const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
     const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
     const int r = rbk * 32 + (tid >> 3);
@@ -416,85 +701,74 @@ __global__ __launch_bounds__(kK3Threads) void value_weights_kernel(K3aArgs a) {
   const int my_row = rbk * 32 + l32;
   const bool row_ok = my_row < a.R_total;
   const float my_M = Mrow[l32];
-  const float* srow = a.scores + (long)(row_ok ? my_row : 0) * a.n_total + tok0;
 
   floatx16 acc[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[nb][v] = 0.0f;
+  float osum = 0.0f;
 
-  half_t* vt = Vt[wave];
-  ChunkLoads cur;
-  int c0 = wave * 32;
-  chunk_loads(a.value, tok0, count, c0 + ut, g, uh, cur);
-  for (; c0 < count; c0 += 4 * 32) {
-    float sc[16];
+  const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
+  const float* srow = a.scores + (long)(row_ok ? my_row : 0) * a.n_total + tok0;
+  const float2* aff = a.vaff + (long)g * a.n_pad + tok0;
+  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_pad + tok0;
+  const uint8_t* col1 = col0 + 32L * a.n_pad;
+
+  // Branch-free steps: every load stays inside the padded buffers (n_pad reaches a
+  // whole split past n_total; the scores row is read at a clamped index), and
+  // tokens past the split's end get p = 0.
+  constexpr int STEPS = kK3WaveTok / 16;  // 8
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int t = c0 + (e >> 3) * 16 + lhi * 8 + (e & 7);
-      sc[e] = (row_ok && t < count) ? srow[t] : -INFINITY;
-    }
-    ChunkLoads nxt;
-    chunk_loads(a.value, tok0, count, c0 + 4 * 32 + ut, g, uh, nxt);
-    {
-      const AffineDq dq = affine_from_header(cur.hdr, cur.m);
-      uint32_t vals[16];
-      unpack_half_f16(cur.pl, dq, vals);
-      half_t* col = vt + uh * 32 * kVtStride + ut;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t v2 = vals[j];
-        uint16_t lo16 = (uint16_t)(v2 & 0xffffu), hi16 = (uint16_t)(v2 >> 16);
-        half_t hlo, hhi;
-        __builtin_memcpy(&hlo, &lo16, 2);
-        __builtin_memcpy(&hhi, &hi16, 2);
-        col[(2 * j) * kVtStride] = hlo;
-        col[(2 * j + 1) * kVtStride] = hhi;
-      }
-    }
-    half8 pa[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+  for (int st = 0; st < STEPS; ++st) {
+    const int t8 = wt0 + st * 16 + lhi * 8;  // this lane's 8 tokens: t8 .. t8+7 (split-relative)
+    float sc[8];
+    if (row_ok && t8 + 8 <= count) {
+      const float4 s0 = *(const float4*)(srow + t8);
+      const float4 s1 = *(const float4*)(srow + t8 + 4);
+      sc[0] = s0.x; sc[1] = s0.y; sc[2] = s0.z; sc[3] = s0.w;
+      sc[4] = s1.x; sc[5] = s1.y; sc[6] = s1.z; sc[7] = s1.w;
+    } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float s = sc[ks * 8 + e];
-        pa[ks][e] = (half_t)(s == -INFINITY ? 0.0f : __expf(s - my_M));
-      }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int kof = ks * 16 + lhi * 8;
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const half8 vb = lds_half8(vt + (nb * 32 + l32) * kVtStride + kof);
-        acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[ks], vb, acc[nb], 0, 0, 0);
+        const bool ok = row_ok && t8 + e < count;
+        const float v = srow[ok ? t8 + e : 0];
+        sc[e] = ok ? v : -INFINITY;
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    cur = nxt;
-  }
-  if (wave > 0) {
+    float2 af[8];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int e = 0; e < 8; ++e) af[e] = aff[t8 + e];
+    const uint2 c0 = *(const uint2*)(col0 + t8);
+    const uint2 c1 = *(const uint2*)(col1 + t8);
+    half8 pa;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) red[wave - 1][lane][nb * 16 + v] = acc[nb][v];
+    for (int e = 0; e < 8; ++e) {
+      const float p = sc[e] == -INFINITY ? 0.0f : __expf(sc[e] - my_M);
+      pa[e] = (half_t)(p * af[e].x);
+      osum += p * af[e].y;
+    }
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0.x, c0.y), acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1.x, c1.y), acc[1], 0, 0, 0);
   }
+  osum += __shfl_xor(osum, 32, 64);
+  // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3)
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v];
+  if (lhi == 0) ored[wave][l32] = osum;
   __syncthreads();
-  if (wave == 0) {
+  for (int e = tid; e < 32 * 64; e += kK3Waves * 64) {
+    const int r = e >> 6, k = e & 63;
+    const int row = rbk * 32 + r;
+    float s = 0.0f, o = 0.0f;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float s = acc[nb][v] + red[0][lane][nb * 16 + v] + red[1][lane][nb * 16 + v] +
-                        red[2][lane][nb * 16 + v];
-        const int row = rbk * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-        if (row < a.R_total) a.w_part[((long)sp * a.R_total + row) * a.rank + g * 64 + nb * 32 + l32] = s;
-      }
+    for (int w = 0; w < kK3Waves; ++w) {
+      s += red[w][r][k];
+      o += ored[w][r];
+    }
+    if (row < a.R_total) a.w_part[((long)sp * a.R_total + row) * a.rank + g * 64 + k] = s + o;
   }
 }
 
@@ -730,13 +1004,16 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
 // Workspace layout and argument checks.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int ntiles, nsplits, R_total, nchunks, n_total;
-  size_t scores, tile_max, tile_sum, w_part, out_part, total;
+  int ntiles, nsplits, R_total, nchunks, n_total, n_pad;
+  size_t coef, vcodes, vaff, scores, tile_max, tile_sum, w_part, out_part, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workspace: [scores][tile statistics][split partials][chunk partials].
+// Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
+// [split partials][chunk partials].
+// The coefficient area holds every token's keys decoded to fp16 [G][n_pad][64]; n_pad covers the
+// rows a last K2 tile (255) or K3a split (1023) may read past n_total; they decode to zeros.
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
   L.ntiles = 0;
@@ -747,9 +1024,16 @@ Layout make_layout(const dkv_attend_args_t* a) {
     L.nsplits += (len + kSplitTok - 1) / kSplitTok;
   }
   L.n_total = a->cu_seqlens_host[a->batch];
+  L.n_pad = (L.n_total + kSplitTok + kDecodeTok - 1) / kDecodeTok * kDecodeTok;
   L.R_total = a->q_heads * a->q_len;
   L.nchunks = a->rank / kChunk;
   size_t off = 0;
+  L.coef = off;
+  off += align256((size_t)L.n_pad * a->rank * 2);
+  L.vcodes = off;
+  off += align256((size_t)L.n_pad * a->rank);
+  L.vaff = off;
+  off += align256((size_t)L.n_pad * (a->rank / 64) * 8);
   L.scores = off;
   off += align256((size_t)L.R_total * L.n_total * 4);
   L.tile_max = off;
@@ -792,7 +1076,8 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
 int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st) {
   if (L.ntiles == 0) return DKV_OK;
   K2Args k{};
-  k.key = a->key;
+  k.coef = (const uint16_t*)(ws + L.coef);
+  k.n_pad = L.n_pad;
   k.cu_seqlens = a->cu_seqlens;
   k.positions = a->positions;
   k.key_basis = a->key_basis;
@@ -829,6 +1114,37 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
 extern "C" size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a) {
   if (check_attend(a, "dkv_attend_workspace_bytes")) return 0;
   return make_layout(a).total;
+}
+
+extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int rc = check_attend(a, "dkv_attend_prepare");
+  if (rc) return rc;
+  DKV_REQUIRE(plane_cap >= 0 && plane_cap <= 8, DKV_EINVAL, "dkv_attend_prepare: plane_cap %d not in 0..8",
+              plane_cap);
+  const Layout L = make_layout(a);
+  DKV_REQUIRE(workspace && workspace_bytes >= L.total, DKV_EWORKSPACE,
+              "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.total);
+  DecodeArgs d{};
+  d.s = a->key;
+  d.coef = (uint16_t*)((char*)workspace + L.coef);
+  d.n_total = L.n_total;
+  d.n_pad = L.n_pad;
+  d.G = a->key.order.groups;
+  d.plane_cap = plane_cap;
+  const dim3 grid((unsigned)(((long)d.G * (L.n_pad / kDecodeTok) + 7) / 8 * 8));
+  hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), d);
+  rc = dkv::check_launch("decode_keys");
+  if (rc || !a->value.blob) return rc;
+  rc = dkv::check_stream(&a->value, "dkv_attend_prepare");
+  if (rc) return rc;
+  DKV_REQUIRE(a->value.order.groups == a->key.order.groups, DKV_ESHAPE, "dkv_attend_prepare: K/V group mismatch");
+  DecodeArgs v = d;
+  v.s = a->value;
+  v.plane_cap = 8;
+  hipLaunchKernelGGL(decode_values_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), v,
+                     (uint8_t*)((char*)workspace + L.vcodes), (float2*)((char*)workspace + L.vaff));
+  return dkv::check_launch("decode_values");
 }
 
 static int check_values(const dkv_attend_args_t* a, int& E_total) {
@@ -875,7 +1191,8 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   const int G = a->key.order.groups;
   if (L.nsplits > 0) {
     K3aArgs k{};
-    k.value = a->value;
+    k.vcodes = (const uint8_t*)(ws + L.vcodes);
+    k.vaff = (const float2*)(ws + L.vaff);
     k.cu_seqlens = a->cu_seqlens;
     k.scores = (const float*)(ws + L.scores);
     k.tile_max = (const float*)(ws + L.tile_max);
@@ -883,13 +1200,14 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.batch = a->batch;
     k.R_total = L.R_total;
     k.n_total = L.n_total;
+    k.n_pad = L.n_pad;
     k.ntiles = L.ntiles;
     k.G = G;
     k.rank = a->rank;
     k.nsplits = L.nsplits;
     k.row_blocks = (L.R_total + 31) / 32;
     const long blocks = (long)L.nsplits * k.row_blocks * G;
-    hipLaunchKernelGGL(value_weights_kernel, dim3((unsigned)blocks), dim3(kK3Threads), 0, st, k);
+    hipLaunchKernelGGL(value_weights_kernel, dim3((unsigned)blocks), dim3(kK3Waves * 64), 0, st, k);
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
   }

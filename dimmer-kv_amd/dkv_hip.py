@@ -23,7 +23,8 @@ _DTYPE = {torch.float32: DKV_F32, torch.float16: DKV_F16, torch.bfloat16: DKV_BF
 
 EXPORTS = [
     "dkv_abi_version", "dkv_last_error", "dkv_pack_planes", "dkv_unpack_dequant", "dkv_dequantize_codes",
-    "dkv_prepare_key_basis", "dkv_prepare_value_basis", "dkv_attend_workspace_bytes", "dkv_attend_layer",
+    "dkv_prepare_key_basis", "dkv_prepare_value_basis", "dkv_attend_workspace_bytes", "dkv_attend_prepare",
+    "dkv_attend_layer",
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
     "dkv_gather_cold",
@@ -151,6 +152,12 @@ def attend_workspace_bytes(args: AttendArgs) -> int:
     if n == 0:
         _check(-2, "dkv_attend_workspace_bytes")
     return n
+
+
+def attend_prepare(args: AttendArgs, workspace: torch.Tensor, plane_cap: int = 8) -> None:
+    """K1 into the workspace: every token's key codes decoded (to ``plane_cap`` planes) for K2."""
+    _check(lib().dkv_attend_prepare(ctypes.byref(args), c_i32(plane_cap), c_vp(ptr(workspace)),
+                                    c_sz(workspace.numel()), c_vp(stream_handle())), "dkv_attend_prepare")
 
 
 def attend_layer(args: AttendArgs, workspace: torch.Tensor) -> None:

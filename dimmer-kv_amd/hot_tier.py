@@ -76,6 +76,7 @@ class PackedStream:
         self.hot_used = hot_used
         self.refine_capacity = refine_capacity
         self.refined = 0
+        self.version = 0  # bumped whenever tokens change (refine), so decoded copies know to refresh
         self.initial_pieces = pieces.clone()
 
     @property
@@ -140,4 +141,5 @@ class PackedStream:
         dkv_hip.gather_cold(self.c_stream(), self.cold, self.cold_off, rows, base, self.blob, self.tok_off,
                             self.pieces)
         self.refined += k
+        self.version += 1
         return fetched

@@ -49,13 +49,15 @@ class DecodeWorkload:
     q_len: int = 1
 
     def step(self) -> None:
-        """One decode step: every layer of compressed attention, in layer order."""
+        """One decode step: K1 decode of the key codes, then every layer of compressed attention."""
+        dkv_hip.attend_prepare(self.args[0], self.workspace)
         for a in self.args:
             dkv_hip.attend_layer(a, self.workspace)
 
     def step_split(self, starts=None, ends=None) -> None:
         """Same work as ``step`` with K2 and K3 launched separately and optional timing
         events recorded around each K2 launch (on the launch stream)."""
+        dkv_hip.attend_prepare(self.args[0], self.workspace)
         for i, a in enumerate(self.args):
             if starts is not None:
                 starts[i].record()

@@ -149,6 +149,19 @@ typedef struct dkv_attend_args {
 } dkv_attend_args_t;
 
 size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);
+
+/* K1 for the attention kernels (replaces the per-conversation fp16
+ * coefficient blocks of scripts/compressed_attention.py:71-77, built from
+ * scripts/progressive.py:47-55 dequantize at each token's hot planes): decodes
+ * every compressed token's key codes, truncated to min(planes, plane_cap)
+ * bit-planes (8 = all hot planes; scoring "with the first 2 planes" passes 2),
+ * into the workspace in the MFMA operand layout.  The decoded keys depend on
+ * the key stream only: call it once before the layers of a decode step (and
+ * again after the stream changes, e.g. dkv_gather_cold); every later
+ * dkv_attend_layer / dkv_attend_scores / dkv_score_layer on the same
+ * workspace reads it. */
+int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap, void* workspace, size_t workspace_bytes,
+                       void* stream);
 int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The two halves of dkv_attend_layer, in this order on one stream with the

@@ -106,7 +106,7 @@ def gpu_attend(case: Case, ctx, layer: int, out_dtype=torch.float32, device="cud
     ve = case.value_exact[layer].to(device).contiguous()
     mask = None if case.mask is None else case.mask.to(device).contiguous()
     args = ctx.layer_args(layer, q, out, ke, ve, mask)
-    dkv_hip.attend_layer(args, ctx.workspace(args))
+    ctx.run_layer(args)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 

@@ -112,8 +112,7 @@ def test_attend_special_cases():
     q = case.queries[0].to(DEV).contiguous()
     out = torch.empty(1, 1, shape.q_heads, shape.head_dim, device=DEV)
     args = ctx.layer_args(0, q, out)
-    import dkv_hip
-    dkv_hip.attend_layer(args, ctx.workspace(args))
+    ctx.run_layer(args)
     torch.cuda.synchronize()
     expect = value_mean_base(case, 0)
     assert np.allclose(out.cpu().numpy(), expect, atol=1e-6, rtol=1e-5)
