@@ -22,7 +22,16 @@ path (the HIP library and its Python wrappers) never calls it.
 
 Parity pins: every function here is checked in ``tests/test_oracle_*.py``
 against closed forms, library routines (transformers' RoPE, torch.topk /
-stable sort), brute force on tiny inputs or invariants.  Functions whose
-bit-exact behaviour only the reference itself could fix are marked
-"parity unpinned" in their docstring.
+stable sort, torch's scaled_dot_product_attention), brute force on tiny
+inputs or invariants.  What only the reference itself could fix bit for bit
+is "parity unpinned" and marked so in the function's docstring:
+
+- ``progressive_ref.quantize8`` on a degenerate group whose fp16 range
+  rounds to 0 (the reference casts NaN to uint8; this build defines code 0);
+- ``progressive_ref.error_table`` last-bit sums at near-ties (numpy's and
+  torch's float32 reduction orders differ), hence allocations at near-ties;
+- ``scoring_ref.topk_indices`` at near-ties of the count-th score (the
+  margin is recorded by the tests);
+- ``rope_ref.rope_tables`` beyond one ulp of an inverse frequency (the product
+  and the tests take the tables from transformers, as the reference does).
 """

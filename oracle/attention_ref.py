@@ -17,7 +17,7 @@ operation, in float32 (the reference's ``dtype=torch.float32`` context):
 value in full (``inverse_transform``, scripts/kvtc.py:88-97) and runs textbook
 softmax attention in float64 with repeat_kv GQA
 (transformers/models/llama/modeling_llama.py:179-188).  The equality of the two
-(scripts/compressed_attention.py:15-19) is checked in tests/test_oracle_attention.py.
+(scripts/compressed_attention.py:15-19) is checked in tests/test_oracle_rope_attention.py.
 """
 
 from __future__ import annotations

@@ -7,7 +7,7 @@ Follows scripts/kvtc.py of the reference:
 - ``allocate_rungs``  :277-298 (fp64 values, cummin along levels, *stable*
   descending sort, take the sorted prefix whose cumulative cost fits)
 
-Pins (tests/test_oracle_kvtc.py): allocate_rungs against an exhaustive
+Pins (tests/test_oracle_kvtc_scoring_packing.py): allocate_rungs against an exhaustive
 brute force of the same greedy rule on tiny inputs, against the invariants
 (budget respected, per-slot upgrades form a prefix), and against torch's
 stable sort on random inputs; quantize_groups against its closed-form grid.

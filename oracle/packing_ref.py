@@ -25,6 +25,10 @@ Layout of one stream ("DKV1"):
   lane rebuild four 8-bit codes with one AND-OR per plane and one rotate
   (rotr(OR_p(word_p & mask(p, w)), w) has byte i = code of coefficient 4w+i
   truncated to the present planes).
+
+Pins (tests/test_oracle_kvtc_scoring_packing.py): per-plane bit positions are
+a bijection, pack/unpack round-trips, both tiers' byte sizes equal the
+reference's counts, and the lane formula above rebuilds the truncated codes.
 """
 
 from __future__ import annotations

@@ -5,9 +5,13 @@ Follows:
   which Llama-3.2 uses through ``LlamaRotaryEmbedding`` (modeling_llama.py:64-126);
 - scripts/kvtc.py:27-29 (``rotate_half``), :32-37 (``rope_tables``), :46-47 (``rerotate``).
 
-Pinned by tests/test_oracle_rope.py against transformers' own
+Pinned by tests/test_oracle_rope_attention.py against transformers' own
 ``LlamaRotaryEmbedding`` (a library routine present in this container) and
 by the closed-form identities cos^2 + sin^2 = 1 and rerotate o derotate = id.
+numpy's float32 ``power`` can differ from torch's by one ulp in an inverse
+frequency, so the tables agree with transformers' to within that ulp times the
+position (checked), not bit for bit.  The product path and the parity tests
+take their cos/sin tables from transformers itself, as the reference does.
 """
 
 from __future__ import annotations

@@ -14,6 +14,10 @@ The softmax here is exact fp32 per row in numpy order.  torch's fp32 sum
 order can differ in the last bit, so index sets are compared with the score
 margin between the count-th and (count+1)-th value recorded; at a near-tie
 the set is parity unpinned.
+
+Pins (tests/test_oracle_kvtc_scoring_packing.py): per-layer probabilities
+against a float64 brute force over every key, the selection count against
+Python's rounding, the index set against torch.topk on distinct scores.
 """
 
 from __future__ import annotations
