@@ -117,8 +117,8 @@ def main():
         copy_calibration(args.copy_calibration)
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); the multi-GPU design is described "
-              "in DESIGN.md and is not run.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for {args.gpus}): this build runs the decode path on a "
+              "single GPU; sharding tokens across GPUs is a design, not a measured configuration.", file=sys.stderr)
         sys.exit(2)
     import torch
 

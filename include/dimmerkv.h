@@ -66,8 +66,9 @@ typedef struct dkv_order {
 /* One stream (keys or values) of a packed hot tier.  Token t's hot blob
  * starts at blob + tok_off[t] and holds pieces[t] pieces
  * (prefix_bytes[pieces[t]] bytes).  Layout: for every group with m > 0
- * planes, [low f16][span f16][m plane words of 8 B]; plane-word bit order is
- * documented in oracle/packing_ref.py and DESIGN.md. */
+ * planes, [low f16][span f16][m plane words of 8 B].  A plane word is two
+ * little-endian u32 halves; coefficient 32h + 4w + i (w < 8, i < 4) of plane
+ * p (0 = most significant bit) sits at bit (8i + w + 7 - p) mod 32 of half h. */
 typedef struct dkv_stream {
   const uint8_t* blob;
   const int64_t* tok_off; /* [n] */
