@@ -32,7 +32,7 @@ constexpr int kSplitTok = 1024;  // tokens per K3a split
 constexpr int kChunk = 128;      // components per K3b workgroup
 
 struct K2Args {
-  const uint16_t* coef;  // decoded key coefficients, fp16 [G][n_pad][64]
+  const uint16_t* coef;  // decoded key coefficients, MFMA fragment order over slots
   const int32_t* cu_seqlens;
   const int32_t* positions;
   const uint16_t* key_basis;
@@ -44,7 +44,7 @@ struct K2Args {
   float* tile_max;
   float* tile_sum;
   float scaling;
-  int batch, layer, Hkv, Hq, q_len, G, n_total, n_pad, ntiles, total_wg, per_xcd, query_dtype;
+  int batch, layer, Hkv, Hq, q_len, G, n_total, n_slots, ntiles, total_wg, per_xcd, query_dtype;
 };
 
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
@@ -61,37 +61,60 @@ DKV_DEVICE half8 load_query8(const void* q, long idx, int dtype) {
 }
 
 // ---------------------------------------------------------------------------
-// K1 (fp16 operand form): decode the hot key codes of every token into the
-// MFMA operand layout coef[g][t][64] (fp16, affine dequantization of the
-// codes truncated to min(m, plane_cap) planes).  One thread per (token,
-// group, half); rows t >= n_total (the padding every tile may over-read) are
-// written as zeros.  The coefficients depend on the stream only, so one
-// decode serves every layer.
+// Token slots.  Every sequence's compressed tokens are cut into tiles of 256
+// (the K2 tile; the last tile of a sequence may be partial) and tile i owns
+// slots 256*i .. 256*i+255 of the decoded buffers, so every tile starts at an
+// aligned slot and its unused slots are padding that decodes to zero.  The
+// buffers hold n_slots = 256 * ntiles + kSplitTok slots: a K3a split (4 tiles)
+// starting at any tile stays inside them.
 // ---------------------------------------------------------------------------
 struct DecodeArgs {
   dkv_stream_t s;
-  uint16_t* coef;
-  int n_total, n_pad, G, plane_cap;
+  const int32_t* cu_seqlens;
+  uint16_t* coef;  // keys: fp16 in MFMA fragment order (see decode_keys_kernel)
+  int batch, ntiles, n_slots, G, plane_cap;
 };
 
-constexpr int kDecodeTok = 128;
+constexpr int kDecodeTok = 128;  // slots per decode block
 
-// Block -> (token block, group) with the group fastest and consecutive ids on
+// Block -> (slot block, group) with the group fastest and consecutive ids on
 // one XCD, so the blocks reading the same tokens' blobs share that XCD's L2.
 DKV_DEVICE int2 decode_block(int G, int nblocks) {
   const int per_xcd = (nblocks + 7) / 8;
   const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  return make_int2(lin / G, lin % G);  // (token block, group); token block may be out of range
+  return make_int2(lin / G, lin % G);  // (slot block, group); slot block may be out of range
 }
 
+// Token held by `slot`, or -1 for a padding slot.
+DKV_DEVICE int slot_token(const DecodeArgs& a, int slot) {
+  const int tile = slot / kTileTok;
+  if (tile >= a.ntiles) return -1;
+  const int2 bt = find_tile(a.cu_seqlens, a.batch, kTileTok, tile);
+  const int tok0 = a.cu_seqlens[bt.x] + bt.y * kTileTok;
+  const int n = slot - tile * kTileTok;
+  return n < a.cu_seqlens[bt.x + 1] - tok0 ? tok0 + n : -1;
+}
+
+// ---------------------------------------------------------------------------
+// K1 (fp16 operand form): decode the hot key codes of every token into the
+// exact register image of a 32x32x16 MFMA operand: for 64-component group g,
+// 32-slot block j and 16-component step ks, lane l (0..63) holds components
+// ks*16 + (l/32)*8 .. +8 of slot 32j + l%32, so K2 loads each operand with one
+// coalesced 16-byte load per lane.  Values are the affine dequantization of
+// the codes truncated to min(m, plane_cap) planes.  One thread per (slot,
+// group, half).  The decoded keys depend on the stream only, so one decode
+// serves every layer.
+// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs a) {
-  const int2 bg = decode_block(a.G, (a.n_pad / kDecodeTok) * a.G);
-  const int tb = bg.x, g = bg.y;
-  if (tb >= a.n_pad / kDecodeTok) return;
-  const int t = tb * kDecodeTok + (threadIdx.x >> 1);
+  const int nsb = a.n_slots / kDecodeTok;
+  const int2 bg = decode_block(a.G, nsb * a.G);
+  const int sb = bg.x, g = bg.y;
+  if (sb >= nsb) return;
+  const int slot = sb * kDecodeTok + (threadIdx.x >> 1);
   const int half = threadIdx.x & 1;
+  const int t = slot_token(a, slot);
   uint32_t vals[16];
-  if (t < a.n_total) {
+  if (t >= 0) {
     const int G = a.G;
     const int kp = a.s.pieces[t];
     const int m = a.s.order.planes[(long)kp * G + g];
@@ -99,17 +122,20 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs 
     const uint8_t* seg = a.s.blob + a.s.tok_off[t] + a.s.order.seg_off[(long)kp * G + g];
     uint32_t pl[8], header;
     load_segment(seg, mu, half, pl, header);
-    if (m > 0 && mu == 0) header = 0u;
     unpack_half_f16(pl, affine_from_header(header, mu), vals);
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j) vals[j] = 0u;
   }
-  uint4* dst = (uint4*)(a.coef + ((long)g * a.n_pad + t) * 64 + half * 32);
-  dst[0] = make_uint4(vals[0], vals[1], vals[2], vals[3]);
-  dst[1] = make_uint4(vals[4], vals[5], vals[6], vals[7]);
-  dst[2] = make_uint4(vals[8], vals[9], vals[10], vals[11]);
-  dst[3] = make_uint4(vals[12], vals[13], vals[14], vals[15]);
+  // components half*32 + 8*c .. +8 (c = 0..3): ks = 2*half + c/2, lane half = c%2
+  const long blk = (long)g * (a.n_slots / 32) + slot / 32;
+  const int l32 = slot % 32;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int ks = 2 * half + c / 2, lh = c % 2;
+    uint4* dst = (uint4*)(a.coef + ((blk * 4 + ks) * 64 + lh * 32 + l32) * 8);
+    *dst = make_uint4(vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -288,17 +314,16 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int tq = wave & 3, hs = wave >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  const uint16_t* coef_tile = a.coef + (long)tok0 * 64;
-  const long coef_group_stride = (long)a.n_pad * 64;
+  // Coefficient operands come straight from the decoded buffer (one 16-byte
+  // load per lane per MFMA operand); the basis block [256][64] goes global ->
+  // registers -> padded, double-buffered LDS.  Both are fetched one group ahead.
+  const half8* coef_frag = (const half8*)a.coef + ((long)(tile * 8 + tq * 2) * 4) * 64 + lane;
+  const long coef_group_stride = (long)(a.n_slots / 32) * 4 * 64;  // in half8 units
   const uint16_t* basis_layer = a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h0 * D * 64;
   const long basis_group_stride = (long)a.Hkv * D * 64;
 
-  half_t* A0 = lds;                          // coefficients [2][256][72]
-  half_t* B0 = lds + 2 * kTileTok * kStride;  // basis        [2][256][72]
+  half_t* B0 = lds;  // basis [2][256][72]
 
-  // The accumulators start at the layer's key mean: key = mean + basis . coefficients.
-  // acc[tb][rb][v] holds token tq*64 + tb*32 + l32 and basis row
-  // hs*128 + rb*32 + 8*(v/4) + 4*lhi + (v&3) of the workgroup's 256 rows.
   const float* mean_rows = a.mean_k + ((long)a.layer * a.Hkv + h0) * D + hs * 128 + 4 * lhi;
   floatx16 acc[2][4];
 #pragma unroll
@@ -312,19 +337,16 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
       acc[0][j][4 * v4 + 3] = acc[1][j][4 * v4 + 3] = m4.w;
     }
 
-  // Coefficient blocks are fetched two groups ahead (two register sets), basis
-  // blocks one group ahead; the basis loads of group g+1 are issued before the
-  // coefficient loads of group g+2 so that waiting for the former leaves the
-  // latter in flight.
-  uint4 a00, a01, a02, a03, a10, a11, a12, a13, br0, br1, br2, br3;
+  // af[tb*4 + ks]: coefficient operand of token block tb, step ks
+  half8 af0[8], af1[8];
+  uint4 br0, br1, br2, br3;
 
-#define DKV_K2_ISSUE_A(g_, x0, x1, x2, x3)                                           \
-  do {                                                                                \
-    const uint4* asrc_ = (const uint4*)(coef_tile + (long)(g_) * coef_group_stride);  \
-    x0 = asrc_[0 * kK2Threads + tid];                                                 \
-    x1 = asrc_[1 * kK2Threads + tid];                                                 \
-    x2 = asrc_[2 * kK2Threads + tid];                                                 \
-    x3 = asrc_[3 * kK2Threads + tid];                                                 \
+#define DKV_K2_ISSUE_A(g_, af_)                                             \
+  do {                                                                      \
+    const half8* src_ = coef_frag + (long)(g_) * coef_group_stride;        \
+    af_[0] = src_[0 * 64]; af_[1] = src_[1 * 64]; af_[2] = src_[2 * 64];   \
+    af_[3] = src_[3 * 64]; af_[4] = src_[4 * 64]; af_[5] = src_[5 * 64];   \
+    af_[6] = src_[6 * 64]; af_[7] = src_[7 * 64];                          \
   } while (0)
 
 #define DKV_K2_ISSUE_B(g_)                                                            \
@@ -339,64 +361,51 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 #define DKV_K2_STORE(dst_, j_, v_) \
   *(uint4*)((dst_) + (((j_) * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = (v_)
 
-#define DKV_K2_FINISH(buf_, x0, x1, x2, x3)                \
+#define DKV_K2_FINISH(buf_)                                \
   do {                                                     \
-    half_t* adst_ = A0 + (buf_) * kTileTok * kStride;      \
     half_t* bdst_ = B0 + (buf_) * kTileTok * kStride;      \
-    DKV_K2_STORE(adst_, 0, x0);                            \
-    DKV_K2_STORE(adst_, 1, x1);                            \
-    DKV_K2_STORE(adst_, 2, x2);                            \
-    DKV_K2_STORE(adst_, 3, x3);                            \
     DKV_K2_STORE(bdst_, 0, br0);                           \
     DKV_K2_STORE(bdst_, 1, br1);                           \
     DKV_K2_STORE(bdst_, 2, br2);                           \
     DKV_K2_STORE(bdst_, 3, br3);                           \
   } while (0)
 
-#define DKV_K2_MFMA(buf_)                                                              \
+#define DKV_K2_MFMA(buf_, af_)                                                         \
   do {                                                                                 \
-    const half_t* At = A0 + (buf_) * kTileTok * kStride;                               \
     const half_t* Bt = B0 + (buf_) * kTileTok * kStride;                               \
     _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                 \
       const int kof = ks * 16 + lhi * 8;                                               \
-      half8 bop[2], aop[4];                                                            \
-      _Pragma("unroll") for (int tb = 0; tb < 2; ++tb)                                 \
-        bop[tb] = lds_half8(At + (tq * 64 + tb * 32 + l32) * kStride + kof);           \
+      half8 aop[4];                                                                    \
       _Pragma("unroll") for (int rb = 0; rb < 4; ++rb)                                 \
         aop[rb] = lds_half8(Bt + (hs * 128 + rb * 32 + l32) * kStride + kof);          \
       _Pragma("unroll") for (int tb = 0; tb < 2; ++tb)                                 \
         _Pragma("unroll") for (int rb = 0; rb < 4; ++rb)                               \
-          acc[tb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], bop[tb], acc[tb][rb], 0, 0, 0); \
+          acc[tb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[rb], af_[tb * 4 + ks], acc[tb][rb], 0, 0, 0); \
     }                                                                                  \
   } while (0)
 
-  // Step g (even): MFMA on LDS buffer 0 while group g+1 (registers a1x) is
-  // stored into buffer 1 and group g+2 is fetched into a0x; odd steps swap.
-  // The loop body is branch-free (group indices past the end are clamped and
-  // the surplus blocks land in a buffer nobody reads) so that every wait on
-  // the loads is exact.
-  DKV_K2_ISSUE_A(0, a00, a01, a02, a03);
+  // Branch-free loop (group indices past the end are clamped; the surplus
+  // basis block lands in a buffer nobody reads); sched_barrier keeps the
+  // compiler from sinking the loads below the MFMAs.
+  DKV_K2_ISSUE_A(0, af0);
   DKV_K2_ISSUE_B(0);
-  DKV_K2_ISSUE_A(1, a10, a11, a12, a13);
-  DKV_K2_FINISH(0, a00, a01, a02, a03);
+  DKV_K2_FINISH(0);
   for (int g = 0; g < G; g += 2) {  // G is a multiple of 4 (rank is a multiple of 256)
-    const int g2 = min(g + 2, G - 1), g3 = min(g + 3, G - 1);
-    // sched_barrier keeps the compiler from sinking the loads below the MFMAs
-    // (which would expose their latency) or hoisting the stores above them.
+    const int g2 = min(g + 2, G - 1);
     __syncthreads();
     DKV_K2_ISSUE_B(g + 1);
-    DKV_K2_ISSUE_A(g2, a00, a01, a02, a03);
+    DKV_K2_ISSUE_A(g + 1, af1);
     __builtin_amdgcn_sched_barrier(0);
-    DKV_K2_MFMA(0);
+    DKV_K2_MFMA(0, af0);
     __builtin_amdgcn_sched_barrier(0);
-    DKV_K2_FINISH(1, a10, a11, a12, a13);
+    DKV_K2_FINISH(1);
     __syncthreads();
     DKV_K2_ISSUE_B(g2);
-    DKV_K2_ISSUE_A(g3, a10, a11, a12, a13);
+    DKV_K2_ISSUE_A(g2, af0);
     __builtin_amdgcn_sched_barrier(0);
-    DKV_K2_MFMA(1);
+    DKV_K2_MFMA(1, af1);
     __builtin_amdgcn_sched_barrier(0);
-    DKV_K2_FINISH(0, a00, a01, a02, a03);
+    DKV_K2_FINISH(0);
   }
 #undef DKV_K2_ISSUE_A
 #undef DKV_K2_ISSUE_B
@@ -548,13 +557,13 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 }
 
 struct K3aArgs {
-  const uint8_t* vcodes;  // decoded value codes, u8 [G][64][n_pad] (token-contiguous per component)
+  const uint8_t* vcodes;  // decoded value codes, u8 [G][64][n_slots] (slot-contiguous per component)
   const float2* vaff;     // (scale, offset) per (group, token): value = code * scale + offset
   const int32_t* cu_seqlens;
   const float* scores;
   const float* tile_max;
   float* w_part;
-  int batch, R_total, n_total, n_pad, ntiles, G, rank, nsplits, row_blocks;
+  int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
 };
 
 // Max over a sequence's tiles of one row, 8 lanes per row (all loads of a lane issued together).
@@ -577,21 +586,24 @@ DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, 
 
 // ---------------------------------------------------------------------------
 // K1 for the value side: every token's value codes (all hot planes) as 8-bit
-// codes, transposed to [G][64][n_pad] so that an MFMA operand (one component,
-// 8 consecutive tokens) is one 8-byte load, plus the per-(group, token) affine
-// form (scale = span / 256, offset = low + span * 2^-(m+1); 0 and 0 for a
-// group without planes).  One block = 128 tokens x one group.
+// codes, transposed to [G][64][n_slots] so that an MFMA operand (one
+// component, 8 consecutive slots) is one 8-byte load, plus the per-(group,
+// slot) affine form (scale = span / 256, offset = low + span * 2^-(m+1); 0 and
+// 0 for a group without planes or a padding slot).  One block = 128 slots x
+// one group.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
-  __shared__ uint32_t tile[64][kDecodeTok / 4 + 1];  // [component][token / 4], bytes of 4 tokens per word
-  const int2 bg = decode_block(a.G, (a.n_pad / kDecodeTok) * a.G);
-  const int tb = bg.x, g = bg.y;
-  if (tb >= a.n_pad / kDecodeTok) return;
+  __shared__ uint32_t tile[64][kDecodeTok / 4 + 1];  // [component][slot / 4], bytes of 4 slots per word
+  const int nsb = a.n_slots / kDecodeTok;
+  const int2 bg = decode_block(a.G, nsb * a.G);
+  const int sb = bg.x, g = bg.y;
+  if (sb >= nsb) return;
   const int tl = threadIdx.x >> 1, half = threadIdx.x & 1;
-  const int t = tb * kDecodeTok + tl;
+  const int slot = sb * kDecodeTok + tl;
+  const int t = slot_token(a, slot);
   uint32_t cw[8];
   float2 aff = make_float2(0.0f, 0.0f);
-  if (t < a.n_total) {
+  if (t >= 0) {
     const int G = a.G;
     const int kp = a.s.pieces[t];
     const int m = a.s.order.planes[(long)kp * G + g];
@@ -612,7 +624,7 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArg
 #pragma unroll
     for (int w = 0; w < 8; ++w) cw[w] = 0u;
   }
-  if (half == 0) vaff[(long)g * a.n_pad + t] = aff;
+  if (half == 0) vaff[(long)g * a.n_slots + slot] = aff;
   // byte i of cw[w] is component half*32 + 4w + i of token t
   uint8_t* tb8 = (uint8_t*)&tile[0][0];
   constexpr int ROWB = (kDecodeTok / 4 + 1) * 4;
@@ -633,7 +645,7 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArg
   v2.y = tile[c][q * 8 + 5];
   v2.z = tile[c][q * 8 + 6];
   v2.w = tile[c][q * 8 + 7];
-  uint4* dst = (uint4*)(vcodes + ((long)g * 64 + c) * a.n_pad + tb * kDecodeTok + q * 32);
+  uint4* dst = (uint4*)(vcodes + ((long)g * 64 + c) * a.n_slots + sb * kDecodeTok + q * 32);
   dst[0] = v;
   dst[1] = v2;
 }
@@ -690,8 +702,9 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
+  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+  const long slot0 = (long)(tb0 + bs.y * (kSplitTok / kTileTok)) * kTileTok;  // first slot of the split
   if (tid < 256) {
-    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
     const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
     const int r = rbk * 32 + (tid >> 3);
     const float m = rows_max8(a.tile_max, a.ntiles, tb0, ntb, r, r < a.R_total, tid & 7);
@@ -711,13 +724,13 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 
   const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
   const float* srow = a.scores + (long)(row_ok ? my_row : 0) * a.n_total + tok0;
-  const float2* aff = a.vaff + (long)g * a.n_pad + tok0;
-  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_pad + tok0;
-  const uint8_t* col1 = col0 + 32L * a.n_pad;
+  const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
+  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_slots + slot0;
+  const uint8_t* col1 = col0 + 32L * a.n_slots;
 
-  // Branch-free steps: every load stays inside the padded buffers (n_pad reaches a
-  // whole split past n_total; the scores row is read at a clamped index), and
-  // tokens past the split's end get p = 0.
+  // Branch-free steps: every load stays inside the slot buffers (they extend a
+  // whole split past the last tile; the scores row is read at a clamped
+  // index), and slots past the split's tokens get p = 0.
   constexpr int STEPS = kK3WaveTok / 16;  // 8
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
@@ -1004,7 +1017,7 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
 // Workspace layout and argument checks.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int ntiles, nsplits, R_total, nchunks, n_total, n_pad;
+  int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
   size_t coef, vcodes, vaff, scores, tile_max, tile_sum, w_part, out_part, total;
 };
 
@@ -1012,8 +1025,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
 // [split partials][chunk partials].
-// The coefficient area holds every token's keys decoded to fp16 [G][n_pad][64]; n_pad covers the
-// rows a last K2 tile (255) or K3a split (1023) may read past n_total; they decode to zeros.
+// The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
   L.ntiles = 0;
@@ -1024,16 +1036,16 @@ Layout make_layout(const dkv_attend_args_t* a) {
     L.nsplits += (len + kSplitTok - 1) / kSplitTok;
   }
   L.n_total = a->cu_seqlens_host[a->batch];
-  L.n_pad = (L.n_total + kSplitTok + kDecodeTok - 1) / kDecodeTok * kDecodeTok;
+  L.n_slots = L.ntiles * kTileTok + kSplitTok;
   L.R_total = a->q_heads * a->q_len;
   L.nchunks = a->rank / kChunk;
   size_t off = 0;
   L.coef = off;
-  off += align256((size_t)L.n_pad * a->rank * 2);
+  off += align256((size_t)L.n_slots * a->rank * 2);
   L.vcodes = off;
-  off += align256((size_t)L.n_pad * a->rank);
+  off += align256((size_t)L.n_slots * a->rank);
   L.vaff = off;
-  off += align256((size_t)L.n_pad * (a->rank / 64) * 8);
+  off += align256((size_t)L.n_slots * (a->rank / 64) * 8);
   L.scores = off;
   off += align256((size_t)L.R_total * L.n_total * 4);
   L.tile_max = off;
@@ -1077,7 +1089,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   if (L.ntiles == 0) return DKV_OK;
   K2Args k{};
   k.coef = (const uint16_t*)(ws + L.coef);
-  k.n_pad = L.n_pad;
+  k.n_slots = L.n_slots;
   k.cu_seqlens = a->cu_seqlens;
   k.positions = a->positions;
   k.key_basis = a->key_basis;
@@ -1127,12 +1139,14 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
               "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.total);
   DecodeArgs d{};
   d.s = a->key;
+  d.cu_seqlens = a->cu_seqlens;
   d.coef = (uint16_t*)((char*)workspace + L.coef);
-  d.n_total = L.n_total;
-  d.n_pad = L.n_pad;
+  d.batch = a->batch;
+  d.ntiles = L.ntiles;
+  d.n_slots = L.n_slots;
   d.G = a->key.order.groups;
   d.plane_cap = plane_cap;
-  const dim3 grid((unsigned)(((long)d.G * (L.n_pad / kDecodeTok) + 7) / 8 * 8));
+  const dim3 grid((unsigned)(((long)d.G * (L.n_slots / kDecodeTok) + 7) / 8 * 8));
   hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), d);
   rc = dkv::check_launch("decode_keys");
   if (rc || !a->value.blob) return rc;
@@ -1200,7 +1214,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.batch = a->batch;
     k.R_total = L.R_total;
     k.n_total = L.n_total;
-    k.n_pad = L.n_pad;
+    k.n_slots = L.n_slots;
     k.ntiles = L.ntiles;
     k.G = G;
     k.rank = a->rank;
