@@ -81,7 +81,7 @@ class CompressedContext:
         self.batch = self.cu_host.numel() - 1
         self.exact_cache = exact_cache
         self._workspace = None
-        self._prepared = None  # (plane_cap, key stream version) decoded into the workspace
+        self._prepared = None  # (plane_cap, stream versions) decoded into the workspace
         self._score_workspace = None
         self._score_prepared = None
         self._cu_exact = {}
@@ -152,13 +152,13 @@ class CompressedContext:
     def prepare(self, args, plane_cap: int = 8) -> None:
         """K1: decode the key codes into the workspace (once per decode step; the layers reuse it)."""
         dkv_hip.attend_prepare(args, self.workspace(args), plane_cap)
-        self._prepared = (plane_cap, self.key.version)
+        self._prepared = (plane_cap, self.key.version, self.value.version)
 
     def run_layer(self, args) -> None:
         """One layer through the C ABI; the key codes are decoded again at layer 0 (the start of
         every forward) and whenever the key stream changed since the last decode."""
         workspace = self.workspace(args)
-        if args.layer == 0 or self._prepared != (8, self.key.version):
+        if args.layer == 0 or self._prepared != (8, self.key.version, self.value.version):
             self.prepare(args)
         dkv_hip.attend_layer(args, workspace)
 

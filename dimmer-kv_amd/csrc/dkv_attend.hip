@@ -1135,8 +1135,10 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   DKV_REQUIRE(plane_cap >= 0 && plane_cap <= 8, DKV_EINVAL, "dkv_attend_prepare: plane_cap %d not in 0..8",
               plane_cap);
   const Layout L = make_layout(a);
-  DKV_REQUIRE(workspace && workspace_bytes >= L.total, DKV_EWORKSPACE,
-              "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.total);
+  // only the decoded areas at the head of the workspace are written, so an attend or a score
+  // workspace (both start with them) will do
+  DKV_REQUIRE(workspace && workspace_bytes >= L.scores, DKV_EWORKSPACE,
+              "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.scores);
   DecodeArgs d{};
   d.s = a->key;
   d.cu_seqlens = a->cu_seqlens;

@@ -210,14 +210,16 @@ def budget_per_stream(shape: ModelShape, tokens: int, sinks: int, recent: int, b
 
 def make_context(shape: ModelShape, tokens: int, seed: int, sinks: int = 4, recent: int = 32,
                  budget: float | None = None, zero_frac: float = 0.05, floor: int = 2, p: float | None = None,
-                 mean_scale: float = 0.01, device="cpu", basis=None) -> SyntheticContext:
+                 mean_scale: float = 0.01, device="cpu", basis=None, mean=None) -> SyntheticContext:
+    """``basis`` / ``mean`` (dicts by stream) let several conversations share one model's tables."""
     middle = max(0, tokens - min(sinks, tokens) - recent)
     stream_budget = None if budget is None else budget_per_stream(shape, tokens, sinks, recent, budget)
     if basis is None:
         basis = {"key": orthonormal_basis(shape.features, shape.rank, seed + 1, device),
                  "value": orthonormal_basis(shape.features, shape.rank, seed + 2, device)}
-    g = _gen(seed + 3)
-    mean = {kind: (torch.randn(shape.features, generator=g) * mean_scale).to(device) for kind in ("key", "value")}
+    if mean is None:
+        g = _gen(seed + 3)
+        mean = {kind: (torch.randn(shape.features, generator=g) * mean_scale).to(device) for kind in ("key", "value")}
     coef = {"key": coefficients(middle, shape.rank, seed + 4, device),
             "value": coefficients(middle, shape.rank, seed + 5, device)}
     planes = {"key": plane_counts(middle, shape.groups, seed + 6, zero_frac, floor, p, stream_budget),

@@ -42,9 +42,10 @@ class Case:
 
 
 def build_case(shape: synth.ModelShape, tokens: int, seed: int, budget=None, zero_frac=0.05, p=None,
-               query_scale=1.0, q_len=1, query_dtype=torch.float32, sinks=4, recent=32, mean_scale=0.01) -> Case:
+               query_scale=1.0, q_len=1, query_dtype=torch.float32, sinks=4, recent=32, mean_scale=0.01,
+               basis=None, mean=None, rope_rows=None) -> Case:
     ctx = synth.make_context(shape, tokens, seed, sinks=sinks, recent=recent, budget=budget, zero_frac=zero_frac,
-                             p=p, mean_scale=mean_scale)
+                             p=p, mean_scale=mean_scale, basis=basis, mean=mean)
     order = pr.plane_major_order(shape.groups)
     codes, low, span, pieces, coef_hot = {}, {}, {}, {}, {}
     for kind in ("key", "value"):
@@ -52,7 +53,7 @@ def build_case(shape: synth.ModelShape, tokens: int, seed: int, budget=None, zer
         codes[kind], low[kind], span[kind] = c, lo, sp
         pieces[kind] = ctx.pieces(kind)
         coef_hot[kind] = pr.dequantize(c, lo, sp, pr.token_planes(order, pieces[kind]))
-    cos, sin = synth.rope_tables(shape, tokens + q_len, "cpu")
+    cos, sin = synth.rope_tables(shape, rope_rows or tokens + q_len, "cpu")
     positions = np.arange(ctx.start, ctx.end)
     new_coef = {kind: synth.coefficients(q_len, shape.rank, seed + 50 + i) for i, kind in enumerate(("key", "value"))}
     exact_coef = {kind: torch.cat([ctx.exact_coef[kind], new_coef[kind]]) for kind in ("key", "value")}

@@ -1,0 +1,114 @@
+"""Host-side logic of the Python mirrors (CPU): method-name parsing and its errors
+(scripts/methods.py:100-108, 192-213, 227-236), checkpoint/model checks
+(scripts/methods.py:134-137, scripts/progressive.py:119-120), the synthetic
+checkpoints' consistency with the oracle, and the kvtc compress path (torch,
+CPU) against the oracle's quantizer and allocator."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import synth
+from oracle import kvtc_ref
+from oracle import progressive_ref as pr
+
+
+def test_budget_of():
+    import methods
+
+    assert methods.budget_of("full") == 1.0
+    assert methods.budget_of("prog@0.03:r0.01") == 0.03
+    assert methods.budget_of("dkvtc@0.02:snap:floor1") == 0.02
+    assert methods.budget_of("dkv:0.15:flat") == 0.15
+    assert np.isnan(methods.budget_of("pca16/lex8"))
+
+
+def _small():
+    shape = synth.ModelShape(2, 2, 64, 4, 256)
+    ctx = synth.make_context(shape, 400, seed=3)
+    return shape, ctx
+
+
+def test_method_errors_follow_reference():
+    import methods
+
+    shape, ctx = _small()
+    m = methods.Methods("synthetic/llama-3.2", device="cpu", model=synth.RopeModel(shape),
+                        kvtc=synth.kvtc_checkpoint(ctx), progressive=synth.order_checkpoint(shape))
+    keys, values = synth.prefill_cache(ctx, dtype=torch.float32)
+    with pytest.raises(ValueError, match="not served"):
+        m.apply("h2o:0.1", keys, values, {})
+    with pytest.raises(ValueError, match="Unknown option"):
+        m.apply("dkvtc@0.1:bogus", keys, values, {})
+    with pytest.raises(ValueError, match="Unknown option"):
+        m.apply("prog@0.1:zz", keys, values, {})
+    with pytest.raises(ValueError, match="Unknown option"):
+        m.apply("kvtc@0.1:ev", keys, values, {})  # :ev only with dkvtc (scripts/methods.py:200)
+    other = methods.Methods("another/model", device="cpu", model=synth.RopeModel(shape),
+                            kvtc=synth.kvtc_checkpoint(ctx), progressive=synth.order_checkpoint(shape))
+    with pytest.raises(RuntimeError, match="was fit for"):
+        other.codec("kvtc")
+    nomodel = methods.Methods("synthetic/llama-3.2", device="cpu", kvtc=synth.kvtc_checkpoint(ctx))
+    with pytest.raises(ValueError, match="model=model"):
+        nomodel.codec("kvtc")
+
+
+def test_progressive_order_mismatch_raises():
+    import progressive
+
+    shape, ctx = _small()
+    order = synth.order_checkpoint(shape, model_id="other")
+    with pytest.raises(RuntimeError, match="was fit for other"):
+        progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), order, "cpu", synth.RopeModel(shape))
+
+
+def test_synthetic_checkpoints_match_oracle_tables():
+    shape, ctx = _small()
+    order = synth.order_checkpoint(shape)["key"]
+    ref = pr.plane_major_order(shape.groups)
+    assert np.array_equal(order["planes"].numpy(), ref.planes)
+    assert np.array_equal(order["prefix_bytes"].numpy().astype(np.int64), ref.prefix_bytes)
+    assert order["rungs"] == ref.rungs
+    ck = synth.kvtc_checkpoint(ctx)
+    for bits, size in zip(ck["key"]["rungs"], ck["key"]["rung_bytes"]):
+        assert size == kvtc_ref.rung_bytes(bits.numpy(), 64)
+
+
+@pytest.mark.parametrize("name", ["kvtc@0.3", "kvtcf@0.3", "dkvtc@0.3:floor1", "dkvtc@0.3:snap:floor1", "dkvtc@0.2:ev"])
+def test_kvtc_methods_on_cpu(name):
+    """The kvtc family runs the reference's torch arithmetic (CPU here): rebuilt caches equal the
+    oracle's quantize-dequantize of the chosen rungs, the budget holds, and exact tokens stay exact."""
+    import kvtc
+    import methods
+
+    shape, ctx = _small()
+    model = synth.RopeModel(shape)
+    m = methods.Methods("synthetic/llama-3.2", device="cpu", model=model, kvtc=synth.kvtc_checkpoint(ctx))
+    keys, values = synth.prefill_cache(ctx, dtype=torch.float32)
+    tokens = keys[0].shape[2]
+    scores = {"snap": [torch.rand(shape.kv_heads, tokens, generator=torch.Generator().manual_seed(l))
+                       for l in range(shape.layers)]}
+    out = m.apply(name, keys, values, scores)
+    codec = m.codec("kvtc")
+    budget = methods.budget_of(name)
+    assert out.used_bytes <= int(budget * tokens * 2 * codec.exact_bytes)
+    start, end = codec.last_span
+    for layer in range(shape.layers):
+        assert torch.equal(out.keys[layer][..., :start, :], keys[layer][..., :start, :])
+        assert torch.equal(out.values[layer][..., end:, :], values[layer][..., end:, :])
+    cos, sin = kvtc.rope_tables(model, tokens, "cpu")
+    matrix = codec.to_matrix(values, "value", cos, sin)
+    stream = codec.streams["value"]
+    coef = ((matrix[start:end] - stream.mean) @ stream.basis).numpy()
+    choice = codec.last_choice["value"].numpy()
+    exact_rung = len(stream.rung_bytes)
+    for r in np.unique(choice):
+        rows = choice == r
+        if r < 0:
+            continue
+        want = coef[rows] if r == exact_rung else kvtc_ref.quantize_groups(coef[rows], stream.rungs[r].numpy(), 64)
+        got = codec.last_coefficients["value"][torch.from_numpy(rows)].numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"rung {r}"
+    assert out.token_bytes.shape == (tokens,)
