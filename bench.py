@@ -111,6 +111,36 @@ def cpu_baseline(w, seconds: float):
                       f"scaled x{s.layers}"}
 
 
+def question_stage(w):
+    """The question before the decode (the configuration's first three steps): score the hot tier
+    with 64 query tokens using the first 2 planes (28 layers), select the top 1 %, gather their
+    cold planes.  Scoring and selection are timed over 3 repetitions after one warm-up; the gather
+    runs once (it changes the cache the decode then reads)."""
+    import torch
+
+    q = w.question
+    q.score()
+    q.select()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    reps = 3
+    ev[0].record()
+    for _ in range(reps):
+        q.score()
+    ev[1].record()
+    for _ in range(reps):
+        q.select()
+    ev[2].record()
+    fetched = q.gather()
+    ev[3].record()
+    torch.cuda.synchronize()
+    out = {"query_tokens": int(q.queries.shape[3]), "plane_cap": q.plane_cap, "selected": q.count,
+           "score_ms": round(ev[0].elapsed_time(ev[1]) / reps, 3), "topk_ms": round(ev[1].elapsed_time(ev[2]) / reps, 3),
+           "gather_ms": round(ev[2].elapsed_time(ev[3]), 3), "fetched_bytes": fetched}
+    print(f"[bench] question: {out}", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -130,11 +160,13 @@ def main():
     if args.config == "cfg3":
         w = workloads.build_ragged(device=dev)
     else:
-        w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline)
+        w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline,
+                                   refine_fraction=0.01 if args.config == "cfg2" else 0.0)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
     print(f"[bench] built {args.config} in {build_s:.1f}s: {w.middle_total} compressed tokens, "
           f"{w.hot_code_bytes() / 2**20:.1f} MiB hot codes", file=sys.stderr, flush=True)
+    question = question_stage(w) if hasattr(w, "question") else None
 
     for _ in range(args.warmup):
         w.step_split()
@@ -210,6 +242,8 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if question is not None:
+        result["question"] = question
     if not args.no_cpu_baseline and args.config != "cfg3":
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)

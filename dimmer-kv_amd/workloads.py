@@ -91,31 +91,85 @@ class DecodeWorkload:
         return self.context.key.n
 
 
-def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device) -> dict:
+class QuestionStage:
+    """Question-time work of the progressive entry point (scripts/methods.py:244-248): score the
+    hot tier with the question's query tokens using each group's first ``plane_cap`` planes, pick
+    the top ``fraction`` of the compressed tokens, fetch their cold planes."""
+
+    def __init__(self, w, queries, key_exact, key_question, fraction, plane_cap=2):
+        self.w, self.queries, self.key_exact, self.key_question = w, queries, key_exact, key_question
+        self.fraction, self.plane_cap = fraction, plane_cap
+        self.count = max(1, int(round(fraction * w.context.key.n)))
+        self.idx = torch.empty(self.count, dtype=torch.int32, device=queries.device)
+        self.args = []
+        s = w.shape
+        scratch = torch.empty(1, queries.shape[3], s.q_heads, s.head_dim, dtype=queries.dtype, device=queries.device)
+        for layer in range(s.layers):
+            self.args.append(w.context.layer_args(layer, queries[layer], scratch, key_exact[layer], key_exact[layer],
+                                                  None, (key_exact.shape[2],)))
+        self._scratch = scratch
+        self.workspace = torch.zeros(dkv_hip.score_workspace_bytes(self.args[0]), dtype=torch.uint8,
+                                     device=queries.device)
+        self.importance = torch.empty(w.context.key.n, dtype=torch.float32, device=queries.device)
+
+    @classmethod
+    def build(cls, w, ctx, seed, fraction, q_len=64):
+        s = w.shape
+        device = w.queries.device
+        queries = synth.make_queries(s, q_len, seed, device, torch.bfloat16)
+        g = torch.Generator("cpu").manual_seed(seed + 1)
+        key_question = (torch.randn(s.layers, s.kv_heads, q_len, s.head_dim, generator=g) * 0.5).to(device)
+        e_ctx = w.key_exact.shape[2] - w.q_len  # context exact tokens (sinks + recent)
+        key_exact = w.key_exact[:, :, :e_ctx].contiguous()
+        return cls(w, queries, key_exact, key_question.contiguous(), fraction)
+
+    def score(self) -> torch.Tensor:
+        """K1 (first plane_cap planes) + K4a over every layer -> importance [n]."""
+        dkv_hip.score_begin(self.importance)
+        dkv_hip.attend_prepare(self.args[0], self.workspace, self.plane_cap)
+        for layer, a in enumerate(self.args):
+            dkv_hip.score_layer(a, self.key_question[layer], self.importance, self.workspace)
+        return self.importance
+
+    def select(self) -> torch.Tensor:
+        dkv_hip.topk(self.importance, self.count, self.idx)
+        return self.idx
+
+    def gather(self) -> int:
+        """K4c on both streams; returns the bytes fetched (progressive.py:232)."""
+        rows = self.idx.long()
+        return sum(self.w.streams[k].refine(rows) for k in ("key", "value"))
+
+
+def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, refine_capacity: int = 0) -> dict:
     order = plane_major_order(shape.groups)
     otab = OrderTables(order.planes, order.prefix_bytes, device)
     streams = {}
     for kind in ("key", "value"):
         codes, low, span = quantize8(coefs[kind].to(device), 64)
         pieces = torch.from_numpy(planes[kind] * shape.groups).to(device)
-        streams[kind] = PackedStream.pack(codes, low, span, pieces, otab, refine_capacity=0, with_cold=False)
+        streams[kind] = PackedStream.pack(codes, low, span, pieces, otab, refine_capacity=refine_capacity,
+                                          with_cold=refine_capacity > 0)
         del codes, low, span
     return streams
 
 
 def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
                  shape: synth.ModelShape | None = None, tokens: int | None = None, budget: float | None = None,
-                 query_dtype: torch.dtype | None = None, keep_host_basis: bool = False) -> DecodeWorkload:
+                 query_dtype: torch.dtype | None = None, keep_host_basis: bool = False,
+                 refine_fraction: float = 0.0) -> DecodeWorkload:
     """A single-conversation decode workload (configs 0-2).  ``keep_host_basis`` keeps float32
-    host copies of the bases (for the CPU baseline)."""
+    host copies of the bases (for the CPU baseline); ``refine_fraction`` > 0 keeps a cold tier
+    and room to refine that fraction of the tokens (the question stage)."""
     if name in CONFIGS:
         s0, t0, b0, qd0 = CONFIGS[name]
         shape, tokens = shape or s0, tokens or t0
         budget = b0 if budget is None else budget
         query_dtype = query_dtype or qd0
     ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device)
-    streams = _pack_streams(ctx.coef, ctx.planes, shape, device)
-    cos, sin = synth.rope_tables(shape, tokens + q_len, device)
+    capacity = int(round(refine_fraction * ctx.middle)) + 1 if refine_fraction > 0 else 0
+    streams = _pack_streams(ctx.coef, ctx.planes, shape, device, capacity)
+    cos, sin = synth.rope_tables(shape, tokens + max(q_len, 64), device)
     tables = ModelTables(ctx.basis["key"], ctx.basis["value"], ctx.mean["key"], ctx.mean["value"], shape.layers,
                          shape.kv_heads, shape.head_dim, cos, sin)
     positions = torch.arange(ctx.start, ctx.end, dtype=torch.int32)
@@ -136,6 +190,8 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
     w.workspace = context.workspace(w.args[0])
     if keep_host_basis:
         w.synthetic_basis_host = {k: v.cpu().numpy() for k, v in ctx.basis.items()}
+    if refine_fraction > 0:
+        w.question = QuestionStage.build(w, ctx, seed + 70, refine_fraction)
     # drop the float32 device bases now that the fp16 kernel layouts exist
     ctx.basis.clear()
     w.synthetic = ctx
