@@ -41,11 +41,19 @@ struct K2Args {
   const float* rope_sin;
   const void* query;
   float* scores;
+  uint16_t* probs;  // fp16 exp(score - tile max), [R][n_slots]; NULL when only scores are needed
   float* tile_max;
   float* tile_sum;
   float scaling;
   int batch, layer, Hkv, Hq, q_len, G, n_total, n_slots, ntiles, total_wg, per_xcd, query_dtype;
 };
+
+DKV_DEVICE uint16_t f16_bits(float v) {
+  half_t h = (half_t)v;
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
 
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
 
@@ -230,6 +238,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
     }
   }
   // combine the two dimension halves (lanes l32 and l32 + 32), write scores, tile statistics
+  float xs[HPWAVE][kSmallRows][2];
 #pragma unroll
   for (int hw = 0; hw < HPWAVE; ++hw) {
     const int hl = hs * HPWAVE + hw;
@@ -243,6 +252,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
         const float full = part[hw][r][tb] + __shfl_xor(part[hw][r][tb], 32, 64);
         const int n = tq * 64 + tb * 32 + l32;
         x[tb] = n < count ? full * a.scaling : -INFINITY;
+        xs[hw][r][tb] = x[tb];
         if (tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
       float mx = fmaxf(x[0], x[1]);
@@ -276,6 +286,24 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       const long o = (long)((h0 + hl) * RH + r) * a.ntiles + tile;
       a.tile_max[o] = M;
       a.tile_sum[o] = S;
+    }
+  }
+  // probabilities relative to the tile maximum, fp16, for the value side; every slot of the
+  // tile is written (0 past the tile's tokens)
+  if (!a.probs) return;
+#pragma unroll
+  for (int hw = 0; hw < HPWAVE; ++hw) {
+    const int hl = hs * HPWAVE + hw;
+#pragma unroll
+    for (int r = 0; r < kSmallRows; ++r) {
+      if (r >= RH) break;
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][r]);
+      const float x = xs[hw][r][lhi];
+      const float p = (x == -INFINITY) ? 0.0f : __expf(x - M);
+      const int n = tq * 64 + lhi * 32 + l32;
+      a.probs[(long)((h0 + hl) * RH + r) * a.n_slots + (long)tile * kTileTok + n] = f16_bits(p);
     }
   }
 }
@@ -542,6 +570,19 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         a.tile_sum[o] = S;
       }
     }
+    // probabilities relative to the tile maximum (fp16) for this block of rows, from the
+    // scores this workgroup wrote above (visible to it after the barrier); 0 past the tokens
+    for (int e = a.probs ? tid : HPW * 32 * kTileTok; e < HPW * 32 * kTileTok; e += kK2Threads) {
+      const int hl = e / (32 * kTileTok), rr = (e / kTileTok) % 32, n = e % kTileTok;
+      const int row = mb * 32 + rr;
+      if (row >= RH) continue;
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
+      const long r_all = (long)(h0 + hl) * RH + row;
+      const float x = n < count ? a.scores[r_all * a.n_total + tok0 + n] : -INFINITY;
+      a.probs[r_all * a.n_slots + (long)tile * kTileTok + n] = f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
+    }
     __syncthreads();
   }
 
@@ -560,7 +601,7 @@ struct K3aArgs {
   const uint8_t* vcodes;  // decoded value codes, u8 [G][64][n_slots] (slot-contiguous per component)
   const float2* vaff;     // (scale, offset) per (group, token): value = code * scale + offset
   const int32_t* cu_seqlens;
-  const float* scores;
+  const uint16_t* probs;  // fp16 exp(score - tile max), [R][n_slots]
   const float* tile_max;
   float* w_part;
   int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
@@ -723,43 +764,41 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   float osum = 0.0f;
 
   const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
-  const float* srow = a.scores + (long)(row_ok ? my_row : 0) * a.n_total + tok0;
+  // K2 left p~ = exp(s - tile max) in fp16; the wave's 128 tokens lie in one tile, whose
+  // factor f = exp(tile max - row max) turns p~ into p = exp(s - row max).
+  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
+  float f = 0.0f;
+  if (row_ok && wt0 < count) {
+    const float mt = a.tile_max[(long)my_row * a.ntiles + tile];
+    f = (mt == -INFINITY) ? 0.0f : __expf(mt - my_M);
+  }
+  const uint16_t* prow = a.probs + (long)(row_ok ? my_row : 0) * a.n_slots + slot0;
   const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
   const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_slots + slot0;
   const uint8_t* col1 = col0 + 32L * a.n_slots;
 
   // Branch-free steps: every load stays inside the slot buffers (they extend a
-  // whole split past the last tile; the scores row is read at a clamped
-  // index), and slots past the split's tokens get p = 0.
+  // whole split past the last tile), and slots past the split's tokens get p = 0
+  // by selection (whatever those slots hold).
   constexpr int STEPS = kK3WaveTok / 16;  // 8
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
     const int t8 = wt0 + st * 16 + lhi * 8;  // this lane's 8 tokens: t8 .. t8+7 (split-relative)
-    float sc[8];
-    if (row_ok && t8 + 8 <= count) {
-      const float4 s0 = *(const float4*)(srow + t8);
-      const float4 s1 = *(const float4*)(srow + t8 + 4);
-      sc[0] = s0.x; sc[1] = s0.y; sc[2] = s0.z; sc[3] = s0.w;
-      sc[4] = s1.x; sc[5] = s1.y; sc[6] = s1.z; sc[7] = s1.w;
-    } else {
+    const half8 pt = *(const half8*)(prow + t8);
+    float4 afv[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool ok = row_ok && t8 + e < count;
-        const float v = srow[ok ? t8 + e : 0];
-        sc[e] = ok ? v : -INFINITY;
-      }
-    }
-    float2 af[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) af[e] = aff[t8 + e];
+    for (int e = 0; e < 4; ++e) afv[e] = *(const float4*)(aff + t8 + 2 * e);
     const uint2 c0 = *(const uint2*)(col0 + t8);
     const uint2 c1 = *(const uint2*)(col1 + t8);
     half8 pa;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = sc[e] == -INFINITY ? 0.0f : __expf(sc[e] - my_M);
-      pa[e] = (half_t)(p * af[e].x);
-      osum += p * af[e].y;
+      const bool ok = t8 + e < count;
+      const float p = (float)pt[e] * f;
+      const float sc = (e & 1) ? afv[e >> 1].z : afv[e >> 1].x;
+      const float of = (e & 1) ? afv[e >> 1].w : afv[e >> 1].y;
+      pa[e] = ok ? (half_t)(p * sc) : (half_t)0.0f;
+      osum += ok ? p * of : 0.0f;
     }
     acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0.x, c0.y), acc[0], 0, 0, 0);
     acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1.x, c1.y), acc[1], 0, 0, 0);
@@ -1018,7 +1057,7 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
-  size_t coef, vcodes, vaff, scores, tile_max, tile_sum, w_part, out_part, total;
+  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1048,6 +1087,8 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)L.n_slots * (a->rank / 64) * 8);
   L.scores = off;
   off += align256((size_t)L.R_total * L.n_total * 4);
+  L.probs = off;
+  off += align256((size_t)L.R_total * L.n_slots * 2);
   L.tile_max = off;
   off += align256((size_t)L.R_total * L.ntiles * 4);
   L.tile_sum = off;
@@ -1085,7 +1126,7 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
   return DKV_OK;
 }
 
-int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st) {
+int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st, bool probs = true) {
   if (L.ntiles == 0) return DKV_OK;
   K2Args k{};
   k.coef = (const uint16_t*)(ws + L.coef);
@@ -1098,6 +1139,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.rope_sin = a->rope_sin;
   k.query = a->query;
   k.scores = (float*)(ws + L.scores);
+  k.probs = probs ? (uint16_t*)(ws + L.probs) : nullptr;
   k.tile_max = (float*)(ws + L.tile_max);
   k.tile_sum = (float*)(ws + L.tile_sum);
   k.scaling = a->scaling;
@@ -1210,7 +1252,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.vcodes = (const uint8_t*)(ws + L.vcodes);
     k.vaff = (const float2*)(ws + L.vaff);
     k.cu_seqlens = a->cu_seqlens;
-    k.scores = (const float*)(ws + L.scores);
+    k.probs = (const uint16_t*)(ws + L.probs);
     k.tile_max = (const float*)(ws + L.tile_max);
     k.w_part = (float*)(ws + L.w_part);
     k.batch = a->batch;
@@ -1551,7 +1593,7 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
               "dkv_score_layer: workspace %zu B < required %zu B", workspace_bytes, S.total);
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
-  rc = launch_keys_scores(a, S.base, ws, st);
+  rc = launch_keys_scores(a, S.base, ws, st, /*probs=*/false);
   if (rc) return rc;
   ExactStatsArgs e{};
   e.query = a->query;

@@ -126,9 +126,12 @@ class PackedStream:
         return int((self.tables.full_bytes - self.tables.prefix64[self.pieces.long()]).sum())
 
     def refine(self, rows: torch.Tensor) -> int:
-        """K4c: fetch the cold pieces of ``rows`` (stream-local, unique) -> bytes fetched (progressive.py:232)."""
-        rows = rows.to(device=self.blob.device, dtype=torch.int64)
-        rows = rows[self.pieces[rows].long() < self.tables.pieces].to(torch.int32).contiguous()
+        """K4c: fetch the cold pieces of ``rows`` (stream-local, unique) -> bytes fetched (progressive.py:232).
+
+        Rows already at full precision cost nothing (their cold blob is empty) and are merged like
+        the others, so no host-side filtering is needed; the fetched count is the only value read
+        back."""
+        rows = rows.to(device=self.blob.device, dtype=torch.int32).contiguous()
         k = rows.numel()
         if k == 0:
             return 0
@@ -136,10 +139,10 @@ class PackedStream:
             raise ValueError("this stream was packed without a cold tier")
         if self.refined + k > self.refine_capacity:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
-        fetched = int((self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum())
+        fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
         base = self.hot_used + self.refined * self.tables.full_bytes
         dkv_hip.gather_cold(self.c_stream(), self.cold, self.cold_off, rows, base, self.blob, self.tok_off,
                             self.pieces)
         self.refined += k
         self.version += 1
-        return fetched
+        return int(fetched)
