@@ -66,6 +66,22 @@ class DecodeWorkload:
                 ends[i].record()
             dkv_hip.attend_values(a, self.workspace)
 
+    def capture(self):
+        """Record one decode step (K1 decode + every layer) in a HIP graph; replaying it removes the
+        per-launch host overhead.  The step allocates nothing and records no memset."""
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            self.step()  # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.step()
+        torch.cuda.synchronize()
+        self.graph = graph
+        return graph
+
     # ---- algorithmic work of one decode step (all layers) ----
     def hot_code_bytes(self) -> int:
         return sum(int(s.tables.prefix64[s.pieces.long()].sum()) for s in self.streams.values())
