@@ -40,6 +40,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", default="cfg2", choices=["cfg0", "cfg1", "cfg2", "cfg3"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-question", action="store_true", help="skip the question stage (score, select, gather)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "keys_scores_cfg2_traffic.txt"))
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -161,7 +162,7 @@ def main():
         w = workloads.build_ragged(device=dev)
     else:
         w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline,
-                                   refine_fraction=0.01 if args.config == "cfg2" else 0.0)
+                                   refine_fraction=0.01 if args.config == "cfg2" and not args.no_question else 0.0)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
     print(f"[bench] built {args.config} in {build_s:.1f}s: {w.middle_total} compressed tokens, "
