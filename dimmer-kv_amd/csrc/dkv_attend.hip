@@ -202,18 +202,26 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   for (int hw = 0; hw < HPWAVE; ++hw)
 #pragma unroll
     for (int r = 0; r < kSmallRows; ++r) part[hw][r][0] = part[hw][r][1] = 0.0f;
+  // loop order: the query rows of a (row block, v4) slice are read once and serve both token blocks
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int n = tq * 64 + tb * 32 + l32;
+  for (int rb = 0; rb < 4; ++rb) {
+    if ((rb % DB) >= HALF_BLK) continue;
+    const int rb2 = rb + HALF_BLK;
+    const int hw = rb / DB;
+    const int hl = hs * HPWAVE + hw;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      if ((rb % DB) >= HALF_BLK) continue;
-      const int rb2 = rb + HALF_BLK;
-      const int hw = rb / DB;
-      const int hl = hs * HPWAVE + hw;
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int j = (rb % DB) * 32 + 8 * v4 + 4 * lhi;  // pair index, 0 .. D/2-1
+      float4 qlo[kSmallRows], qhi[kSmallRows];
 #pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const int j = (rb % DB) * 32 + 8 * v4 + 4 * lhi;  // pair index, 0 .. D/2-1
+      for (int r = 0; r < kSmallRows; ++r) {
+        if (r >= RH) break;
+        qlo[r] = *(const float4*)(qs + (hl * kSmallRows + r) * D + j);
+        qhi[r] = *(const float4*)(qs + (hl * kSmallRows + r) * D + j + HALF_D);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        const int n = tq * 64 + tb * 32 + l32;
         const float4 c4 = *(const float4*)(cs + n * CSTR + j);
         const float4 s4 = *(const float4*)(sn + n * CSTR + j);
         const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
@@ -229,10 +237,8 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 #pragma unroll
         for (int r = 0; r < kSmallRows; ++r) {
           if (r >= RH) break;
-          const float4 qlo = *(const float4*)(qs + (hl * kSmallRows + r) * D + j);
-          const float4 qhi = *(const float4*)(qs + (hl * kSmallRows + r) * D + j + HALF_D);
-          part[hw][r][tb] += qlo.x * rlo[0] + qlo.y * rlo[1] + qlo.z * rlo[2] + qlo.w * rlo[3] + qhi.x * rhi[0] +
-                             qhi.y * rhi[1] + qhi.z * rhi[2] + qhi.w * rhi[3];
+          part[hw][r][tb] += qlo[r].x * rlo[0] + qlo[r].y * rlo[1] + qlo[r].z * rlo[2] + qlo[r].w * rlo[3] +
+                             qhi[r].x * rhi[0] + qhi[r].y * rhi[1] + qhi[r].z * rhi[2] + qhi[r].w * rhi[3];
         }
       }
     }
