@@ -737,6 +737,7 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   __shared__ float red[kK3Waves][32][65];
   __shared__ float ored[kK3Waves][32];
   __shared__ float Mrow[32];
+  __shared__ __attribute__((aligned(16))) float2 saff[kK3Waves][kK3WaveTok];  // (scale, offset) of each wave's tokens
 
   const int bid = blockIdx.x;
   const int rbk = bid % a.row_blocks;
@@ -751,6 +752,29 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   const int l32 = lane & 31, lhi = lane >> 5;
   const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
   const long slot0 = (long)(tb0 + bs.y * (kSplitTok / kTileTok)) * kTileTok;  // first slot of the split
+  const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
+  const int my_row = rbk * 32 + l32;
+  const bool row_ok = my_row < a.R_total;
+
+  // every global load of the wave goes out first: the affine pairs of its 128 tokens (one
+  // 16-byte load per lane, staged in LDS for the broadcast reads), its probability rows and
+  // value codes for all 8 steps; the row maxima come from the tile statistics meanwhile.
+  const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
+  const float4 aff2 = *(const float4*)(aff + wt0 + 2 * lane);
+  const uint16_t* prow = a.probs + (long)(row_ok ? my_row : 0) * a.n_slots + slot0;
+  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_slots + slot0;
+  const uint8_t* col1 = col0 + 32L * a.n_slots;
+  constexpr int STEPS = kK3WaveTok / 16;  // 8
+  half8 pt[STEPS];
+  uint2 c0[STEPS], c1[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int t8 = wt0 + st * 16 + lhi * 8;
+    pt[st] = *(const half8*)(prow + t8);
+    c0[st] = *(const uint2*)(col0 + t8);
+    c1[st] = *(const uint2*)(col1 + t8);
+  }
+  *(float4*)&saff[wave][2 * lane] = aff2;
   if (tid < 256) {
     const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
     const int r = rbk * 32 + (tid >> 3);
@@ -758,8 +782,6 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     if ((tid & 7) == 0) Mrow[tid >> 3] = m;
   }
   __syncthreads();
-  const int my_row = rbk * 32 + l32;
-  const bool row_ok = my_row < a.R_total;
   const float my_M = Mrow[l32];
 
   floatx16 acc[2];
@@ -769,7 +791,6 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     for (int v = 0; v < 16; ++v) acc[nb][v] = 0.0f;
   float osum = 0.0f;
 
-  const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
   // K2 left p~ = exp(s - tile max) in fp16; the wave's 128 tokens lie in one tile, whose
   // factor f = exp(tile max - row max) turns p~ into p = exp(s - row max).
   const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
@@ -778,36 +799,22 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     const float mt = a.tile_max[(long)my_row * a.ntiles + tile];
     f = (mt == -INFINITY) ? 0.0f : __expf(mt - my_M);
   }
-  const uint16_t* prow = a.probs + (long)(row_ok ? my_row : 0) * a.n_slots + slot0;
-  const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
-  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_slots + slot0;
-  const uint8_t* col1 = col0 + 32L * a.n_slots;
-
-  // Branch-free steps: every load stays inside the slot buffers (they extend a
-  // whole split past the last tile), and slots past the split's tokens get p = 0
-  // by selection (whatever those slots hold).
-  constexpr int STEPS = kK3WaveTok / 16;  // 8
+  // every load above stayed inside the slot buffers (they extend a whole split past the last
+  // tile); slots past the split's tokens get p = 0 by selection, whatever they hold
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
     const int t8 = wt0 + st * 16 + lhi * 8;  // this lane's 8 tokens: t8 .. t8+7 (split-relative)
-    const half8 pt = *(const half8*)(prow + t8);
-    float4 afv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) afv[e] = *(const float4*)(aff + t8 + 2 * e);
-    const uint2 c0 = *(const uint2*)(col0 + t8);
-    const uint2 c1 = *(const uint2*)(col1 + t8);
     half8 pa;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool ok = t8 + e < count;
-      const float p = (float)pt[e] * f;
-      const float sc = (e & 1) ? afv[e >> 1].z : afv[e >> 1].x;
-      const float of = (e & 1) ? afv[e >> 1].w : afv[e >> 1].y;
-      pa[e] = ok ? (half_t)(p * sc) : (half_t)0.0f;
-      osum += ok ? p * of : 0.0f;
+      const float2 af = saff[wave][st * 16 + lhi * 8 + e];
+      const float p = (float)pt[st][e] * f;
+      pa[e] = ok ? (half_t)(p * af.x) : (half_t)0.0f;
+      osum += ok ? p * af.y : 0.0f;
     }
-    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0.x, c0.y), acc[0], 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1.x, c1.y), acc[1], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0[st].x, c0[st].y), acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1[st].x, c1[st].y), acc[1], 0, 0, 0);
   }
   osum += __shfl_xor(osum, 32, 64);
   // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3)
