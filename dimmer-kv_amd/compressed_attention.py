@@ -14,6 +14,12 @@ from the packed bit-plane hot tier (hot_tier.PackedStream): the key codes are
 unpacked into LDS and multiplied on MFMA, so neither the FP16 key cache nor a
 coefficient matrix is materialised.
 
+Both of the reference's entry points build a context: ``prog@`` through
+``ProgressiveCache.context`` (packed bit planes), and ``dkvtc@`` through the
+reference's own constructor ``CompressedContext(codec, keys, values, model,
+dtype)`` (:34-89) after ``KVTCCodec.compress``, which here packs the chosen
+ladder codes (hot_tier.LadderStream) instead of fp16 coefficient blocks.
+
 ``CompressedContext.attend`` keeps the reference's contract (:113-137):
 (module, query [B, Hq, q_len, d], key/value [B, Hkv, T_exact, d] exact cache
 after ``update``, additive attention_mask or None, scaling) ->
@@ -25,7 +31,10 @@ from __future__ import annotations
 import torch
 
 import dkv_hip
-from hot_tier import PackedStream
+from hot_tier import LadderStream, LadderTables, PackedStream
+
+# Exact tokens one sequence may hold in the shared softmax (the kernels' exact-token split).
+MAX_EXACT_TOKENS = 1024
 
 
 class ModelTables:
@@ -62,12 +71,26 @@ class ModelTables:
 class CompressedContext:
     """Compressed middle tokens of one or more conversations, attended to directly.
 
-    ``cu_seqlens`` (int32 [B+1]) splits the packed streams into B
-    conversations for a fused varlen decode; B = 1 is the reference's case.
+    Two constructors:
+
+    - ``CompressedContext(codec, keys, values, model, dtype=torch.float16)``, the reference's
+      (scripts/compressed_attention.py:34-89), after ``codec.compress`` (the ``dkvtc@`` /
+      ``kvtc@`` entry points): the compressed tokens' ladder codes are packed per token;
+    - ``CompressedContext(tables, key, value, positions, q_heads, cu_seqlens=None,
+      exact_cache=None)`` over packed streams (``prog@``, and ragged batches): ``cu_seqlens``
+      (int32 [B+1]) splits the streams into B conversations for a fused varlen decode.
     """
 
-    def __init__(self, tables: ModelTables, key: PackedStream, value: PackedStream, positions: torch.Tensor,
-                 q_heads: int, cu_seqlens: torch.Tensor | None = None, exact_cache=None):
+    def __init__(self, *args, **kwargs):
+        from kvtc import KVTCCodec
+
+        if args and isinstance(args[0], KVTCCodec):
+            self._init_kvtc(*args, **kwargs)
+        else:
+            self._init_streams(*args, **kwargs)
+
+    def _init_streams(self, tables: ModelTables, key, value, positions: torch.Tensor, q_heads: int,
+                      cu_seqlens: torch.Tensor | None = None, exact_cache=None, extra=None):
         if key.n != value.n:
             raise ValueError("key and value streams hold different token counts")
         self.tables, self.key, self.value = tables, key, value
@@ -86,11 +109,109 @@ class CompressedContext:
         self._score_prepared = None
         self._cu_exact = {}
         self.importance = None  # float32 [n] while a question is being scored
+        # Middle tokens held exactly (kvtc's exact rung), per layer float32 [Hkv, E_x, d] (keys RoPE'd);
+        # they join the exact tokens of every softmax.
+        self.extra = extra
+
+    def _init_kvtc(self, codec, keys: list[torch.Tensor], values: list[torch.Tensor], model, dtype=torch.float16):
+        """The reference constructor (scripts/compressed_attention.py:34-89) over ``codec``'s last
+        compress: tokens whose key was evicted are left out (:50); the others are packed at their
+        rungs into ladder streams over the union of the groups they use (:53-54), an evicted value
+        decoding to the mean; tokens with a key or value at the exact rung are rebuilt once
+        (inverse transform, RoPE) and attended as exact tokens.  The exact cache holds the sinks
+        and the recent window (:85-88).  ``dtype`` is the reference's coefficient dtype; the
+        kernels decode keys to fp16 MFMA operands and value codes exactly whatever it is."""
+        from common import build_cache
+        from kvtc import inverse_transform, rerotate, rope_tables
+
+        start, end = codec.last_span
+        tokens = keys[0].shape[2]
+        device = codec.device
+        layers, heads, dim, group = codec.layers, codec.heads, codec.head_dim, codec.group
+        streams = codec.streams
+        choice = {k: codec.last_choice[k].to(device) for k in ("key", "value")}
+        exact_rung = {k: len(streams[k].rung_bytes) for k in ("key", "value")}
+        kept = choice["key"] >= 0
+        promoted = kept & ((choice["key"] == exact_rung["key"]) | (choice["value"] == exact_rung["value"]))
+        coded = kept & ~promoted
+        rows = coded.nonzero().flatten()
+        # groups any coded token uses in either stream, padded to a multiple of 4 with empty groups
+        groups = streams["key"].rungs.shape[1]
+        used = torch.zeros(groups, dtype=torch.bool, device=device)
+        for kind in ("key", "value"):
+            r = choice[kind][rows]
+            r = r[(r >= 0) & (r < exact_rung[kind])].unique()
+            if r.numel():
+                used |= (streams[kind].rungs.to(device)[r] > 0).any(dim=0)
+        cols = used.nonzero().flatten()
+        padded = max(4, -(-cols.numel() // 4) * 4)
+        cos, sin = rope_tables(model, tokens, device)
+        packed, bases = {}, {}
+        for kind in ("key", "value"):
+            rungs = torch.zeros(streams[kind].rungs.shape[0], padded, dtype=torch.long)
+            rungs[:, :cols.numel()] = streams[kind].rungs.cpu()[:, cols.cpu()]
+            table = LadderTables(rungs, None, device, group)
+            codes, low, scale = codec.last_codes[kind]
+            c = torch.zeros(rows.numel(), padded, group, dtype=torch.uint8, device=device)
+            lo = torch.zeros(rows.numel(), padded, dtype=torch.float16, device=device)
+            sc = torch.zeros_like(lo)
+            c[:, :cols.numel()] = codes[rows][:, cols]
+            lo[:, :cols.numel()] = low[rows][:, cols]
+            sc[:, :cols.numel()] = scale[rows][:, cols]
+            packed[kind] = LadderStream.pack(c, lo, sc, choice[kind][rows], table)
+            basis = torch.zeros(streams[kind].basis.shape[0], padded * group, device=device)
+            col_idx = (cols[:, None] * group + torch.arange(group, device=device)).flatten()
+            basis[:, :col_idx.numel()] = streams[kind].basis[:, col_idx]
+            bases[kind] = basis
+        tables = ModelTables(bases["key"], bases["value"], streams["key"].mean, streams["value"].mean, layers, heads,
+                             dim, cos, sin)
+        extra = None
+        exact_tokens = tokens - (end - start)
+        idx = promoted.nonzero().flatten()
+        if exact_tokens + idx.numel() > MAX_EXACT_TOKENS:
+            raise ValueError(f"{exact_tokens} exact and {idx.numel()} exact-rung tokens exceed the "
+                             f"{MAX_EXACT_TOKENS} exact tokens a sequence may hold")
+        if idx.numel():
+            extra = {}
+            for kind in ("key", "value"):
+                matrix = inverse_transform(codec.last_coefficients[kind][idx].float(), streams[kind], group)
+                per_layer = matrix.view(-1, layers, heads, dim)
+                parts = []
+                for layer in range(layers):
+                    part = per_layer[:, layer].transpose(0, 1)  # [heads, E_x, d]
+                    if kind == "key":
+                        part = rerotate(part, cos[start + idx], sin[start + idx])
+                    parts.append(part.float().contiguous())
+                extra[kind] = parts
+        exact_keys = [torch.cat([k[..., :start, :], k[..., end:, :]], dim=2) for k in keys]
+        exact_values = [torch.cat([v[..., :start, :], v[..., end:, :]], dim=2) for v in values]
+        self._init_streams(tables, packed["key"], packed["value"], rows + start,
+                           model.config.num_attention_heads, exact_cache=build_cache(exact_keys, exact_values, model),
+                           extra=extra)
+        self.codec, self.model, self.dtype = codec, model, dtype
+        self.start, self.end, self.context_tokens = start, end, tokens
+
+    def _with_extra(self, layer: int, key_exact, value_exact, mask, q_len: int):
+        """Prepends the exact-rung middle tokens (never masked) to a batch-1 exact cache."""
+        if self.extra is None:
+            return key_exact, value_exact, mask
+        ek, ev = self.extra["key"][layer], self.extra["value"][layer]
+        if key_exact is None:
+            return ek, ev, None
+        key_exact = torch.cat([ek, key_exact], dim=1)
+        value_exact = torch.cat([ev, value_exact], dim=1)
+        if mask is not None:
+            mask = torch.cat([mask.new_zeros(q_len, ek.shape[1]), mask], dim=1).contiguous()
+        return key_exact, value_exact, mask
 
     # ----- memory accounting (scripts/compressed_attention.py:91-102) -----
     def code_bytes(self) -> int:
-        """Bytes held for the compressed tokens: the packed hot tiers (reference accounting)."""
-        return self.key.hot_bytes() + self.value.hot_bytes()
+        """Bytes held for the compressed tokens: the packed hot tiers (reference accounting), plus
+        the float32 rows of exact-rung tokens."""
+        extra = 0
+        if self.extra is not None:
+            extra = sum(t.numel() * t.element_size() for kind in ("key", "value") for t in self.extra[kind])
+        return self.key.hot_bytes() + self.value.hot_bytes() + extra
 
     def basis_bytes(self) -> int:
         return self.tables.basis_bytes()
@@ -180,6 +301,11 @@ class CompressedContext:
             lengths = (key.shape[2],)
             if attention_mask is not None:
                 mask = attention_mask[0, 0, :, -key.shape[2]:].float().contiguous()
+        if self.extra is not None:
+            if batch != 1:
+                raise ValueError("a context with exact-rung tokens takes one conversation")
+            key_exact, value_exact, mask = self._with_extra(layer, key_exact, value_exact, mask, q_len)
+            lengths = (key_exact.shape[1],)
         args = self.layer_args(layer, query, out, key_exact, value_exact, mask, lengths, scaling)
         self.run_layer(args)
         if self.importance is not None:
@@ -215,7 +341,9 @@ class CompressedContext:
         if past > 0:
             key_exact = key[0, :, :past].float().contiguous()
             value_exact = key_exact  # values are not read by the scoring kernels
-            lengths = (past,)
+        key_exact, value_exact, _ = self._with_extra(layer, key_exact, value_exact, None, q_len)
+        if key_exact is not None:
+            lengths = (key_exact.shape[1],)
         scratch = torch.empty(1, q_len, query.shape[1], query.shape[3], dtype=query.dtype, device=query.device)
         args = self.layer_args(layer, query, scratch, key_exact, value_exact, None, lengths, scaling)
         need = dkv_hip.score_workspace_bytes(args)

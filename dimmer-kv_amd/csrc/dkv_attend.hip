@@ -122,7 +122,16 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs 
   const int half = threadIdx.x & 1;
   const int t = slot_token(a, slot);
   uint32_t vals[16];
-  if (t >= 0) {
+  if (t >= 0 && a.s.format == DKV_FMT_LADDER) {
+    const int G = a.G;
+    const int r = a.s.pieces[t];
+    const bool ok = r >= 0 && r < a.s.ladder.rungs;
+    const int b = ok ? a.s.ladder.bits[(long)r * G + g] : 0;
+    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + (ok ? a.s.ladder.seg_off[(long)r * G + g] : 0);
+    uint32_t cw[8], header;
+    load_ladder_half(seg, b, half, cw, header);
+    ladder_half_f16(cw, header, vals);
+  } else if (t >= 0) {
     const int G = a.G;
     const int kp = a.s.pieces[t];
     const int m = a.s.order.planes[(long)kp * G + g];
@@ -650,7 +659,17 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArg
   const int t = slot_token(a, slot);
   uint32_t cw[8];
   float2 aff = make_float2(0.0f, 0.0f);
-  if (t >= 0) {
+  if (t >= 0 && a.s.format == DKV_FMT_LADDER) {
+    // value = code * scale + low: the affine pair is (scale, low)
+    const int G = a.G;
+    const int r = a.s.pieces[t];
+    const bool ok = r >= 0 && r < a.s.ladder.rungs;
+    const int b = ok ? a.s.ladder.bits[(long)r * G + g] : 0;
+    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + (ok ? a.s.ladder.seg_off[(long)r * G + g] : 0);
+    uint32_t header;
+    load_ladder_half(seg, b, half, cw, header);
+    aff = make_float2(half_bits_to_float((uint16_t)(header >> 16)), half_bits_to_float((uint16_t)(header & 0xffffu)));
+  } else if (t >= 0) {
     const int G = a.G;
     const int kp = a.s.pieces[t];
     const int m = a.s.order.planes[(long)kp * G + g];
@@ -1120,9 +1139,9 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
   if (rc) return rc;
   DKV_REQUIRE(a->head_dim == 64 || a->head_dim == 128, DKV_ESHAPE, "%s: head_dim must be 64 or 128 (got %d)", what,
               a->head_dim);
-  DKV_REQUIRE(a->rank > 0 && a->rank % 256 == 0 && a->rank == 64 * a->key.order.groups, DKV_ESHAPE,
+  DKV_REQUIRE(a->rank > 0 && a->rank % 256 == 0 && a->rank == 64 * dkv::stream_groups(a->key), DKV_ESHAPE,
               "%s: rank %d must be a multiple of 256 and equal 64 * groups (%d)", what, a->rank,
-              a->key.order.groups);
+              dkv::stream_groups(a->key));
   DKV_REQUIRE(a->kv_heads > 0 && a->q_heads % a->kv_heads == 0, DKV_ESHAPE, "%s: q_heads %d not a multiple of %d",
               what, a->q_heads, a->kv_heads);
   DKV_REQUIRE(a->kv_heads % (256 / a->head_dim) == 0, DKV_ESHAPE, "%s: kv_heads %d must be a multiple of %d", what,
@@ -1161,7 +1180,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.Hkv = a->kv_heads;
   k.Hq = a->q_heads;
   k.q_len = a->q_len;
-  k.G = a->key.order.groups;
+  k.G = dkv::stream_groups(a->key);
   k.n_total = L.n_total;
   k.ntiles = L.ntiles;
   k.query_dtype = a->query_dtype;
@@ -1189,6 +1208,8 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   if (rc) return rc;
   DKV_REQUIRE(plane_cap >= 0 && plane_cap <= 8, DKV_EINVAL, "dkv_attend_prepare: plane_cap %d not in 0..8",
               plane_cap);
+  DKV_REQUIRE(a->key.format == DKV_FMT_PLANES || plane_cap == 8, DKV_EINVAL,
+              "dkv_attend_prepare: a plane cap needs a bit-plane key stream (ladder streams have no planes)");
   const Layout L = make_layout(a);
   // only the decoded areas at the head of the workspace are written, so an attend or a score
   // workspace (both start with them) will do
@@ -1201,7 +1222,7 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   d.batch = a->batch;
   d.ntiles = L.ntiles;
   d.n_slots = L.n_slots;
-  d.G = a->key.order.groups;
+  d.G = dkv::stream_groups(a->key);
   d.plane_cap = plane_cap;
   const dim3 grid((unsigned)(((long)d.G * (L.n_slots / kDecodeTok) + 7) / 8 * 8));
   hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), d);
@@ -1209,7 +1230,8 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   if (rc || !a->value.blob) return rc;
   rc = dkv::check_stream(&a->value, "dkv_attend_prepare");
   if (rc) return rc;
-  DKV_REQUIRE(a->value.order.groups == a->key.order.groups, DKV_ESHAPE, "dkv_attend_prepare: K/V group mismatch");
+  DKV_REQUIRE(dkv::stream_groups(a->value) == dkv::stream_groups(a->key), DKV_ESHAPE,
+              "dkv_attend_prepare: K/V group mismatch");
   DecodeArgs v = d;
   v.s = a->value;
   v.plane_cap = 8;
@@ -1221,7 +1243,8 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
 static int check_values(const dkv_attend_args_t* a, int& E_total) {
   int rc = dkv::check_stream(&a->value, "dkv_attend_values");
   if (rc) return rc;
-  DKV_REQUIRE(a->value.order.groups == a->key.order.groups, DKV_ESHAPE, "dkv_attend_values: K/V group mismatch");
+  DKV_REQUIRE(dkv::stream_groups(a->value) == dkv::stream_groups(a->key), DKV_ESHAPE,
+              "dkv_attend_values: K/V group mismatch");
   DKV_REQUIRE(a->value_basis && a->mean_v && a->out, DKV_EINVAL, "dkv_attend_values: null value/out pointer");
   DKV_REQUIRE(a->out_dtype >= DKV_F32 && a->out_dtype <= DKV_BF16, DKV_EINVAL, "dkv_attend_values: bad out dtype");
   DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "dkv_attend_values: mask is only supported for batch == 1");
@@ -1259,7 +1282,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
               "dkv_attend_values: workspace %zu B < required %zu B", workspace_bytes, L.total);
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
-  const int G = a->key.order.groups;
+  const int G = dkv::stream_groups(a->key);
   if (L.nsplits > 0) {
     K3aArgs k{};
     k.vcodes = (const uint8_t*)(ws + L.vcodes);

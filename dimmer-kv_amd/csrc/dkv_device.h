@@ -159,6 +159,76 @@ DKV_DEVICE void unpack_half_f16(const uint32_t (&pl)[8], AffineDq a, uint32_t (&
   }
 }
 
+// ---------------------------------------------------------------------------
+// kvtc ladder codes.  A (token, group) segment with b in {2, 4, 8} bits is
+// [low f16][scale f16][64 codes of b bits, LSB-first]; the codes of half h
+// (coefficients 32h .. 32h+31) are the b u32 words starting at byte 4 + 4bh.
+// They are returned in the plane path's code-word form: byte i of cw[w] is the
+// code of coefficient 32h + 4w + i.  b = 0 gives zero codes and header.
+// ---------------------------------------------------------------------------
+DKV_DEVICE int dkv_groups(const dkv_stream_t& s) {
+  return s.format == DKV_FMT_LADDER ? s.ladder.groups : s.order.groups;
+}
+
+DKV_DEVICE uint32_t spread_nibbles(uint32_t x) {  // 4 nibbles (16 bits) -> 4 bytes
+  return (x & 0xfu) | ((x & 0xf0u) << 4) | ((x & 0xf00u) << 8) | ((x & 0xf000u) << 12);
+}
+
+DKV_DEVICE uint32_t spread_pairs(uint32_t x) {  // 4 two-bit fields (8 bits) -> 4 bytes
+  return (x & 0x3u) | ((x & 0xcu) << 6) | ((x & 0x30u) << 12) | ((x & 0xc0u) << 18);
+}
+
+DKV_DEVICE void load_ladder_half(const uint8_t* seg, int b, int half, uint32_t (&cw)[8], uint32_t& header) {
+  const uint32_t* w = (const uint32_t*)seg;
+  header = b > 0 ? w[0] : 0u;
+  const uint32_t* c = w + 1 + b * half;
+  uint32_t raw[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) raw[k] = k < b ? c[k] : 0u;
+  if (b == 4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      cw[2 * k] = spread_nibbles(raw[k] & 0xffffu);
+      cw[2 * k + 1] = spread_nibbles(raw[k] >> 16);
+    }
+  } else if (b == 2) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cw[4 * k + j] = spread_pairs((raw[k] >> (8 * j)) & 0xffu);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cw[k] = raw[k];  // b == 8 (b == 0: all zero)
+  }
+}
+
+// Ladder coefficient in the reference's fp32 operation order
+// (scripts/kvtc.py:78): code * scale + low, the product and the sum each
+// rounded on its own.  A zero header (b = 0) gives 0.
+DKV_DEVICE float ladder_value(uint32_t code, float low, float scale) {
+#pragma clang fp contract(off)
+  const float prod = (float)code * scale;
+  return prod + low;
+}
+
+// 32 ladder codes of one (token, group, half) -> 32 fp16 values (the fp16
+// cast of the exact fp32 coefficient), as 16 packed half2 words.
+DKV_DEVICE void ladder_half_f16(const uint32_t (&cw)[8], uint32_t header, uint32_t (&out)[16]) {
+  const float low = half_bits_to_float((uint16_t)(header & 0xffffu));
+  const float scale = half_bits_to_float((uint16_t)(header >> 16));
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint16_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const half_t h = (half_t)ladder_value((cw[w] >> (8 * i)) & 0xffu, low, scale);
+      __builtin_memcpy(&b[i], &h, 2);
+    }
+    out[2 * w] = (uint32_t)b[0] | ((uint32_t)b[1] << 16);
+    out[2 * w + 1] = (uint32_t)b[2] | ((uint32_t)b[3] << 16);
+  }
+}
+
 // Sequence/tile lookup from cu_seqlens without a host-built table: returns
 // the sequence b and the tile index inside it for a global tile id, where
 // sequence b has ceil(len_b / tile) tiles.

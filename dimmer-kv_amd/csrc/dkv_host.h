@@ -35,12 +35,34 @@ inline int check_order(const dkv_order_t& o, const char* what) {
   return DKV_OK;
 }
 
+inline int check_ladder(const dkv_ladder_t& l, const char* what) {
+  if (l.groups <= 0 || l.rungs <= 0) {
+    set_error("%s: bad ladder (groups=%d rungs=%d)", what, l.groups, l.rungs);
+    return DKV_ESHAPE;
+  }
+  if (!l.bits || !l.seg_off || !l.rung_bytes) {
+    set_error("%s: ladder tables must be non-null", what);
+    return DKV_EINVAL;
+  }
+  return DKV_OK;
+}
+
 inline int check_stream(const dkv_stream_t* s, const char* what) {
   if (!s || !s->blob || !s->tok_off || !s->pieces) {
     set_error("%s: stream blob/tok_off/pieces must be non-null", what);
     return DKV_EINVAL;
   }
+  if (s->format == DKV_FMT_LADDER) return check_ladder(s->ladder, what);
+  if (s->format != DKV_FMT_PLANES) {
+    set_error("%s: unknown stream format %d", what, s->format);
+    return DKV_EINVAL;
+  }
   return check_order(s->order, what);
+}
+
+// 64-component groups of a (checked) stream.
+inline int stream_groups(const dkv_stream_t& s) {
+  return s.format == DKV_FMT_LADDER ? s.ladder.groups : s.order.groups;
 }
 
 }  // namespace dkv

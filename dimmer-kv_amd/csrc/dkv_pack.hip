@@ -99,17 +99,109 @@ extern "C" int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const 
 }
 
 // ---------------------------------------------------------------------------
+// Ladder pack: one thread per (token, group, half).  The 32 codes of the half
+// are squeezed to b bits each, LSB-first (code j at bit b*j), into b words;
+// the thread of half 0 also writes the [low][scale] header.
+// ---------------------------------------------------------------------------
+DKV_DEVICE uint32_t gather_nibbles(uint32_t c) {  // 4 bytes < 16 -> 16 bits
+  return (c & 0xfu) | ((c >> 4) & 0xf0u) | ((c >> 8) & 0xf00u) | ((c >> 12) & 0xf000u);
+}
+
+DKV_DEVICE uint32_t gather_pairs(uint32_t c) {  // 4 bytes < 4 -> 8 bits
+  return (c & 0x3u) | ((c >> 6) & 0xcu) | ((c >> 12) & 0x30u) | ((c >> 18) & 0xc0u);
+}
+
+__global__ __launch_bounds__(256) void pack_ladder_kernel(const uint8_t* __restrict__ codes,
+                                                          const uint16_t* __restrict__ low,
+                                                          const uint16_t* __restrict__ scale,
+                                                          const int16_t* __restrict__ rung, int n, dkv_ladder_t lad,
+                                                          uint8_t* __restrict__ blob,
+                                                          const int64_t* __restrict__ tok_off) {
+  const int G = lad.groups;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)n * G * 2) return;
+  const int h = (int)(id & 1);
+  const long tg = id >> 1;
+  const int t = (int)(tg / G), g = (int)(tg % G);
+  const int r = rung[t];
+  if (r < 0 || r >= lad.rungs) return;
+  const int b = lad.bits[(long)r * G + g];
+  if (b != 2 && b != 4 && b != 8) return;
+  uint32_t* seg = (uint32_t*)(blob + tok_off[t] + lad.seg_off[(long)r * G + g]);
+  if (h == 0) seg[0] = (uint32_t)low[tg] | ((uint32_t)scale[tg] << 16);
+  const uint4* src = (const uint4*)(codes + tg * 64 + h * 32);
+  const uint4 c0 = src[0], c1 = src[1];
+  const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  uint32_t* dst = seg + 1 + b * h;
+  if (b == 8) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) dst[k] = cw[k];
+  } else if (b == 4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      dst[k] = gather_nibbles(cw[2 * k] & 0x0f0f0f0fu) | (gather_nibbles(cw[2 * k + 1] & 0x0f0f0f0fu) << 16);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      uint32_t wv = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv |= gather_pairs(cw[4 * k + j] & 0x03030303u) << (8 * j);
+      dst[k] = wv;
+    }
+  }
+}
+
+extern "C" int dkv_pack_ladder(const uint8_t* codes, const uint16_t* low, const uint16_t* scale, const int16_t* rung,
+                               int32_t n, dkv_ladder_t ladder, uint8_t* blob, const int64_t* tok_off, void* stream) {
+  DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_pack_ladder: n < 0");
+  int rc = dkv::check_ladder(ladder, "dkv_pack_ladder");
+  if (rc) return rc;
+  DKV_REQUIRE(codes && low && scale && rung && blob && tok_off, DKV_EINVAL, "dkv_pack_ladder: null pointer");
+  if (n == 0) return DKV_OK;
+  const long threads = (long)n * ladder.groups * 2;
+  const long blocks = (threads + 255) / 256;
+  DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_pack_ladder: too many tokens");
+  hipLaunchKernelGGL(pack_ladder_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), codes, low,
+                     scale, rung, n, ladder, blob, tok_off);
+  return dkv::check_launch("dkv_pack_ladder");
+}
+
+// ---------------------------------------------------------------------------
 // K1: one thread per (token, group, half): 32 coefficients.
 // ---------------------------------------------------------------------------
+// Ladder streams: code * scale + low in fp32 (scripts/kvtc.py:78), then the
+// output cast.  A rung outside the ladder decodes to zeros.
+template <int DT>
+DKV_DEVICE void unpack_ladder_half(const dkv_stream_t& s, int t, int g, int h, long base, void* __restrict__ out) {
+  const int G = s.ladder.groups;
+  const int r = s.pieces[t];
+  const bool ok = r >= 0 && r < s.ladder.rungs;
+  const int b = ok ? s.ladder.bits[(long)r * G + g] : 0;
+  const uint8_t* seg = s.blob + s.tok_off[t] + (ok ? s.ladder.seg_off[(long)r * G + g] : 0);
+  uint32_t cw[8], header;
+  load_ladder_half(seg, b, h, cw, header);
+  const float low = half_bits_to_float((uint16_t)(header & 0xffffu));
+  const float scale = half_bits_to_float((uint16_t)(header >> 16));
+#pragma unroll
+  for (int w = 0; w < 8; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      store_from_float(out, base + 4 * w + i, DT, ladder_value((cw[w] >> (8 * i)) & 0xffu, low, scale));
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void unpack_dequant_kernel(dkv_stream_t s, int t0, int nt, void* __restrict__ out) {
-  const int G = s.order.groups;
+  const int G = dkv_groups(s);
   const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (long)nt * G * 2) return;
   const int h = (int)(id & 1);
   const long tg = id >> 1;
   const int tt = (int)(tg / G), g = (int)(tg % G);
   const int t = t0 + tt;
+  if (s.format == DKV_FMT_LADDER) {
+    unpack_ladder_half<DT>(s, t, g, h, (long)tt * (64L * G) + g * 64 + h * 32, out);
+    return;
+  }
   const int k = s.pieces[t];
   const int m = s.order.planes[(long)k * G + g];
   const uint8_t* seg = s.blob + s.tok_off[t] + s.order.seg_off[(long)k * G + g];
@@ -158,7 +250,7 @@ extern "C" int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt,
   DKV_REQUIRE(out_dtype == DKV_F32 || out_dtype == DKV_F16 || out_dtype == DKV_BF16, DKV_EINVAL,
               "dkv_unpack_dequant: bad dtype %d", out_dtype);
   if (nt == 0) return DKV_OK;
-  const long threads = (long)nt * s->order.groups * 2;
+  const long threads = (long)nt * dkv::stream_groups(*s) * 2;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   hipStream_t st = dkv::as_stream(stream);
   if (out_dtype == DKV_F32)
@@ -246,6 +338,7 @@ extern "C" int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const
                                int64_t* tok_off, int16_t* pieces, void* stream) {
   int rc = dkv::check_stream(s, "dkv_gather_cold");
   if (rc) return rc;
+  DKV_REQUIRE(s->format == DKV_FMT_PLANES, DKV_EINVAL, "dkv_gather_cold: only bit-plane streams have a cold tier");
   DKV_REQUIRE(cold && cold_tok_off && idx && refined && tok_off && pieces && s->order.cold_off, DKV_EINVAL,
               "dkv_gather_cold: null pointer");
   DKV_REQUIRE(k >= 0 && refined_base_off >= 0, DKV_ESHAPE, "dkv_gather_cold: bad k / offset");

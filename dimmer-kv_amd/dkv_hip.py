@@ -16,13 +16,14 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libdimmerkv_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DKV_F32, DKV_F16, DKV_BF16 = 0, 1, 2
+DKV_FMT_PLANES, DKV_FMT_LADDER = 0, 1
 _DTYPE = {torch.float32: DKV_F32, torch.float16: DKV_F16, torch.bfloat16: DKV_BF16}
 
 EXPORTS = [
-    "dkv_abi_version", "dkv_last_error", "dkv_pack_planes", "dkv_unpack_dequant", "dkv_dequantize_codes",
+    "dkv_abi_version", "dkv_last_error", "dkv_pack_planes", "dkv_pack_ladder", "dkv_unpack_dequant", "dkv_dequantize_codes",
     "dkv_prepare_key_basis", "dkv_prepare_value_basis", "dkv_attend_workspace_bytes", "dkv_attend_prepare",
     "dkv_attend_layer",
     "dkv_attend_scores", "dkv_attend_values",
@@ -38,8 +39,13 @@ class Order(ctypes.Structure):
                 ("prefix_bytes", c_vp)]
 
 
+class Ladder(ctypes.Structure):
+    _fields_ = [("groups", c_i32), ("rungs", c_i32), ("bits", c_vp), ("seg_off", c_vp), ("rung_bytes", c_vp)]
+
+
 class Stream(ctypes.Structure):
-    _fields_ = [("blob", c_vp), ("tok_off", c_vp), ("pieces", c_vp), ("order", Order)]
+    _fields_ = [("blob", c_vp), ("tok_off", c_vp), ("pieces", c_vp), ("order", Order), ("format", c_i32),
+                ("ladder", Ladder)]
 
 
 class AttendArgs(ctypes.Structure):
@@ -122,6 +128,13 @@ def pack_planes(codes, low, span, pieces, order: Order, hot, hot_off, cold=None,
     _check(lib().dkv_pack_planes(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(span)), c_vp(ptr(pieces)), c_i32(n),
                                  order, c_vp(ptr(hot)), c_vp(ptr(hot_off)), c_vp(ptr(cold)), c_vp(ptr(cold_off)),
                                  c_vp(stream_handle())), "dkv_pack_planes")
+
+
+def pack_ladder(codes, low, scale, rung, ladder: Ladder, blob, tok_off) -> None:
+    n = codes.shape[0]
+    _check(lib().dkv_pack_ladder(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(scale)), c_vp(ptr(rung)), c_i32(n),
+                                 ladder, c_vp(ptr(blob)), c_vp(ptr(tok_off)), c_vp(stream_handle())),
+           "dkv_pack_ladder")
 
 
 def unpack_dequant(stream: Stream, t0: int, nt: int, out: torch.Tensor) -> None:

@@ -13,6 +13,12 @@ include/dimmerkv.h / oracle/packing_ref.py.
 full blobs in a refine area at the end of the hot allocation, and their
 offsets/piece counts are redirected there, so the attention kernels see the
 refined tokens with no other change.
+
+``LadderStream`` holds the kvtc ladder codes of the ``dkvtc@`` entry point
+(scripts/kvtc.py:62-79, scripts/kvtc_storage.py:21-75) in the same
+token-addressed form: one blob per token at its rung, ``[low f16][scale f16]
+[64 codes of b bits, LSB-first]`` for every group with b > 0 bits, so the
+same attention kernels decode either format.
 """
 
 from __future__ import annotations
@@ -108,7 +114,7 @@ class PackedStream:
 
     def c_stream(self) -> dkv_hip.Stream:
         return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(),
-                              self.tables.c_order())
+                              self.tables.c_order(), dkv_hip.DKV_FMT_PLANES)
 
     def dequantize(self, t0: int = 0, nt: int | None = None, dtype=torch.float32) -> torch.Tensor:
         """K1: coefficients [nt, 64G] of tokens t0.. at their hot prefix (bit-exact in float32)."""
@@ -146,3 +152,92 @@ class PackedStream:
         self.refined += k
         self.version += 1
         return int(fetched)
+
+
+LADDER_GROUP = 64
+LADDER_WIDTHS = (0, 2, 4, 8)
+
+
+class LadderTables:
+    """Device copies of one stream's kvtc rung ladder (scripts/kvtc.py:100-105 ``rungs`` [R, G]
+    bit widths and ``rung_bytes``) plus each rung's segment offsets.  One more row, ``empty``
+    (index R), has every group at 0 bits: the rung of a token whose coefficients are all dropped
+    (an evicted value decodes to the mean, scripts/kvtc.py:245-247)."""
+
+    def __init__(self, rungs, rung_bytes, device, group: int = LADDER_GROUP):
+        if group != LADDER_GROUP:
+            raise ValueError(f"the ladder kernels take groups of {LADDER_GROUP} components (got {group})")
+        bits = np.asarray(torch.as_tensor(rungs).cpu(), dtype=np.int64)
+        if bits.ndim != 2 or not np.isin(bits, LADDER_WIDTHS).all():
+            raise ValueError(f"ladder bit widths must be a [rungs, groups] table over {LADDER_WIDTHS}")
+        seg = np.where(bits > 0, HEADER_BYTES + bits * group // 8, 0)
+        sizes = seg.sum(axis=1)
+        if rung_bytes is not None and not np.array_equal(sizes, np.asarray(rung_bytes, dtype=np.int64)):
+            raise ValueError("rung_bytes do not match the ladder (8b bytes + 4 B per group with b > 0)")
+        bits = np.concatenate([bits, np.zeros((1, bits.shape[1]), np.int64)])
+        seg = np.concatenate([seg, np.zeros((1, seg.shape[1]), np.int64)])
+        seg_off = np.zeros_like(seg)
+        seg_off[:, 1:] = np.cumsum(seg[:, :-1], axis=1)
+        self.groups = bits.shape[1]
+        self.rungs = bits.shape[0]
+        self.empty = self.rungs - 1
+        self.bits_np = bits
+        self.bits = torch.as_tensor(bits.astype(np.uint8)).to(device)
+        self.seg_off = torch.as_tensor(seg_off.astype(np.int32)).to(device)
+        self.sizes64 = torch.as_tensor(seg.sum(axis=1)).to(device)
+        self.rung_bytes = self.sizes64.to(torch.int32)
+
+    def c_ladder(self) -> dkv_hip.Ladder:
+        return dkv_hip.Ladder(self.groups, self.rungs, self.bits.data_ptr(), self.seg_off.data_ptr(),
+                              self.rung_bytes.data_ptr())
+
+
+class LadderStream:
+    """kvtc ladder codes of one stream (keys or values) for n tokens (the ``dkvtc@`` hot tier)."""
+
+    def __init__(self, tables: LadderTables, blob, tok_off, rung, used: int):
+        self.tables = tables
+        self.blob, self.tok_off, self.pieces = blob, tok_off, rung  # ``pieces`` holds each token's rung
+        self.used = used
+        self.version = 0
+
+    @property
+    def n(self) -> int:
+        return self.pieces.numel()
+
+    @classmethod
+    def pack(cls, codes: torch.Tensor, low: torch.Tensor, scale: torch.Tensor, rung: torch.Tensor,
+             tables: LadderTables) -> "LadderStream":
+        """codes u8 [n, G, 64], low/scale f16 [n, G], rung [n] (-1 = every group dropped) -> one blob
+        per token (GPU pack kernel)."""
+        device = codes.device
+        rung = rung.to(device=device, dtype=torch.int64)
+        if rung.numel() and (int(rung.min()) < -1 or int(rung.max()) >= tables.empty):
+            raise ValueError(f"rung ids must lie in -1..{tables.empty - 1}")
+        rung = torch.where(rung < 0, torch.full_like(rung, tables.empty), rung).to(torch.int16).contiguous()
+        sizes = tables.sizes64[rung.long()] if rung.numel() else torch.zeros(0, dtype=torch.int64, device=device)
+        tok_off, total = _exclusive_cumsum(sizes)
+        blob = torch.zeros(max(total, 16), dtype=torch.uint8, device=device)
+        if rung.numel():
+            dkv_hip.pack_ladder(codes.contiguous(), low.contiguous().view(torch.int16),
+                                scale.contiguous().view(torch.int16), rung, tables.c_ladder(), blob, tok_off)
+        return cls(tables, blob, tok_off, rung, total)
+
+    def c_stream(self) -> dkv_hip.Stream:
+        return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(), dkv_hip.Order(),
+                              dkv_hip.DKV_FMT_LADDER, self.tables.c_ladder())
+
+    def dequantize(self, t0: int = 0, nt: int | None = None, dtype=torch.float32) -> torch.Tensor:
+        """K1: coefficients [nt, 64G] of tokens t0.. (bit-exact with scripts/kvtc.py:78 in float32)."""
+        nt = self.n - t0 if nt is None else nt
+        out = torch.empty(nt, LADDER_GROUP * self.tables.groups, dtype=dtype, device=self.blob.device)
+        if nt:
+            dkv_hip.unpack_dequant(self.c_stream(), t0, nt, out)
+        return out
+
+    def hot_bytes(self) -> int:
+        """Bytes held for this stream's tokens: the rung sizes (scripts/kvtc.py:243 accounting)."""
+        return self.used
+
+    def refine(self, rows: torch.Tensor) -> int:
+        raise ValueError("kvtc ladder streams have no cold tier to refine from")

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define DKV_ABI_VERSION 1
+#define DKV_ABI_VERSION 2
 
 /* Status codes.  The Python wrapper maps them to the reference's exception
  * types: DKV_EINVAL/DKV_ESHAPE -> ValueError, DKV_EBUDGET -> AssertionError,
@@ -63,17 +63,45 @@ typedef struct dkv_order {
   const int32_t* prefix_bytes; /* [K+1] */
 } dkv_order_t;
 
-/* One stream (keys or values) of a packed hot tier.  Token t's hot blob
- * starts at blob + tok_off[t] and holds pieces[t] pieces
- * (prefix_bytes[pieces[t]] bytes).  Layout: for every group with m > 0
- * planes, [low f16][span f16][m plane words of 8 B].  A plane word is two
- * little-endian u32 halves; coefficient 32h + 4w + i (w < 8, i < 4) of plane
- * p (0 = most significant bit) sits at bit (8i + w + 7 - p) mod 32 of half h. */
+/* kvtc rung ladder of one stream (scripts/kvtc.py:100-105 Stream.rungs /
+ * rung_bytes): bits[r][g] in {0, 2, 4, 8} is the width of group g at rung r.
+ * seg_off[r][g] is the byte offset of group g's segment in a token blob at
+ * rung r and rung_bytes[r] the blob size (scripts/kvtc.py:82-85: 8b bytes of
+ * codes + 4 B of shift/scale per group with b > 0). */
+typedef struct dkv_ladder {
+  int32_t groups;              /* G = rank / 64 */
+  int32_t rungs;               /* R (rows of the tables) */
+  const uint8_t* bits;         /* [R][G] */
+  const int32_t* seg_off;      /* [R][G] */
+  const int32_t* rung_bytes;   /* [R] */
+} dkv_ladder_t;
+
+/* Stream formats. */
+#define DKV_FMT_PLANES 0 /* progressive bit planes (scripts/progressive.py) */
+#define DKV_FMT_LADDER 1 /* kvtc ladder codes (scripts/kvtc.py, scripts/kvtc_storage.py) */
+
+/* One stream (keys or values) of a packed hot tier; token t's blob starts at
+ * blob + tok_off[t].
+ *
+ * DKV_FMT_PLANES: the blob holds pieces[t] pieces (prefix_bytes[pieces[t]]
+ * bytes).  Layout: for every group with m > 0 planes, [low f16][span f16][m
+ * plane words of 8 B].  A plane word is two little-endian u32 halves;
+ * coefficient 32h + 4w + i (w < 8, i < 4) of plane p (0 = most significant
+ * bit) sits at bit (8i + w + 7 - p) mod 32 of half h.
+ *
+ * DKV_FMT_LADDER: pieces[t] is the token's rung r (ladder.bits row) and the
+ * blob holds rung_bytes[r] bytes: for every group with b > 0 bits,
+ * [low f16][scale f16][64 codes of b bits, LSB-first: code j at bit b*j of the
+ * segment's code bytes] (the packing of scripts/kvtc_storage.py:21-27 applied
+ * per (token, group)); the coefficient is code * scale + low in fp32
+ * (scripts/kvtc.py:74-78), 0 for a group with b = 0.  `order` is unused. */
 typedef struct dkv_stream {
   const uint8_t* blob;
   const int64_t* tok_off; /* [n] */
   const int16_t* pieces;  /* [n] */
   dkv_order_t order;
+  int32_t format;         /* DKV_FMT_* */
+  dkv_ladder_t ladder;
 } dkv_stream_t;
 
 int dkv_abi_version(void);
@@ -89,10 +117,20 @@ int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const uint16_t* s
                     int32_t n, dkv_order_t order, uint8_t* hot, const int64_t* hot_off, uint8_t* cold,
                     const int64_t* cold_off, void* stream);
 
+/* codes u8 [n][G][64] (below 2^bits), low/scale f16 [n][G], rung [n] ->
+ * ladder blobs at tok_off[t] (int64 [n]) in the DKV_FMT_LADDER layout
+ * (replaces the per-rung code sections of scripts/kvtc_storage.py:63-75 with
+ * one self-contained blob per token, so any token decodes on its own). */
+int dkv_pack_ladder(const uint8_t* codes, const uint16_t* low, const uint16_t* scale, const int16_t* rung,
+                    int32_t n, dkv_ladder_t ladder, uint8_t* blob, const int64_t* tok_off, void* stream);
+
 /* ---- K1: unpack + dequantize (replaces scripts/progressive.py:47-55
- *      dequantize applied to TokenStore rows at their hot prefix, :196-201) -
+ *      dequantize applied to TokenStore rows at their hot prefix, :196-201;
+ *      for ladder streams scripts/kvtc.py:62-79 quantize_groups' dequantized
+ *      output, as read back by scripts/kvtc_storage.py:109-119) ----------
  * Tokens t0..t0+nt-1 of the stream -> out [nt][64G] in out_dtype.  With
- * DKV_F32 the values are bit-identical to the reference's fp32 dequantize. */
+ * DKV_F32 the values are bit-identical to the reference's fp32 dequantize
+ * (and DKV_F16 to its fp16 cast of it). */
 int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt, void* out, int32_t out_dtype,
                        void* stream);
 

@@ -2,7 +2,10 @@
 (oracle; test infrastructure only).
 
 Follows scripts/kvtc.py of the reference:
-- ``quantize_groups`` :62-79 (round half to even, fp16 low/scale)
+- ``quantize_groups`` :62-79 (round half to even, fp16 low/scale), split into
+  ``quantize_groups_codes`` (the integer codes and fp16 low/scale that
+  scripts/kvtc_storage.py:63-73 stores) and ``dequantize_codes``
+  (code * scale + low, scripts/kvtc.py:78 and kvtc_storage.py:119)
 - ``rung_bytes``      :82-85
 - ``allocate_rungs``  :277-298 (fp64 values, cummin along levels, *stable*
   descending sort, take the sorted prefix whose cumulative cost fits)
@@ -10,7 +13,8 @@ Follows scripts/kvtc.py of the reference:
 Pins (tests/test_oracle_kvtc_scoring_packing.py): allocate_rungs against an exhaustive
 brute force of the same greedy rule on tiny inputs, against the invariants
 (budget respected, per-slot upgrades form a prefix), and against torch's
-stable sort on random inputs; quantize_groups against its closed-form grid.
+stable sort on random inputs; quantize_groups against its closed-form grid
+and against dequantize_codes(quantize_groups_codes(.)) bit for bit.
 """
 
 from __future__ import annotations
@@ -38,6 +42,42 @@ def quantize_groups(coefficients: np.ndarray, bits: np.ndarray, group: int) -> n
         q = np.clip(np.rint((part - low) / scale), 0, 2**width - 1).astype(np.float32)
         out[:, chosen] = (q * scale).astype(np.float32) + low
     return out.reshape(tokens, features)
+
+
+def quantize_groups_codes(coefficients: np.ndarray, bits: np.ndarray, group: int):
+    """The integer side of kvtc.py:62-79: codes u8 [tokens, groups, group], low and scale f16
+    [tokens, groups] (scripts/kvtc_storage.py:70-73); groups with 0 bits get zeros."""
+    x = coefficients.astype(np.float32)
+    tokens, features = x.shape
+    groups = features // group
+    grouped = x.reshape(tokens, groups, group)
+    codes = np.zeros((tokens, groups, group), np.uint8)
+    low16 = np.zeros((tokens, groups), np.float16)
+    scale16 = np.zeros((tokens, groups), np.float16)
+    for width in BIT_OPTIONS[1:]:
+        chosen = np.nonzero(bits == width)[0]
+        if chosen.size == 0:
+            continue
+        part = grouped[:, chosen]
+        lo = part.min(axis=-1, keepdims=True).astype(np.float16)
+        sc = np.maximum((part.max(axis=-1, keepdims=True) - lo.astype(np.float32)) / np.float32(2**width - 1),
+                        np.float32(1e-8)).astype(np.float16)
+        q = np.clip(np.rint((part - lo.astype(np.float32)) / sc.astype(np.float32)), 0, 2**width - 1)
+        codes[:, chosen] = q.astype(np.uint8)
+        low16[:, chosen] = lo[..., 0]
+        scale16[:, chosen] = sc[..., 0]
+    return codes, low16, scale16
+
+
+def dequantize_codes(codes: np.ndarray, low: np.ndarray, scale: np.ndarray, bits: np.ndarray) -> np.ndarray:
+    """code * scale + low in float32, product and sum rounded separately (kvtc.py:78); 0 where a
+    group has 0 bits.  ``bits`` is [groups] or [tokens, groups]."""
+    c = codes.astype(np.float32)
+    prod = (c * scale.astype(np.float32)[..., None]).astype(np.float32)
+    out = (prod + low.astype(np.float32)[..., None]).astype(np.float32)
+    b = np.broadcast_to(bits, low.shape)
+    out[b == 0] = 0.0
+    return out.reshape(codes.shape[0], -1)
 
 
 def rung_bytes(bits: np.ndarray, group: int) -> int:

@@ -26,9 +26,18 @@ Layout of one stream ("DKV1"):
   (rotr(OR_p(word_p & mask(p, w)), w) has byte i = code of coefficient 4w+i
   truncated to the present planes).
 
+kvtc ladder streams (the ``dkvtc@`` entry point; ``pack_ladder``): token t at
+rung r has one blob of ``rung_bytes[r]`` bytes: for every group with b > 0
+bits, in group order, ``[low f16][scale f16][64 codes of b bits]``, the codes
+LSB-first (code j at bit b*j of the code bytes: the bit order of
+scripts/kvtc_storage.py:21-27 ``_pack``, applied to one (token, group) at a
+time, which is whole bytes since 64b is a multiple of 8).
+
 Pins (tests/test_oracle_kvtc_scoring_packing.py): per-plane bit positions are
 a bijection, pack/unpack round-trips, both tiers' byte sizes equal the
-reference's counts, and the lane formula above rebuilds the truncated codes.
+reference's counts, and the lane formula above rebuilds the truncated codes;
+ladder code bytes against hand-computed bytes and numpy.packbits(bitorder=
+"little") of each code's bits, blob sizes against kvtc_ref.rung_bytes.
 """
 
 from __future__ import annotations
@@ -131,3 +140,36 @@ def unpack(blob: np.ndarray, offsets: np.ndarray, pieces: np.ndarray, order: Ord
                 acc |= (word_codes(word, p) << (7 - p)).astype(np.uint8)
             codes[t, g] = acc
     return codes, low, span, order.planes[np.asarray(pieces, dtype=np.int64)]
+
+
+def ladder_segment_offsets(bits: np.ndarray, group: int = 64) -> np.ndarray:
+    """Byte offset of group g's segment in a token blob at rung r: [R, G]."""
+    seg = np.where(bits > 0, HEADER_BYTES + bits * group // 8, 0).astype(np.int64)
+    off = np.zeros_like(seg)
+    off[:, 1:] = np.cumsum(seg[:, :-1], axis=1)
+    return off
+
+
+def pack_ladder_codes(codes64: np.ndarray, width: int) -> bytes:
+    """64 codes of ``width`` bits, LSB-first: code j occupies bits width*j .. width*j+width-1."""
+    out = bytearray(len(codes64) * width // 8)
+    for j, c in enumerate(codes64.astype(np.int64)):
+        bit = width * j
+        out[bit // 8] |= (int(c) & ((1 << width) - 1)) << (bit % 8)
+    return bytes(out)
+
+
+def pack_ladder(codes: np.ndarray, low: np.ndarray, scale: np.ndarray, rung: np.ndarray, bits: np.ndarray,
+                group: int = 64):
+    """codes u8 [n, G, 64], low/scale f16 [n, G], rung [n] (rows of ``bits`` [R, G]) -> (blob u8,
+    offsets int64 [n+1])."""
+    parts, offsets = [], [0]
+    for t in range(codes.shape[0]):
+        row = bits[rung[t]]
+        blob = bytearray()
+        for g in np.nonzero(row > 0)[0]:
+            blob += _header_bytes(low[t, g], scale[t, g])
+            blob += pack_ladder_codes(codes[t, g], int(row[g]))
+        parts.append(bytes(blob))
+        offsets.append(offsets[-1] + len(blob))
+    return np.frombuffer(b"".join(parts), np.uint8).copy(), np.asarray(offsets, np.int64)

@@ -112,3 +112,22 @@ def test_kvtc_methods_on_cpu(name):
         got = codec.last_coefficients["value"][torch.from_numpy(rows)].numpy()
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"rung {r}"
     assert out.token_bytes.shape == (tokens,)
+
+
+def test_ladder_tables_match_oracle():
+    """Ladder segment offsets and rung sizes (scripts/kvtc.py:82-85) and the checks on bad tables."""
+    import hot_tier
+    from oracle import packing_ref
+
+    bits = synth.ladder_rungs(8)
+    sizes = [kvtc_ref.rung_bytes(b.numpy(), 64) for b in bits]
+    t = hot_tier.LadderTables(bits, sizes, "cpu")
+    assert t.rungs == len(bits) + 1 and t.empty == len(bits)
+    assert np.array_equal(t.seg_off.numpy()[:-1], packing_ref.ladder_segment_offsets(bits.numpy()))
+    assert np.array_equal(t.sizes64.numpy()[:-1], sizes) and int(t.sizes64[-1]) == 0
+    with pytest.raises(ValueError, match="rung_bytes"):
+        hot_tier.LadderTables(bits, [s + 4 for s in sizes], "cpu")
+    with pytest.raises(ValueError, match="bit widths"):
+        hot_tier.LadderTables(bits * 0 + 3, None, "cpu")
+    with pytest.raises(ValueError, match="groups of 64"):
+        hot_tier.LadderTables(bits, None, "cpu", group=32)

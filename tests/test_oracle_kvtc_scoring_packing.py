@@ -212,3 +212,57 @@ def test_pack_unpack_and_tier_sizes():
         k = pieces[t]
         sizes = np.where(order.planes[k] > 0, 4 + 8 * order.planes[k].astype(int), 0)
         assert np.array_equal(seg[k], np.concatenate([[0], np.cumsum(sizes)[:-1]]))
+
+
+def test_ladder_code_bytes_known_answers_and_packbits():
+    """LSB-first code packing (scripts/kvtc_storage.py:21-27 bit order) on hand-computed bytes and
+    against numpy.packbits(bitorder="little") of each code's bits."""
+    assert packing_ref.pack_ladder_codes(np.tile([0, 1, 2, 3], 16), 2) == bytes([0xE4]) * 16
+    assert packing_ref.pack_ladder_codes(np.tile([1, 2], 32), 4) == bytes([0x21]) * 32
+    assert packing_ref.pack_ladder_codes(np.arange(64), 8) == bytes(range(64))
+    rng = np.random.default_rng(11)
+    for width in (2, 4, 8):
+        codes = rng.integers(0, 2**width, 64)
+        bits = ((codes[:, None] >> np.arange(width)) & 1).astype(np.uint8).reshape(-1)
+        want = np.packbits(bits, bitorder="little").tobytes()
+        assert packing_ref.pack_ladder_codes(codes, width) == want
+
+
+def test_quantize_groups_codes_dequantize_and_shipped_torch():
+    """quantize_groups == dequantize_codes(quantize_groups_codes) bit for bit, and the shipped
+    torch codes (kvtc.quantize_groups_codes) equal the oracle's."""
+    import kvtc
+
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((50, 4 * 64)) * np.array([3.0, 0.5, 1e-3, 7.0]).repeat(64)).astype(np.float32)
+    bits = np.array([8, 0, 2, 4])
+    codes, low, scale = kvtc_ref.quantize_groups_codes(x, bits, 64)
+    assert codes[:, 0].max() <= 255 and codes[:, 2].max() <= 3 and codes[:, 3].max() <= 15
+    assert not codes[:, 1].any()
+    deq = kvtc_ref.dequantize_codes(codes, low, scale, bits)
+    assert np.array_equal(deq.view(np.uint32), kvtc_ref.quantize_groups(x, bits, 64).view(np.uint32))
+    c, lo, sc = kvtc.quantize_groups_codes(torch.from_numpy(x), torch.from_numpy(bits), 64)
+    assert np.array_equal(c.numpy(), codes)
+    assert np.array_equal(lo.numpy().view(np.uint16), low.view(np.uint16))
+    assert np.array_equal(sc.numpy().view(np.uint16), scale.view(np.uint16))
+
+
+def test_pack_ladder_sizes_and_offsets():
+    rng = np.random.default_rng(13)
+    bits = np.array([[2, 0, 0, 0], [4, 2, 0, 2], [8, 4, 2, 0], [8, 8, 8, 8]])
+    n = 30
+    codes = rng.integers(0, 256, (n, 4, 64)).astype(np.uint8)
+    low = rng.standard_normal((n, 4)).astype(np.float16)
+    scale = np.abs(rng.standard_normal((n, 4))).astype(np.float16)
+    rung = rng.integers(0, 4, n)
+    masked = codes & ((1 << bits[rung]) - 1).astype(np.uint8)[..., None]
+    blob, off = packing_ref.pack_ladder(masked, low, scale, rung, bits)
+    assert np.array_equal(np.diff(off), [kvtc_ref.rung_bytes(bits[r], 64) for r in rung])
+    seg = packing_ref.ladder_segment_offsets(bits)
+    for t in range(n):
+        for g in np.nonzero(bits[rung[t]])[0]:
+            s = off[t] + seg[rung[t], g]
+            assert blob[s:s + 2].view(np.float16)[0] == low[t, g]
+            width = bits[rung[t], g]
+            body = blob[s + 4:s + 4 + 8 * width].tobytes()
+            assert body == packing_ref.pack_ladder_codes(masked[t, g], width)
