@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", default="cfg2", choices=["cfg0", "cfg1", "cfg2", "cfg3"])
+    p.add_argument("--method", default="prog", choices=["prog", "dkvtc"],
+                   help="entry point whose cache is decoded: prog@b:r0.01 (bit planes, default) or "
+                        "dkvtc@b:snap:floor1 (kvtc ladder codes; cfg1/cfg2)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-question", action="store_true", help="skip the question stage (score, select, gather)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
@@ -158,7 +161,15 @@ def main():
     torch.manual_seed(0)
     dev = "cuda"
     t_build = time.perf_counter()
-    if args.config == "cfg3":
+    if args.method == "dkvtc":
+        if args.config not in ("cfg1", "cfg2"):
+            print("--method dkvtc runs at cfg1 or cfg2", file=sys.stderr)
+            sys.exit(2)
+        w = workloads.build_dkvtc(args.config, device=dev)
+        args.no_cpu_baseline = True
+        if args.traffic_file == str(ROOT / "profiles" / "keys_scores_cfg2_traffic.txt"):
+            args.traffic_file = str(ROOT / "profiles" / f"keys_scores_{args.config}_dkvtc_traffic.txt")
+    elif args.config == "cfg3":
         w = workloads.build_ragged(device=dev)
     else:
         w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline,
@@ -229,13 +240,15 @@ def main():
             "workload": {"cfg2": "Llama-3.2-3B shape, 16384-token context at 3% budget, 28-layer decode",
                          "cfg1": "Llama-3.2-1B shape, 8192-token context at 2% budget, 16-layer decode",
                          "cfg0": "Llama-3.2-1B shape, 1500-token context, 16-layer decode",
-                         "cfg3": "32 ragged Llama-3.2-3B conversations U[2K,16K] at 3%, one varlen decode"}[args.config],
+                         "cfg3": "32 ragged Llama-3.2-3B conversations U[2K,16K] at 3%, one varlen decode"}[args.config]
+                        + (f", {w.name.split(':', 1)[1]} (kvtc ladder codes)" if args.method == "dkvtc" else ""),
             "config": args.config,
+            "method": "dkvtc@b:snap:floor1" if args.method == "dkvtc" else "prog@b:r0.01",
             "compressed_tokens": w.middle_total,
             "exact_tokens_per_seq": list(w.exact_lengths)[:4],
             "batch": w.batch,
             "layers": L,
-            "rank": w.shape.rank,
+            "rank": w.tables.rank,
             "hot_code_bytes": w.hot_code_bytes(),
             "parallelism": "single GPU",
         },

@@ -328,15 +328,17 @@ def order_checkpoint(shape: ModelShape, model_id: str = "synthetic/llama-3.2") -
     return {"model": model_id, "key": dict(entry), "value": dict(entry)}
 
 
-def prefill_cache(ctx: "SyntheticContext", coef_middle: dict | None = None, device="cpu", dtype=torch.float16):
+def prefill_cache(ctx: "SyntheticContext", coef_middle: dict | None = None, device="cpu", dtype=torch.float16,
+                  compute_device="cpu"):
     """Per-layer keys/values [1, Hkv, T, d] of a whole conversation (sinks, middle, recent), keys RoPE'd:
-    what a prefill leaves in a DynamicCache (scripts/common.py:62-67)."""
+    what a prefill leaves in a DynamicCache (scripts/common.py:62-67).  ``compute_device`` is where
+    the float32 decode runs (the context's tensors must live there)."""
     s = ctx.shape
     coef_middle = ctx.coef if coef_middle is None else coef_middle
-    cos, sin = rope_tables(s, ctx.tokens, "cpu")
-    coef = {kind: torch.cat([ctx.exact_coef[kind][:ctx.start].cpu(), coef_middle[kind].cpu(),
-                             ctx.exact_coef[kind][ctx.start:].cpu()]) for kind in ("key", "value")}
-    keys, values = decode_exact(ctx, coef, torch.arange(ctx.tokens), cos, sin)
+    cos, sin = rope_tables(s, ctx.tokens, compute_device)
+    coef = {kind: torch.cat([ctx.exact_coef[kind][:ctx.start].to(compute_device), coef_middle[kind].to(compute_device),
+                             ctx.exact_coef[kind][ctx.start:].to(compute_device)]) for kind in ("key", "value")}
+    keys, values = decode_exact(ctx, coef, torch.arange(ctx.tokens, device=compute_device), cos, sin)
     return ([keys[l][None].to(device=device, dtype=dtype) for l in range(s.layers)],
             [values[l][None].to(device=device, dtype=dtype) for l in range(s.layers)])
 

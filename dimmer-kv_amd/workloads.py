@@ -84,23 +84,26 @@ class DecodeWorkload:
 
     # ---- algorithmic work of one decode step (all layers) ----
     def hot_code_bytes(self) -> int:
-        return sum(int(s.tables.prefix64[s.pieces.long()].sum()) for s in self.streams.values())
+        """Packed code bytes the step reads (bit-plane prefixes, or ladder rung blobs)."""
+        return sum(int(s.tables.prefix64[s.pieces.long()].sum()) if isinstance(s, PackedStream) else s.hot_bytes()
+                   for s in self.streams.values())
 
     def bytes_per_layer(self) -> int:
         s = self.shape
-        basis = 2 * s.rank * s.kv_heads * s.head_dim * 2  # fp16 key + value basis slices
+        basis = 2 * self.tables.rank * s.kv_heads * s.head_dim * 2  # fp16 key + value basis slices
         return self.hot_code_bytes() + basis
 
     def k2_flops_per_layer(self) -> int:
         s = self.shape
         n = self.middle_total
-        return 2 * n * s.rank * s.kv_heads * s.head_dim + 2 * n * s.q_heads * self.q_len * s.head_dim
+        return 2 * n * self.tables.rank * s.kv_heads * s.head_dim + 2 * n * s.q_heads * self.q_len * s.head_dim
 
     def flops_per_layer(self) -> int:
         s = self.shape
         n = self.middle_total
         rows = s.q_heads * self.q_len
-        return (self.k2_flops_per_layer() + 2 * rows * n * s.rank + 2 * rows * self.batch * s.rank * s.head_dim)
+        r = self.tables.rank
+        return self.k2_flops_per_layer() + 2 * rows * n * r + 2 * rows * self.batch * r * s.head_dim
 
     @property
     def middle_total(self) -> int:
@@ -210,6 +213,59 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
         w.question = QuestionStage.build(w, ctx, seed + 70, refine_fraction)
     # drop the float32 device bases now that the fp16 kernel layouts exist
     ctx.basis.clear()
+    w.synthetic = ctx
+    return w
+
+
+def build_dkvtc(name: str = "cfg2", seed: int = 2024, device="cuda", budget: float | None = None,
+                method: str | None = None, query_dtype: torch.dtype | None = None) -> DecodeWorkload:
+    """The ``dkvtc@<budget>:snap:floor1`` decode workload at a config's shape, built through the
+    reference entry points: a synthetic prefill cache (fp16), ``Methods.apply`` (KVTCCodec.compress
+    with per-token rungs, synthetic snap importance, floor at the finest affordable uniform rung),
+    then ``CompressedContext(codec, keys, values, model)`` over the packed ladder codes.  The exact
+    cache of each layer is the middle tokens kept at the exact rung, the sinks and recent window,
+    and one new token."""
+    import methods
+
+    shape, tokens, b0, qd0 = CONFIGS[name]
+    budget = b0 if budget is None else budget
+    query_dtype = query_dtype or qd0
+    method = method or f"dkvtc@{budget}:snap:floor1"
+    ctx = synth.make_context(shape, tokens, seed, device=device)
+    model = synth.RopeModel(shape, device)
+    kvtc_ck = synth.kvtc_checkpoint(ctx)
+    keys, values = synth.prefill_cache(ctx, device=device, dtype=torch.float16, compute_device=device)
+    g = torch.Generator("cpu").manual_seed(seed + 80)
+    scores = {"snap": [torch.rand(shape.kv_heads, tokens, generator=g).to(device) for _ in range(shape.layers)]}
+    m = methods.Methods("synthetic/llama-3.2", device=device, model=model, kvtc=kvtc_ck)
+    m.apply(method, keys, values, scores)
+    codec = m.codec("kvtc")
+    context = CompressedContext(codec, keys, values, model)
+    del keys, values
+    cos, sin = synth.rope_tables(shape, tokens + 1, device)
+    new_coef = {kind: synth.coefficients(1, shape.rank, seed + 50 + i, device)
+                for i, kind in enumerate(("key", "value"))}
+    new_k, new_v = synth.decode_exact(ctx, new_coef, torch.tensor([tokens], device=device), cos, sin)
+    ke, ve = [], []
+    for layer in range(shape.layers):
+        exact = context.exact_cache.layers[layer]
+        parts_k = [exact.keys[0].float(), new_k[layer]]
+        parts_v = [exact.values[0].float(), new_v[layer]]
+        if context.extra is not None:
+            parts_k.insert(0, context.extra["key"][layer])
+            parts_v.insert(0, context.extra["value"][layer])
+        ke.append(torch.cat(parts_k, dim=1))
+        ve.append(torch.cat(parts_v, dim=1))
+    key_exact = torch.stack(ke).contiguous()
+    value_exact = torch.stack(ve).contiguous()
+    queries = synth.make_queries(shape, 1, seed + 60, device, query_dtype)
+    outs = torch.empty(shape.layers, 1, 1, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
+    streams = {"key": context.key, "value": context.value}
+    w = DecodeWorkload(name + ":" + method, shape, context, context.tables, streams, queries, key_exact, value_exact,
+                       outs, tokens=tokens, middle=context.key.n, exact_lengths=(key_exact.shape[2],))
+    w.args = [context.layer_args(l, queries[l], outs[l], key_exact[l], value_exact[l]) for l in range(shape.layers)]
+    w.workspace = context.workspace(w.args[0])
+    w.codec = codec
     w.synthetic = ctx
     return w
 

@@ -76,3 +76,51 @@ def test_cfg2_question_then_decode_matches_oracle():
         torch.cuda.synchronize()
         err, fro = assert_close(out32.cpu().numpy(), ref, what=f"cfg2 layer {layer}", base=base)
         print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+
+
+def test_cfg2_dkvtc_decode_matches_oracle():
+    """The dkvtc@0.03:snap:floor1 entry point at full size: prefill -> Methods.apply ->
+    CompressedContext(codec, keys, values, model) -> 28-layer decode over the ladder codes,
+    deterministic, and equal to the oracle's attention over codec.last_coefficients on layers
+    spread over the model."""
+    import workloads
+    from helpers import assert_close
+    from oracle import attention_ref
+
+    print("[case] full-size cfg2: dkvtc decode step", flush=True)
+    w = workloads.build_dkvtc("cfg2", device=DEV)
+    s, codec, ctx = w.shape, w.codec, w.context
+    start, _ = codec.last_span
+    choice_k = codec.last_choice["key"].cpu().numpy()
+    kept = choice_k >= 0
+    n_extra = 0 if ctx.extra is None else ctx.extra["key"][0].shape[1]
+    print(f"  coded tokens {ctx.key.n}, exact-rung tokens {n_extra}, ladder groups {ctx.tables.rank // 64}",
+          flush=True)
+    w.step()
+    torch.cuda.synchronize()
+    first = w.outs.clone()
+    w.step()
+    torch.cuda.synchronize()
+    assert torch.equal(first, w.outs)
+    coef = {k: codec.last_coefficients[k].float().cpu().numpy()[kept] for k in ("key", "value")}
+    pos = np.nonzero(kept)[0] + start
+    cos = w.tables.rope_cos.cpu().numpy()[pos]
+    sin = w.tables.rope_sin.cpu().numpy()[pos]
+    cos, sin = np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
+    wd = s.kv_heads * s.head_dim
+    for layer in (0, 13, 27):
+        basis = {k: codec.streams[k].basis[layer * wd:(layer + 1) * wd].T.cpu().numpy() for k in ("key", "value")}
+        mean = {k: codec.streams[k].mean[layer * wd:(layer + 1) * wd].cpu().numpy() for k in ("key", "value")}
+        ref = attention_ref.attend(w.queries[layer].float().cpu().numpy(), coef["key"], coef["value"], basis["key"],
+                                   basis["value"], mean["key"], mean["value"], cos, sin,
+                                   w.key_exact[layer][None, :, n_extra:].cpu().numpy(),
+                                   w.value_exact[layer][None, :, n_extra:].cpu().numpy())
+        base = np.broadcast_to(np.repeat(mean["value"].reshape(s.kv_heads, 1, -1), s.gqa, axis=1)
+                               .reshape(1, 1, s.q_heads, -1), ref.shape)
+        assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"dkvtc layer {layer} (bf16 out)", rel_fro=1e9)
+        out32 = torch.empty(1, 1, s.q_heads, s.head_dim, dtype=torch.float32, device=DEV)
+        args = ctx.layer_args(layer, w.queries[layer], out32, w.key_exact[layer], w.value_exact[layer])
+        ctx.run_layer(args)
+        torch.cuda.synchronize()
+        err, fro = assert_close(out32.cpu().numpy(), ref, what=f"dkvtc layer {layer}", base=base)
+        print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
