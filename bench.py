@@ -45,7 +45,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-question", action="store_true", help="skip the question stage (score, select, gather)")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
-    p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "keys_scores_cfg2_traffic.txt"))
+    p.add_argument("--traffic-file", default=None,
+                   help="rocprofv3 FETCH/WRITE summary of K2 for this workload "
+                        "(default profiles/keys_scores_<config>[_dkvtc]_traffic.txt)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -160,6 +162,9 @@ def main():
 
     torch.manual_seed(0)
     dev = "cuda"
+    if args.traffic_file is None:
+        suffix = "_dkvtc" if args.method == "dkvtc" else ""
+        args.traffic_file = str(ROOT / "profiles" / f"keys_scores_{args.config}{suffix}_traffic.txt")
     t_build = time.perf_counter()
     if args.method == "dkvtc":
         if args.config not in ("cfg1", "cfg2"):
@@ -167,8 +172,6 @@ def main():
             sys.exit(2)
         w = workloads.build_dkvtc(args.config, device=dev)
         args.no_cpu_baseline = True
-        if args.traffic_file == str(ROOT / "profiles" / "keys_scores_cfg2_traffic.txt"):
-            args.traffic_file = str(ROOT / "profiles" / f"keys_scores_{args.config}_dkvtc_traffic.txt")
     elif args.config == "cfg3":
         w = workloads.build_ragged(device=dev)
     else:

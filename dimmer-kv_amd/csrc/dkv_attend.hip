@@ -103,6 +103,18 @@ DKV_DEVICE int slot_token(const DecodeArgs& a, int slot) {
   return n < a.cu_seqlens[bt.x + 1] - tok0 ? tok0 + n : -1;
 }
 
+// The value side's per-step buffers are blocked by 16 slots so that a wave's
+// MFMA operand loads are whole cache lines:
+//   value codes    u8   [G][n_slots/16][64 components][16 slots]
+//   probabilities  fp16 [n_slots/16][R_total rows][16 slots]
+DKV_DEVICE long vcode_index(int g, int c, long slot, int n_slots) {
+  return (((long)g * (n_slots >> 4) + (slot >> 4)) * 64 + c) * 16 + (slot & 15);
+}
+
+DKV_DEVICE long prob_index(long row, long slot, int R_total) {
+  return ((slot >> 4) * R_total + row) * 16 + (slot & 15);
+}
+
 // ---------------------------------------------------------------------------
 // K1 (fp16 operand form): decode the hot key codes of every token into the
 // exact register image of a 32x32x16 MFMA operand: for 64-component group g,
@@ -318,7 +330,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       const float x = xs[hw][r][lhi];
       const float p = (x == -INFINITY) ? 0.0f : __expf(x - M);
       const int n = tq * 64 + lhi * 32 + l32;
-      a.probs[(long)((h0 + hl) * RH + r) * a.n_slots + (long)tile * kTileTok + n] = f16_bits(p);
+      a.probs[prob_index((long)(h0 + hl) * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len)] = f16_bits(p);
     }
   }
 }
@@ -596,7 +608,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
       for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
       const long r_all = (long)(h0 + hl) * RH + row;
       const float x = n < count ? a.scores[r_all * a.n_total + tok0 + n] : -INFINITY;
-      a.probs[r_all * a.n_slots + (long)tile * kTileTok + n] = f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
+      a.probs[prob_index(r_all, (long)tile * kTileTok + n, a.Hq * a.q_len)] =
+          f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
     }
     __syncthreads();
   }
@@ -613,10 +626,10 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 }
 
 struct K3aArgs {
-  const uint8_t* vcodes;  // decoded value codes, u8 [G][64][n_slots] (slot-contiguous per component)
+  const uint8_t* vcodes;  // decoded value codes, u8 [G][n_slots/16][64][16] (vcode_index)
   const float2* vaff;     // (scale, offset) per (group, token): value = code * scale + offset
   const int32_t* cu_seqlens;
-  const uint16_t* probs;  // fp16 exp(score - tile max), [R][n_slots]
+  const uint16_t* probs;  // fp16 exp(score - tile max), [n_slots/16][R][16] (prob_index)
   const float* tile_max;
   float* w_part;
   int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
@@ -642,11 +655,12 @@ DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, 
 
 // ---------------------------------------------------------------------------
 // K1 for the value side: every token's value codes (all hot planes) as 8-bit
-// codes, transposed to [G][64][n_slots] so that an MFMA operand (one
-// component, 8 consecutive slots) is one 8-byte load, plus the per-(group,
-// slot) affine form (scale = span / 256, offset = low + span * 2^-(m+1); 0 and
-// 0 for a group without planes or a padding slot).  One block = 128 slots x
-// one group.
+// codes, transposed to [G][n_slots/16][64][16] so that an MFMA operand (one
+// component, 8 consecutive slots) is one 8-byte load and a wave's 32
+// components of one 16-slot block are 512 contiguous bytes, plus the
+// per-(group, slot) affine form (scale = span / 256, offset = low + span *
+// 2^-(m+1); 0 and 0 for a group without planes or a padding slot).  One block
+// = 128 slots x one group, whose codes are one contiguous 8 KB run.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
   __shared__ uint32_t tile[64][kDecodeTok / 4 + 1];  // [component][slot / 4], bytes of 4 slots per word
@@ -699,19 +713,19 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArg
 #pragma unroll
     for (int i = 0; i < 4; ++i) tb8[(half * 32 + 4 * w + i) * ROWB + tl] = (uint8_t)(cw[w] >> (8 * i));
   __syncthreads();
-  // 64 components x 128 tokens: thread -> component c, 32 tokens
-  const int c = threadIdx.x >> 2, q = threadIdx.x & 3;
-  uint4 v;
-  v.x = tile[c][q * 8 + 0];
-  v.y = tile[c][q * 8 + 1];
-  v.z = tile[c][q * 8 + 2];
-  v.w = tile[c][q * 8 + 3];
-  uint4 v2;
-  v2.x = tile[c][q * 8 + 4];
-  v2.y = tile[c][q * 8 + 5];
-  v2.z = tile[c][q * 8 + 6];
-  v2.w = tile[c][q * 8 + 7];
-  uint4* dst = (uint4*)(vcodes + ((long)g * 64 + c) * a.n_slots + sb * kDecodeTok + q * 32);
+  // 8 blocks of 16 slots x 64 components = 8 KB contiguous: thread k writes bytes 32k .. 32k+31,
+  // the 16 slots of block k / 32 for components 2 (k % 32) and 2 (k % 32) + 1
+  const int blk = threadIdx.x >> 5, c = 2 * (threadIdx.x & 31);
+  uint4 v, v2;
+  v.x = tile[c][blk * 4 + 0];
+  v.y = tile[c][blk * 4 + 1];
+  v.z = tile[c][blk * 4 + 2];
+  v.w = tile[c][blk * 4 + 3];
+  v2.x = tile[c + 1][blk * 4 + 0];
+  v2.y = tile[c + 1][blk * 4 + 1];
+  v2.z = tile[c + 1][blk * 4 + 2];
+  v2.w = tile[c + 1][blk * 4 + 3];
+  uint4* dst = (uint4*)(vcodes + vcode_index(g, c, (long)sb * kDecodeTok + blk * 16, a.n_slots));
   dst[0] = v;
   dst[1] = v2;
 }
@@ -780,19 +794,24 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   // value codes for all 8 steps; the row maxima come from the tile statistics meanwhile.
   const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
   const float4 aff2 = *(const float4*)(aff + wt0 + 2 * lane);
-  const uint16_t* prow = a.probs + (long)(row_ok ? my_row : 0) * a.n_slots + slot0;
-  const uint8_t* col0 = a.vcodes + ((long)g * 64 + l32) * a.n_slots + slot0;
-  const uint8_t* col1 = col0 + 32L * a.n_slots;
+  // step st covers slots slot0 + wt0 + 16 st .. +16 (one 16-slot block): the wave's probability
+  // rows are 1 KB and each half of its code operand 512 B of contiguous memory
+  const uint16_t* prow = a.probs + prob_index(row_ok ? my_row : 0, slot0 + wt0, a.R_total) + lhi * 8;
+  const uint8_t* col0 = a.vcodes + vcode_index(g, l32, slot0 + wt0, a.n_slots) + lhi * 8;
+  const uint8_t* col1 = col0 + 32 * 16;
   constexpr int STEPS = kK3WaveTok / 16;  // 8
   half8 pt[STEPS];
   uint2 c0[STEPS], c1[STEPS];
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
-    const int t8 = wt0 + st * 16 + lhi * 8;
-    pt[st] = *(const half8*)(prow + t8);
-    c0[st] = *(const uint2*)(col0 + t8);
-    c1[st] = *(const uint2*)(col1 + t8);
+    pt[st] = *(const half8*)(prow + (long)st * a.R_total * 16);
+    c0[st] = *(const uint2*)(col0 + st * 64 * 16);
+    c1[st] = *(const uint2*)(col1 + st * 64 * 16);
   }
+  // this wave's 128 tokens lie in one tile; its maximum for this lane's row (read now, used once
+  // the row maxima are known)
+  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
+  const float mt = (row_ok && wt0 < count) ? a.tile_max[(long)my_row * a.ntiles + tile] : -INFINITY;
   *(float4*)&saff[wave][2 * lane] = aff2;
   if (tid < 256) {
     const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
@@ -810,14 +829,9 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     for (int v = 0; v < 16; ++v) acc[nb][v] = 0.0f;
   float osum = 0.0f;
 
-  // K2 left p~ = exp(s - tile max) in fp16; the wave's 128 tokens lie in one tile, whose
-  // factor f = exp(tile max - row max) turns p~ into p = exp(s - row max).
-  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
-  float f = 0.0f;
-  if (row_ok && wt0 < count) {
-    const float mt = a.tile_max[(long)my_row * a.ntiles + tile];
-    f = (mt == -INFINITY) ? 0.0f : __expf(mt - my_M);
-  }
+  // K2 left p~ = exp(s - tile max) in fp16; the tile's factor f = exp(tile max - row max) turns
+  // p~ into p = exp(s - row max).
+  const float f = (mt == -INFINITY) ? 0.0f : __expf(mt - my_M);
   // every load above stayed inside the slot buffers (they extend a whole split past the last
   // tile); slots past the split's tokens get p = 0 by selection, whatever they hold
 #pragma unroll

@@ -27,6 +27,10 @@ CONFIGS = {
     "cfg1": (synth.SHAPE_1B, 8192, 0.02, torch.bfloat16),
     "cfg2": (synth.SHAPE_3B, 16384, 0.03, torch.bfloat16),
 }
+# At 8K tokens the 36 exact tokens alone take 22 % of a 2 % budget, which leaves less than the
+# 2-plane floor (640 B/token K+V at rank 1024); config 1 quotes its budget per compressed token
+# (655.36 B/token = the floor plus top-ups), so its plane maps are drawn against that.
+BUDGET_OVER_MIDDLE = {"cfg1"}
 
 
 @dataclass
@@ -185,7 +189,8 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
         shape, tokens = shape or s0, tokens or t0
         budget = b0 if budget is None else budget
         query_dtype = query_dtype or qd0
-    ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device)
+    ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device,
+                             budget_over_middle=name in BUDGET_OVER_MIDDLE)
     capacity = int(round(refine_fraction * ctx.middle)) + 1 if refine_fraction > 0 else 0
     streams = _pack_streams(ctx.coef, ctx.planes, shape, device, capacity)
     cos, sin = synth.rope_tables(shape, tokens + max(q_len, 64), device)
