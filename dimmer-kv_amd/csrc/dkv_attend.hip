@@ -57,13 +57,24 @@ DKV_DEVICE uint16_t f16_bits(float v) {
 
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
 
+// 8 consecutive query elements (idx a multiple of 8) as fp16, with one or two vector loads.
 DKV_DEVICE half8 load_query8(const void* q, long idx, int dtype) {
   half8 r;
   if (dtype == DKV_F16) {
     r = *(const half8*)((const half_t*)q + idx);
-  } else {
+  } else if (dtype == DKV_BF16) {
+    const uint4 v = *(const uint4*)((const uint16_t*)q + idx);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (half_t)load_as_float(q, idx + i, dtype);
+    for (int i = 0; i < 4; ++i) {
+      r[2 * i] = (half_t)__uint_as_float(w[i] << 16);
+      r[2 * i + 1] = (half_t)__uint_as_float(w[i] & 0xffff0000u);
+    }
+  } else {
+    const float4 a = *(const float4*)((const float*)q + idx);
+    const float4 b = *(const float4*)((const float*)q + idx + 4);
+    r[0] = (half_t)a.x; r[1] = (half_t)a.y; r[2] = (half_t)a.z; r[3] = (half_t)a.w;
+    r[4] = (half_t)b.x; r[5] = (half_t)b.y; r[6] = (half_t)b.z; r[7] = (half_t)b.w;
   }
   return r;
 }
@@ -1379,9 +1390,10 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
 // ===========================================================================
 // K4a: question scoring of the hot tier (scripts/progressive.py:239-254 with
 // scripts/dimmer.py:52-66).  Per layer: K2 scores every (query head, query
-// position) row against the compressed keys; exact_stats adds the softmax
-// mass of the exact context tokens and of the question's own keys (causal);
-// importance_part accumulates sum over rows of p = exp(s - M) / L per token;
+// position) row against the compressed keys; row_stats merges the tiles'
+// softmax statistics with those of the exact context tokens and of the
+// question's own keys (causal); importance_part accumulates sum over rows of
+// p = exp(s - M) / L per token;
 // importance_add folds the row-chunk partials into importance[n] in a fixed
 // order, so results do not depend on scheduling.
 // ===========================================================================
@@ -1390,70 +1402,100 @@ namespace {
 constexpr int kRowChunk = 64;  // rows per importance_part workgroup
 constexpr int kTokChunk = 256;
 
-struct ExactStatsArgs {
+struct RowStatsArgs {
   const void* query;
   const float* key_exact;     // [Hkv][E][D]
   const float* key_question;  // [Hkv][Lq][D]
-  float* stat;                // [R_total][2] (max, sum exp)
+  const float* tile_max;      // [R_total][ntiles] (compressed part, from K2)
+  const float* tile_sum;
+  float* stat;                // [R_total][2]: softmax maximum M and 1 / L over every key of the row
   float scaling;
-  int Hkv, Hq, q_len, D, E, query_dtype;
+  int Hkv, Hq, q_len, D, E, query_dtype, ntiles;
 };
 
-__global__ __launch_bounds__(128) void exact_stats_kernel(ExactStatsArgs a) {
+constexpr int kStatKeysPerThread = 16;  // keys per thread kept in registers (more are recomputed)
+
+// One workgroup per (query head, query position) row: the softmax statistics over the
+// compressed tokens (merged from K2's per-tile maxima and sums), the exact context tokens and
+// the question's own keys up to this position (causal).
+__global__ __launch_bounds__(128) void row_stats_kernel(RowStatsArgs a) {
   __shared__ float q[128];
-  __shared__ float red[128];
+  __shared__ float red[2][2];
   const int row = blockIdx.x;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int gq = a.Hq / a.Hkv;
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
   const int D = a.D;
   if (tid < D) q[tid] = load_as_float(a.query, ((long)qh * a.q_len + qi) * D + tid, a.query_dtype);
+  // compressed part: online merge of this thread's tiles
+  float mc = -INFINITY, lc = 0.0f;
+  for (int t = tid; t < a.ntiles; t += 128) {
+    const float mt = a.tile_max[(long)row * a.ntiles + t], st = a.tile_sum[(long)row * a.ntiles + t];
+    if (mt == -INFINITY) continue;
+    if (mt > mc) {
+      lc = lc * __expf(mc - mt) + st;
+      mc = mt;
+    } else {
+      lc += st * __expf(mt - mc);
+    }
+  }
   __syncthreads();
   const int nkeys = a.E + qi + 1;  // exact context tokens + question keys 0..qi
-  float m = -INFINITY;
-  for (int j = tid; j < nkeys; j += 128) {
-    const float* kr = j < a.E ? a.key_exact + ((long)h * a.E + j) * D
-                              : a.key_question + ((long)h * a.q_len + (j - a.E)) * D;
+  float dots[kStatKeysPerThread];
+  float me = -INFINITY;
+  for (int k = 0, j = tid; j < nkeys; ++k, j += 128) {
+    const float4* kr = (const float4*)(j < a.E ? a.key_exact + ((long)h * a.E + j) * D
+                                               : a.key_question + ((long)h * a.q_len + (j - a.E)) * D);
     float dot = 0.0f;
-    for (int d = 0; d < D; ++d) dot += q[d] * kr[d];
-    m = fmaxf(m, dot * a.scaling);
+    for (int i = 0; i < D / 4; i += 8) {
+      float4 k4[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) k4[u] = kr[i + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        dot += q[4 * (i + u)] * k4[u].x + q[4 * (i + u) + 1] * k4[u].y + q[4 * (i + u) + 2] * k4[u].z +
+               q[4 * (i + u) + 3] * k4[u].w;
+    }
+    dot *= a.scaling;
+    if (k < kStatKeysPerThread) dots[k] = dot;
+    me = fmaxf(me, dot);
   }
-  red[tid] = m;
+  // joint maximum over both parts, then the sum of exponentials
+  float m = fmaxf(me, mc);
+  m = wave_max(m);
+  if (lane == 0) red[0][wave] = m;
   __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
-    __syncthreads();
+  const float M = fmaxf(red[0][0], red[0][1]);
+  float l = (mc == -INFINITY || M == -INFINITY) ? 0.0f : lc * __expf(mc - M);
+  for (int k = 0, j = tid; j < nkeys; ++k, j += 128) {
+    float dot;
+    if (k < kStatKeysPerThread) {
+      dot = dots[k];
+    } else {
+      const float* kr = j < a.E ? a.key_exact + ((long)h * a.E + j) * D
+                                : a.key_question + ((long)h * a.q_len + (j - a.E)) * D;
+      dot = 0.0f;
+      for (int d = 0; d < D; ++d) dot += q[d] * kr[d];
+      dot *= a.scaling;
+    }
+    l += __expf(dot - M);
   }
-  const float M = red[0];
+  l = wave_sum(l);
+  if (lane == 0) red[1][wave] = l;
   __syncthreads();
-  float l = 0.0f;
-  for (int j = tid; j < nkeys; j += 128) {
-    const float* kr = j < a.E ? a.key_exact + ((long)h * a.E + j) * D
-                              : a.key_question + ((long)h * a.q_len + (j - a.E)) * D;
-    float dot = 0.0f;
-    for (int d = 0; d < D; ++d) dot += q[d] * kr[d];
-    l += __expf(dot * a.scaling - M);
-  }
-  red[tid] = l;
-  __syncthreads();
-  for (int s = 64; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
-    __syncthreads();
-  }
   if (tid == 0) {
+    const float L = red[1][0] + red[1][1];
     a.stat[2 * row] = M;
-    a.stat[2 * row + 1] = red[0];
+    a.stat[2 * row + 1] = L > 0.0f ? 1.0f / L : 0.0f;
   }
 }
 
 struct ImportanceArgs {
   const float* scores;  // [R_total][n]
-  const float* tile_max;
-  const float* tile_sum;
-  const float* stat;    // [R_total][2] exact-part (max, sum exp)
+  const float* stat;    // [R_total][2] (M, 1 / L) of every row (row_stats_kernel)
   float* part;          // [nrc][n]
-  int R_total, n, ntiles;
+  int R_total, n;
 };
 
 __global__ __launch_bounds__(kTokChunk) void importance_part_kernel(ImportanceArgs a) {
@@ -1464,28 +1506,9 @@ __global__ __launch_bounds__(kTokChunk) void importance_part_kernel(ImportanceAr
   const int tid = threadIdx.x;
   const int r0 = rc * kRowChunk;
   const int nr = min(kRowChunk, a.R_total - r0);
-  const int lane = tid & 63, wave = tid >> 6;
-  for (int r = wave; r < nr; r += kTokChunk / 64) {
-    const int row = r0 + r;
-    const float* tm = a.tile_max + (long)row * a.ntiles;
-    const float* ts = a.tile_sum + (long)row * a.ntiles;
-    float Mc = -INFINITY;
-    for (int t = lane; t < a.ntiles; t += 64) Mc = fmaxf(Mc, tm[t]);
-    Mc = wave_max(Mc);
-    float Lc = 0.0f;
-    if (Mc != -INFINITY)
-      for (int t = lane; t < a.ntiles; t += 64)
-        if (tm[t] != -INFINITY) Lc += ts[t] * __expf(tm[t] - Mc);
-    Lc = wave_sum(Lc);
-    if (lane == 0) {
-      const float Me = a.stat[2 * row], Le = a.stat[2 * row + 1];
-      const float M = fmaxf(Mc, Me);
-      float L = 0.0f;
-      if (Mc != -INFINITY) L += Lc * __expf(Mc - M);
-      if (Me != -INFINITY) L += Le * __expf(Me - M);
-      Mr[r] = M;
-      invL[r] = L > 0.0f ? 1.0f / L : 0.0f;
-    }
+  if (tid < nr) {
+    Mr[tid] = a.stat[2 * (r0 + tid)];
+    invL[tid] = a.stat[2 * (r0 + tid) + 1];
   }
   __syncthreads();
   const int tok = tc * kTokChunk + tid;
@@ -1645,10 +1668,12 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   hipStream_t st = dkv::as_stream(stream);
   rc = launch_keys_scores(a, S.base, ws, st, /*probs=*/false);
   if (rc) return rc;
-  ExactStatsArgs e{};
+  RowStatsArgs e{};
   e.query = a->query;
   e.key_exact = a->key_exact;
   e.key_question = key_question;
+  e.tile_max = (const float*)(ws + S.base.tile_max);
+  e.tile_sum = (const float*)(ws + S.base.tile_sum);
   e.stat = (float*)(ws + S.stat);
   e.scaling = a->scaling;
   e.Hkv = a->kv_heads;
@@ -1657,20 +1682,18 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   e.D = a->head_dim;
   e.E = E;
   e.query_dtype = a->query_dtype;
-  hipLaunchKernelGGL(exact_stats_kernel, dim3(S.base.R_total), dim3(128), 0, st, e);
-  rc = dkv::check_launch("exact_stats");
+  e.ntiles = S.base.ntiles;
+  hipLaunchKernelGGL(row_stats_kernel, dim3(S.base.R_total), dim3(128), 0, st, e);
+  rc = dkv::check_launch("row_stats");
   if (rc) return rc;
   const int n = S.base.n_total;
   if (n == 0) return DKV_OK;
   ImportanceArgs im{};
   im.scores = (const float*)(ws + S.base.scores);
-  im.tile_max = (const float*)(ws + S.base.tile_max);
-  im.tile_sum = (const float*)(ws + S.base.tile_sum);
   im.stat = (const float*)(ws + S.stat);
   im.part = (float*)(ws + S.part);
   im.R_total = S.base.R_total;
   im.n = n;
-  im.ntiles = S.base.ntiles;
   const int ntc = (n + kTokChunk - 1) / kTokChunk;
   hipLaunchKernelGGL(importance_part_kernel, dim3(ntc * S.nrc), dim3(kTokChunk), 0, st, im);
   rc = dkv::check_launch("importance_part");
