@@ -110,3 +110,72 @@ def test_encode_then_attend_over_codes():
     base = np.broadcast_to(np.repeat(ctx.mean["value"][layer * w:(layer + 1) * w].numpy().reshape(shape.kv_heads, 1, -1),
                                      shape.gqa, axis=1).reshape(1, 1, shape.q_heads, -1), ref.shape)
     assert_close(out.cpu().numpy(), ref, what="encode->attend", base=base)
+
+
+def test_cfg4_fullsize_encode_bit_exact():
+    """Config 4 at full size: Llama-3.2-3B shape, 16,384 tokens, 3 % budget, 2-plane floor.  quantize8
+    bit for bit, the error table to float32 summation order, the allocation bit for bit on the GPU's
+    errors (floor offset as scripts/kvtc.py:209-219), packed tiers byte for byte on sampled tokens,
+    every tier size and the budget by the reference's byte formulas."""
+    import time
+
+    import kvtc
+    import progressive
+
+    shape = synth.SHAPE_3B
+    tokens = 16384
+    print("[case] cfg4 full-size encode (3B, 16384 tokens, 3 %, 2-plane floor)", flush=True)
+    ctx = synth.make_context(shape, tokens, seed=4040, device=DEV)
+    model = synth.RopeModel(shape, DEV)
+    codec = progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), synth.order_checkpoint(shape), DEV, model)
+    keys, values = synth.prefill_cache(ctx, device=DEV, dtype=torch.float16, compute_device=DEV)
+    order = pr.plane_major_order(shape.groups)
+    floor = order.rungs.index(2 * shape.groups)  # the rung holding 2 planes of every group
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    stored = codec.encode(keys, values, 0.03, 32, floor_rung=floor)
+    torch.cuda.synchronize()
+    print(f"  encode {1e3 * (time.perf_counter() - t0):.1f} ms", flush=True)
+    start, end = stored.start, stored.end
+    middle = end - start
+    cos, sin = kvtc.rope_tables(model, tokens, DEV)
+    rng = np.random.default_rng(4)
+    sample = np.sort(rng.choice(middle, 256, replace=False))
+    for kind in ("key", "value"):
+        coef = codec.stream_coefficients(kind, keys if kind == "key" else values, cos, sin, start, end)
+        c_np = coef.float().cpu().numpy()
+        codes, low, span = pr.quantize8(c_np, 64)
+        g_codes, g_low, g_span = codec.last_quantized[kind]
+        assert np.array_equal(g_codes.cpu().numpy(), codes), f"{kind}: quantize8 codes"
+        assert np.array_equal(g_low.cpu().numpy().view(np.uint16), low.view(np.uint16))
+        assert np.array_equal(g_span.cpu().numpy().view(np.uint16), span.view(np.uint16))
+        table = codec.error_table(coef, g_codes, g_low, g_span).cpu().numpy()
+        np.testing.assert_allclose(table, pr.error_table(c_np, codes, low, span), rtol=2e-5, atol=1e-9)
+        del coef, c_np, table
+        pieces = stored.stores[kind].hot_pieces.cpu().numpy()
+        assert (pieces >= order.rungs[floor]).all(), f"{kind}: a token below the 2-plane floor"
+        packed = stored.stores[kind].packed
+        hot, hot_off, cold, cold_off = packing_ref.pack(codes[sample], low[sample], span[sample], pieces[sample], order)
+        blob = packed.blob.cpu().numpy()
+        tok_off = packed.tok_off.cpu().numpy()
+        cblob = packed.cold.cpu().numpy()
+        ctok = packed.cold_off.cpu().numpy()
+        for i, t in enumerate(sample):
+            assert np.array_equal(blob[tok_off[t]:tok_off[t] + hot_off[i + 1] - hot_off[i]], hot[hot_off[i]:hot_off[i + 1]])
+            assert np.array_equal(cblob[ctok[t]:ctok[t] + cold_off[i + 1] - cold_off[i]], cold[cold_off[i]:cold_off[i + 1]])
+        assert np.array_equal(np.diff(np.append(tok_off, packed.hot_used)), order.prefix_bytes[pieces])
+    # allocation: the reference rule over levels[floor:] on the GPU's float32 errors
+    errors = codec.last_errors.float().cpu().numpy()
+    levels = len(order.rungs)
+    kept = [b for i, b in enumerate(codec.last_level_bytes) if i % levels >= floor]
+    remaining = stored.budget_bytes - (tokens - middle) * 2 * codec.exact_bytes
+    want = kvtc_ref.allocate_rungs(errors[:, floor:], np.array(kept), middle, remaining) + floor
+    assert np.array_equal(codec.last_chosen.cpu().numpy(), want)
+    orders = {"key": order, "value": order}
+    pieces = {k: stored.stores[k].hot_pieces.cpu().numpy() for k in ("key", "value")}
+    assert stored.hot_bytes == pr.hot_bytes(orders, pieces, tokens - middle, shape.exact_bytes)
+    assert stored.cold_bytes == pr.cold_bytes(orders, pieces)
+    assert stored.hot_bytes <= stored.budget_bytes
+    print(f"  hot {stored.hot_bytes} B of budget {stored.budget_bytes} B, cold {stored.cold_bytes} B; "
+          f"mean planes K {np.mean(pieces['key']) / shape.groups:.2f}, V {np.mean(pieces['value']) / shape.groups:.2f}",
+          flush=True)
