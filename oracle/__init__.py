@@ -7,14 +7,17 @@ answer-time path so that the HIP kernels can be checked against it:
                     transformers/modeling_rope_utils.py:621-662)
 - ``progressive_ref`` quantize8 / dequantize / order and byte accounting
                     (scripts/progressive.py:32-236)
-- ``kvtc_ref``      allocate_rungs / quantize_groups (scripts/kvtc.py:62-79, 277-298)
+- ``kvtc_ref``      allocate_rungs / quantize_groups and its integer codes
+                    (scripts/kvtc.py:62-79, 277-298; scripts/kvtc_storage.py:63-73, 119)
 - ``attention_ref`` CompressedContext.attend math and an independent fp64
                     decode-then-attend (scripts/compressed_attention.py:105-137)
 - ``scoring_ref``   question_importance + top-k selection
                     (scripts/progressive.py:239-254, scripts/dimmer.py:45-77,
                     scripts/methods.py:244-248)
-- ``packing_ref``   the packed hot/cold bit-plane layout this build defines
-                    (its byte totals follow scripts/progressive.py:185-194, 232)
+- ``packing_ref``   the packed hot/cold bit-plane layout and the per-token kvtc
+                    ladder layout this build defines (byte totals follow
+                    scripts/progressive.py:185-194, 232 and scripts/kvtc.py:82-85;
+                    ladder code bits LSB-first as scripts/kvtc_storage.py:21-27)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker. The product
