@@ -206,18 +206,35 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   const int l32 = lane & 31, lhi = lane >> 5;
   const int gq = a.Hq / a.Hkv;
 
-  // stage RoPE rows of the tile's tokens and the query rows of the workgroup's heads
+  // stage RoPE rows of the tile's tokens and the query rows of the workgroup's heads.  The loads
+  // of a batch go out together (indices clamped to the tile's last token, padding rows replaced
+  // afterwards), so the staging costs two memory round trips per batch, not one per row.
   constexpr int V4_PER_ROW = HALF_D / 4;
-  for (int e = tid; e < kTileTok * V4_PER_ROW; e += kK2Threads) {
-    const int n = e / V4_PER_ROW, c = e % V4_PER_ROW;
-    float4 cv = make_float4(1.f, 1.f, 1.f, 1.f), sv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (n < count) {
-      const long pos = a.positions[tok0 + n];
-      cv = *(const float4*)(a.rope_cos + pos * HALF_D + 4 * c);
-      sv = *(const float4*)(a.rope_sin + pos * HALF_D + 4 * c);
+  constexpr int STAGE_ITERS = kTileTok * V4_PER_ROW / kK2Threads;  // 8 (D = 128) or 4 (D = 64)
+  constexpr int STAGE_BATCH = 4;
+#pragma unroll
+  for (int i0 = 0; i0 < STAGE_ITERS; i0 += STAGE_BATCH) {
+    long pos[STAGE_BATCH];
+#pragma unroll
+    for (int i = 0; i < STAGE_BATCH; ++i) {
+      const int n = (tid + (i0 + i) * kK2Threads) / V4_PER_ROW;
+      pos[i] = a.positions[tok0 + min(n, count - 1)];
     }
-    *(float4*)(cs + n * CSTR + 4 * c) = cv;
-    *(float4*)(sn + n * CSTR + 4 * c) = sv;
+    float4 cv[STAGE_BATCH], sv[STAGE_BATCH];
+#pragma unroll
+    for (int i = 0; i < STAGE_BATCH; ++i) {
+      const int c = (tid + (i0 + i) * kK2Threads) % V4_PER_ROW;
+      cv[i] = *(const float4*)(a.rope_cos + pos[i] * HALF_D + 4 * c);
+      sv[i] = *(const float4*)(a.rope_sin + pos[i] * HALF_D + 4 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < STAGE_BATCH; ++i) {
+      const int e = tid + (i0 + i) * kK2Threads;
+      const int n = e / V4_PER_ROW, c = e % V4_PER_ROW;
+      const bool ok = n < count;
+      *(float4*)(cs + n * CSTR + 4 * c) = ok ? cv[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+      *(float4*)(sn + n * CSTR + 4 * c) = ok ? sv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
   }
   for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
     const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
@@ -653,9 +670,9 @@ DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, 
     const float* tm = tile_max + (long)row * ntiles + tb0;
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (sub + 8 * i < ntb) ? tm[sub + 8 * i] : -INFINITY;
+    for (int i = 0; i < 8; ++i) v[i] = tm[min(sub + 8 * i, ntb - 1)];  // unconditional: issued together
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, v[i]);
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, sub + 8 * i < ntb ? v[i] : -INFINITY);
     for (int t = sub + 64; t < ntb; t += 8) m = fmaxf(m, tm[t]);
   }
   m = fmaxf(m, __shfl_xor(m, 1, 64));
@@ -886,7 +903,6 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 // sequence's splits, multiply once by the value-basis chunk [128][D].
 // ---------------------------------------------------------------------------
 constexpr int kMaxExact = 1024;
-constexpr int kMaxSplitsUnrolled = 32;
 
 struct K3bArgs {
   const int32_t* cu_seqlens;
@@ -920,13 +936,15 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
     for (int e = tid; e < nr * kChunk; e += 256) {
       const int rr = e / kChunk, i = e % kChunk;
       const float* src = a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + rr) * a.rank + c * kChunk + i;
-      float v[kMaxSplitsUnrolled];
-#pragma unroll
-      for (int sp = 0; sp < kMaxSplitsUnrolled; ++sp) v[sp] = sp < nsp ? src[sp * sp_stride] : 0.0f;
+      // splits in batches of 8 whose loads go out together (indices clamped, extras masked)
       float s = 0.0f;
+      for (int s0 = 0; s0 < nsp; s0 += 8) {
+        float v[8];
 #pragma unroll
-      for (int sp = 0; sp < kMaxSplitsUnrolled; ++sp) s += v[sp];
-      for (int sp = kMaxSplitsUnrolled; sp < nsp; ++sp) s += src[sp * sp_stride];
+        for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, nsp - 1) * sp_stride];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += s0 + k < nsp ? v[k] : 0.0f;
+      }
       W[rr][i] = s;
     }
     __syncthreads();
@@ -935,7 +953,7 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
     for (int rr = 0; rr < 8; ++rr) acc0[rr] = acc1[rr] = 0.0f;
     uint32_t bw[kChunk / 4];
 #pragma unroll
-    for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = ii < ilen ? bv[(long)(part * ilen + ii) * npair + dp] : 0u;
+    for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = bv[(long)(part * ilen + min(ii, ilen - 1)) * npair + dp];
 #pragma unroll
     for (int ii = 0; ii < kChunk / 4; ++ii) {
       if (ii >= ilen) break;
@@ -997,6 +1015,8 @@ struct K3cArgs {
   int batch, layer, Hkv, Hq, q_len, D, R_total, nchunks, E_total, query_dtype, out_dtype, ntiles;
 };
 
+constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
+
 __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
   __shared__ float q[128];
   __shared__ float se[kMaxExact];
@@ -1012,54 +1032,89 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
   const int h = qh / gq;
   const int e0 = a.cu_exact ? a.cu_exact[b] : 0;
   const int E = a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
+  const int d = tid % D, part = tid / D, parts = 256 / D;
+  // Every global load of the first 64 exact tokens goes out in one round, before any wait: each
+  // dependent round trip to memory costs microseconds here, and this kernel is nothing but them.
+  // (1) the tiles' softmax statistics (wave 0), (2) the query, (3) this thread's share of the
+  // chunk partials, (4) a quarter key row (token tid / 4, 32 dimensions), (5) exact values.
+  float mm = -INFINITY, ll = 0.0f;
   if (wave == 0) {
     const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
     const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
     const float* tm = a.tile_max + (long)row * a.ntiles + tb0;
     const float* ts = a.tile_sum + (long)row * a.ntiles + tb0;
-    float m = -INFINITY;
-    for (int t = lane; t < ntb; t += 64) m = fmaxf(m, tm[t]);
-    m = wave_max(m);
-    float l = 0.0f;
-    if (m != -INFINITY)
-      for (int t = lane; t < ntb; t += 64)
-        if (tm[t] != -INFINITY) l += ts[t] * __expf(tm[t] - m);
-    l = wave_sum(l);
+    for (int t = lane; t < ntb; t += 64) {  // online merge of this lane's tiles
+      const float mt = tm[t], st = ts[t];
+      if (mt == -INFINITY) continue;
+      if (mt > mm) {
+        ll = ll * __expf(mm - mt) + st;
+        mm = mt;
+      } else {
+        ll += st * __expf(mt - mm);
+      }
+    }
+  }
+  if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
+  const int my_chunks = (a.nchunks - part + parts - 1) / parts;
+  float vparts[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = part + min(i, max(my_chunks - 1, 0)) * parts;
+    vparts[i] = my_chunks > 0 ? a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d] : 0.0f;
+  }
+  const int kj = tid >> 2, ks = tid & 3;
+  const bool kslice = ks * 32 < D;
+  float4 k4[8];
+  float mval = 0.0f;
+  if (E > 0) {
+    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
+                                       min(ks * 32, D - 32));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
+  }
+  float vv[kExactVB];
+#pragma unroll
+  for (int i = 0; i < kExactVB; ++i)
+    vv[i] = E > 0 ? a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d] : 0.0f;
+  // the chunk partials beyond the first batch (many components only)
+  float vc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vc += i < my_chunks ? vparts[i] : 0.0f;
+  for (int i = 8; i < my_chunks; ++i) vc += a.out_part[(((long)(part + i * parts) * a.batch + b) * a.R_total + row) * D + d];
+  if (wave == 0) {
+    const float m = wave_max(mm);
+    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
     if (lane == 0) {
       bc[0] = m;
       bc[1] = l;
     }
   }
-  if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
-  // the thread's share of the chunk partials (independent of the softmax)
-  const int d = tid % D, part = tid / D, parts = 256 / D;
-  float vparts[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int c = part + i * parts;
-    vparts[i] = c < a.nchunks ? a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d] : 0.0f;
-  }
-  float vc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) vc += vparts[i];
-  for (int c = part + 16 * parts; c < a.nchunks; c += parts)
-    vc += a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d];
   __syncthreads();
-  // exact scores: one token per thread
+  // exact scores: four lanes per token, 32 dimensions each, 64 tokens per pass
   float me = -INFINITY;
-  for (int j = tid; j < E; j += 256) {
-    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D);
-    float4 k4[32];
+  const int E64 = (E + 63) & ~63;
+  for (int j = kj; j < E64; j += 64) {
+    if (j != kj && j < E) {
+      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
 #pragma unroll
-    for (int i = 0; i < 32; ++i) k4[i] = i < D / 4 ? kr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+      if (a.mask) mval = a.mask[(long)qi * E + j];
+    }
     float dot = 0.0f;
+    if (kslice) {
+      const float* qr = q + ks * 32;
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
-      if (i < D / 4) dot += q[4 * i] * k4[i].x + q[4 * i + 1] * k4[i].y + q[4 * i + 2] * k4[i].z + q[4 * i + 3] * k4[i].w;
-    float s = dot * a.scaling;
-    if (a.mask) s += a.mask[(long)qi * E + j];
-    se[j] = s;
-    me = fmaxf(me, s);
+      for (int i = 0; i < 8; ++i)
+        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    if (j < E) {
+      const float sc = dot * a.scaling + mval;
+      if (ks == 0) se[j] = sc;
+      me = fmaxf(me, sc);
+    }
   }
   me = wave_max(me);
   if (lane == 0) wred[0][wave] = me;
@@ -1079,19 +1134,21 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
   __syncthreads();
   const float Le = wred[1][0] + wred[1][1] + wred[1][2] + wred[1][3];
   const float denom = ec * Lc + Le;
-  // exact values: thread (d, part) takes tokens part, part + parts, ... in batches of 8
+  // exact values: thread (d, part) takes tokens part, part + parts, ...
   float ve = 0.0f;
-  for (int j0 = part; j0 < E; j0 += 8 * parts) {
-    float vv[8];
+#pragma unroll
+  for (int i = 0; i < kExactVB; ++i) {
+    const int j = part + i * parts;
+    if (j < E) ve += se[j] * vv[i];
+  }
+  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
+    float v8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = j0 + i * parts;
-      vv[i] = j < E ? a.value_exact[((long)h * a.E_total + e0 + j) * D + d] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = j0 + i * parts;
-      if (j < E) ve += se[j] * vv[i];
+      if (j < E) ve += se[j] * v8[i];
     }
   }
   buf[0][tid] = vc;
