@@ -192,7 +192,7 @@ constexpr int kSmallRows = 4;
 template <int D>
 DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
                                            float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
-                                           int tile, int h0, int b, int RH) {
+                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs) {
   constexpr int HPW = 256 / D;
   constexpr int DB = D / 32;
   constexpr int HALF_BLK = DB / 2;
@@ -200,15 +200,13 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   constexpr int CSTR = HALF_D + 4;  // floats per staged RoPE row (keeps b128 reads conflict-free)
   float* cs = (float*)lds_h;                 // [256][CSTR] cos
   float* sn = cs + kTileTok * CSTR;          // [256][CSTR] sin
-  float* qs = sn + kTileTok * CSTR;          // [HPW][kSmallRows][D] query rows
+  // pos_s (the tile's positions) and qs ([HPW][kSmallRows][D] query rows) were staged at kernel start
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tq = wave & 3, hs = wave >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int gq = a.Hq / a.Hkv;
 
-  // stage RoPE rows of the tile's tokens and the query rows of the workgroup's heads.  The loads
-  // of a batch go out together (indices clamped to the tile's last token, padding rows replaced
-  // afterwards), so the staging costs two memory round trips per batch, not one per row.
+  // stage RoPE rows of the tile's tokens (positions from LDS; the loads of a batch go out together,
+  // padding rows replaced afterwards)
   constexpr int V4_PER_ROW = HALF_D / 4;
   constexpr int STAGE_ITERS = kTileTok * V4_PER_ROW / kK2Threads;  // 8 (D = 128) or 4 (D = 64)
   constexpr int STAGE_BATCH = 4;
@@ -216,10 +214,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   for (int i0 = 0; i0 < STAGE_ITERS; i0 += STAGE_BATCH) {
     long pos[STAGE_BATCH];
 #pragma unroll
-    for (int i = 0; i < STAGE_BATCH; ++i) {
-      const int n = (tid + (i0 + i) * kK2Threads) / V4_PER_ROW;
-      pos[i] = a.positions[tok0 + min(n, count - 1)];
-    }
+    for (int i = 0; i < STAGE_BATCH; ++i) pos[i] = pos_s[(tid + (i0 + i) * kK2Threads) / V4_PER_ROW];
     float4 cv[STAGE_BATCH], sv[STAGE_BATCH];
 #pragma unroll
     for (int i = 0; i < STAGE_BATCH; ++i) {
@@ -235,12 +230,6 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       *(float4*)(cs + n * CSTR + 4 * c) = ok ? cv[i] : make_float4(1.f, 1.f, 1.f, 1.f);
       *(float4*)(sn + n * CSTR + 4 * c) = ok ? sv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-  }
-  for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
-    const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
-    const int qh = (h0 + hl) * gq + r / a.q_len, qi = r % a.q_len;
-    qs[(hl * kSmallRows + r) * D + d] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + d,
-                                                      a.query_dtype);
   }
   __syncthreads();
 
@@ -380,6 +369,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __shared__ __attribute__((aligned(16))) half_t lds[2 * 2 * kTileTok * kStride];
   __shared__ float stat_m[HPW][4][32];
   __shared__ float stat_s[HPW][4][32];
+  __shared__ int pos_s[kTileTok];                  // the tile's RoPE positions (decode epilogue)
+  __shared__ float q_s[HPW * kSmallRows * D];      // the workgroup's query rows (decode epilogue)
 
   const int bid = blockIdx.x;
   const int lin = (bid & 7) * a.per_xcd + (bid >> 3);
@@ -396,6 +387,19 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tq = wave & 3, hs = wave >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
+  const int RH = (a.Hq / a.Hkv) * a.q_len;
+
+  // the decode epilogue's positions and query rows are fetched now, behind the main loop
+  if (RH <= kSmallRows) {
+    if (tid < kTileTok) pos_s[tid] = a.positions[tok0 + min(tid, count - 1)];
+    const int gq = a.Hq / a.Hkv;
+    for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
+      const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
+      const int qh = (h0 + hl) * gq + r / a.q_len, qi = r % a.q_len;
+      q_s[(hl * kSmallRows + r) * D + d] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + d,
+                                                         a.query_dtype);
+    }
+  }
 
   // Coefficient operands come straight from the decoded buffer (one 16-byte
   // load per lane per MFMA operand); the basis block [256][64] goes global ->
@@ -498,10 +502,9 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __syncthreads();
 
   const int gq = a.Hq / a.Hkv;
-  const int RH = gq * a.q_len;
   const int half_d = D / 2;
   if (RH <= kSmallRows) {
-    keys_scores_small_epilogue<D>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH);
+    keys_scores_small_epilogue<D>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s);
     return;
   }
 
@@ -951,6 +954,7 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
     float acc0[8], acc1[8];
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) acc0[rr] = acc1[rr] = 0.0f;
+    // (issued after the partial sums: putting these loads first measured slower)
     uint32_t bw[kChunk / 4];
 #pragma unroll
     for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = bv[(long)(part * ilen + min(ii, ilen - 1)) * npair + dp];
