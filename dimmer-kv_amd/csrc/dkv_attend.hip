@@ -209,7 +209,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   // padding rows replaced afterwards)
   constexpr int V4_PER_ROW = HALF_D / 4;
   constexpr int STAGE_ITERS = kTileTok * V4_PER_ROW / kK2Threads;  // 8 (D = 128) or 4 (D = 64)
-  constexpr int STAGE_BATCH = 4;
+  constexpr int STAGE_BATCH = 4;  // (one round of 8 measured slower: the main loop's registers)
 #pragma unroll
   for (int i0 = 0; i0 < STAGE_ITERS; i0 += STAGE_BATCH) {
     long pos[STAGE_BATCH];
@@ -293,19 +293,16 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       float x[2];
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
-        const float full = part[hw][r][tb] + __shfl_xor(part[hw][r][tb], 32, 64);
+        const float full = sum_xor32(part[hw][r][tb]);  // the lane's and its partner's dimension halves
         const int n = tq * 64 + tb * 32 + l32;
         x[tb] = n < count ? full * a.scaling : -INFINITY;
         xs[hw][r][tb] = x[tb];
         if (tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
-      float mx = fmaxf(x[0], x[1]);
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      const float mx = max32(fmaxf(x[0], x[1]));
       float sm = 0.0f;
       if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+      sm = sum32(sm);
       if (lane == 0) {
         stat_m[hl][tq][r] = mx;
         stat_s[hl][tq][r] = sm;
@@ -593,13 +590,10 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
           x[tb] = ok ? sacc[tb][v] * a.scaling : -INFINITY;
           if (ok) a.scores[(long)(h * RH + row) * a.n_total + tok0 + n] = x[tb];
         }
-        float mx = fmaxf(x[0], x[1]);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        const float mx = max32(fmaxf(x[0], x[1]));
         float sm = 0.0f;
         if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+        sm = sum32(sm);
         if (l32 == 0) {
           const int rr = 8 * (v >> 2) + 4 * lhi + (v & 3);
           stat_m[hl][tq][rr] = mx;
@@ -678,10 +672,7 @@ DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, 
     for (int i = 0; i < 8; ++i) m = fmaxf(m, sub + 8 * i < ntb ? v[i] : -INFINITY);
     for (int t = sub + 64; t < ntb; t += 8) m = fmaxf(m, tm[t]);
   }
-  m = fmaxf(m, __shfl_xor(m, 1, 64));
-  m = fmaxf(m, __shfl_xor(m, 2, 64));
-  m = fmaxf(m, __shfl_xor(m, 4, 64));
-  return m;
+  return max8(m);
 }
 
 // ---------------------------------------------------------------------------
@@ -880,7 +871,7 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0[st].x, c0[st].y), acc[0], 0, 0, 0);
     acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1[st].x, c1[st].y), acc[1], 0, 0, 0);
   }
-  osum += __shfl_xor(osum, 32, 64);
+  osum = sum_xor32(osum);
   // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3)
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
@@ -1112,8 +1103,8 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
       for (int i = 0; i < 8; ++i)
         dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
     }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
+    dot += lane_xor1(dot);
+    dot += lane_xor2(dot);
     if (j < E) {
       const float sc = dot * a.scaling + mval;
       if (ks == 0) se[j] = sc;

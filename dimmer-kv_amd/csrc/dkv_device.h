@@ -243,14 +243,59 @@ DKV_DEVICE int2 find_tile(const int32_t* cu, int batch, int tile, int gid) {
   return make_int2(-1, 0);
 }
 
-DKV_DEVICE float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// ---------------------------------------------------------------------------
+// Cross-lane steps on the VALU (DPP and gfx950's permlane swaps) instead of
+// LDS-routed shuffles: each is a few cycles rather than an LDS round trip.
+// The DPP forms: quad_perm [1,0,3,2] = lane ^ 1, quad_perm [2,3,0,1] = lane ^ 2,
+// row_half_mirror = lane i <-> 7 - i within 8, row_mirror = i <-> 15 - i
+// within 16.  After the two quad steps every lane of a quad holds the quad's
+// reduction, so the mirrors then pair lanes of different quads (and halves of
+// a row): the four steps reduce a row of 16.  The permlane swaps exchange rows
+// (lane ^ 16) and wave halves (lane ^ 32); they return each lane's own value
+// and its partner's in an order that depends on the row, so they serve only
+// symmetric combinations (sum, max).
+// ---------------------------------------------------------------------------
+template <int CTRL>
+DKV_DEVICE float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+DKV_DEVICE float lane_xor1(float v) { return dpp_f32<0xB1>(v); }
+DKV_DEVICE float lane_xor2(float v) { return dpp_f32<0x4E>(v); }
+DKV_DEVICE float lane_half_mirror(float v) { return dpp_f32<0x141>(v); }
+DKV_DEVICE float lane_mirror(float v) { return dpp_f32<0x140>(v); }
+
+DKV_DEVICE float sum_xor16(float v) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+DKV_DEVICE float max_xor16(float v) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+DKV_DEVICE float sum_xor32(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+DKV_DEVICE float max_xor32(float v) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
-DKV_DEVICE float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// Reductions over groups of 8, 16 and 32 consecutive lanes (every lane of a group gets the result).
+DKV_DEVICE float max8(float v) {
+  v = fmaxf(v, lane_xor1(v));
+  v = fmaxf(v, lane_xor2(v));
+  return fmaxf(v, lane_half_mirror(v));
 }
+DKV_DEVICE float max16(float v) { v = max8(v); return fmaxf(v, lane_mirror(v)); }
+DKV_DEVICE float sum16(float v) {
+  v += lane_xor1(v);
+  v += lane_xor2(v);
+  v += lane_half_mirror(v);
+  return v + lane_mirror(v);
+}
+DKV_DEVICE float max32(float v) { return max_xor16(max16(v)); }
+DKV_DEVICE float sum32(float v) { return sum_xor16(sum16(v)); }
+
+DKV_DEVICE float wave_max(float v) { return max_xor32(max32(v)); }
+DKV_DEVICE float wave_sum(float v) { return sum_xor32(sum32(v)); }
