@@ -121,15 +121,33 @@ class CompressedContext:
         (inverse transform, RoPE) and attended as exact tokens.  The exact cache holds the sinks
         and the recent window (:85-88).  ``dtype`` is the reference's coefficient dtype; the
         kernels decode keys to fp16 MFMA operands and value codes exactly whatever it is."""
-        from common import build_cache
-        from kvtc import inverse_transform, rerotate, rope_tables
+        from kvtc import inverse_transform
 
         start, end = codec.last_span
-        tokens = keys[0].shape[2]
+        streams = codec.streams
+        choice = {k: codec.last_choice[k].to(codec.device) for k in ("key", "value")}
+
+        def promoted_rows(kind, idx):
+            return inverse_transform(codec.last_coefficients[kind][idx].float(), streams[kind], codec.group)
+
+        exact_keys = [torch.cat([k[..., :start, :], k[..., end:, :]], dim=2) for k in keys]
+        exact_values = [torch.cat([v[..., :start, :], v[..., end:, :]], dim=2) for v in values]
+        self._init_ladder(codec, model, dtype, start, end, keys[0].shape[2], choice, codec.last_codes, promoted_rows,
+                          exact_keys, exact_values)
+
+    def _init_ladder(self, codec, model, dtype, start: int, end: int, tokens: int, choice: dict, codes: dict,
+                     promoted_rows, exact_keys: list, exact_values: list):
+        """Context over kvtc ladder codes: ``choice`` holds each middle token's rung per stream
+        (-1 evicted, len(rung_bytes) exact), ``codes`` per stream (codes u8 [middle, G, 64], fp16
+        shifts and scales [middle, G]) at those rungs, ``promoted_rows(kind, idx)`` the pre-RoPE
+        matrix rows [len(idx), features] of middle tokens attended exactly, and ``exact_keys`` /
+        ``exact_values`` the per-layer sinks + recent window."""
+        from common import build_cache
+        from kvtc import rerotate, rope_tables
+
         device = codec.device
         layers, heads, dim, group = codec.layers, codec.heads, codec.head_dim, codec.group
         streams = codec.streams
-        choice = {k: codec.last_choice[k].to(device) for k in ("key", "value")}
         exact_rung = {k: len(streams[k].rung_bytes) for k in ("key", "value")}
         kept = choice["key"] >= 0
         promoted = kept & ((choice["key"] == exact_rung["key"]) | (choice["value"] == exact_rung["value"]))
@@ -151,11 +169,11 @@ class CompressedContext:
             rungs = torch.zeros(streams[kind].rungs.shape[0], padded, dtype=torch.long)
             rungs[:, :cols.numel()] = streams[kind].rungs.cpu()[:, cols.cpu()]
             table = LadderTables(rungs, None, device, group)
-            codes, low, scale = codec.last_codes[kind]
+            code, low, scale = codes[kind]
             c = torch.zeros(rows.numel(), padded, group, dtype=torch.uint8, device=device)
             lo = torch.zeros(rows.numel(), padded, dtype=torch.float16, device=device)
             sc = torch.zeros_like(lo)
-            c[:, :cols.numel()] = codes[rows][:, cols]
+            c[:, :cols.numel()] = code[rows][:, cols]
             lo[:, :cols.numel()] = low[rows][:, cols]
             sc[:, :cols.numel()] = scale[rows][:, cols]
             packed[kind] = LadderStream.pack(c, lo, sc, choice[kind][rows], table)
@@ -174,8 +192,7 @@ class CompressedContext:
         if idx.numel():
             extra = {}
             for kind in ("key", "value"):
-                matrix = inverse_transform(codec.last_coefficients[kind][idx].float(), streams[kind], group)
-                per_layer = matrix.view(-1, layers, heads, dim)
+                per_layer = promoted_rows(kind, idx).view(-1, layers, heads, dim)
                 parts = []
                 for layer in range(layers):
                     part = per_layer[:, layer].transpose(0, 1)  # [heads, E_x, d]
@@ -183,8 +200,6 @@ class CompressedContext:
                         part = rerotate(part, cos[start + idx], sin[start + idx])
                     parts.append(part.float().contiguous())
                 extra[kind] = parts
-        exact_keys = [torch.cat([k[..., :start, :], k[..., end:, :]], dim=2) for k in keys]
-        exact_values = [torch.cat([v[..., :start, :], v[..., end:, :]], dim=2) for v in values]
         self._init_streams(tables, packed["key"], packed["value"], rows + start,
                            model.config.num_attention_heads, exact_cache=build_cache(exact_keys, exact_values, model),
                            extra=extra)
@@ -357,36 +372,45 @@ class CompressedContext:
         dkv_hip.score_layer(args, key_question, self.importance, self._score_workspace)
 
 
+def _stops(token: int, tokenizer) -> bool:
+    return token == tokenizer.eos_token_id or token in tokenizer.all_special_ids
+
+
 def greedy_answer(model, tokenizer, context: CompressedContext | None, cache, input_ids: torch.Tensor,
                   start_position: int, max_new_tokens: int = 12, evicted=None, stop_at_eos: bool = True):
-    """Greedy decoding on top of a prefilled cache (scripts/compressed_attention.py:140-169).
+    """Greedy decoding on top of a prefilled cache (scripts/compressed_attention.py:140-169): at most
+    ``max_new_tokens`` forward passes, the first over ``input_ids`` (the question) at positions from
+    ``start_position``, each later one over the token the previous pass chose; an end-of-sequence or
+    special token ends the reply without being part of it (unless ``stop_at_eos`` is False).
 
-    With ``context`` set, attention runs over the compressed tokens directly and
-    ``cache`` must be ``context.exact_cache``.  Returns (text, first-step logits)."""
+    With ``context`` set, every attention call of the model runs over the compressed tokens directly
+    (the HIP decode kernels) and ``cache`` must be ``context.exact_cache``; otherwise ``cache`` is a
+    full cache with optional per-layer ``evicted`` masks.  Returns (text, first-step logits)."""
     import dimmer
 
     device = input_ids.device
+    reply: list[int] = []
+    first_logits = None
     dimmer.STATE.compressed = context
     dimmer.set_eviction(evicted)
-    generated, first_logits = [], None
     try:
-        ids = input_ids
-        position = start_position
+        feed, position = input_ids, start_position
         for _ in range(max_new_tokens):
-            positions = torch.arange(position, position + ids.shape[1], device=device)[None]
-            logits = model(input_ids=ids, past_key_values=cache, position_ids=positions, use_cache=True).logits
+            width = feed.shape[1]
+            step_positions = torch.arange(position, position + width, device=device).unsqueeze(0)
+            last = model(input_ids=feed, past_key_values=cache, position_ids=step_positions,
+                         use_cache=True).logits[0, -1]
             if first_logits is None:
-                first_logits = logits[0, -1].float()
-            position += ids.shape[1]
-            token = int(logits[0, -1].argmax())
-            if stop_at_eos and (token == tokenizer.eos_token_id or token in tokenizer.all_special_ids):
+                first_logits = last.float()
+            token = int(torch.argmax(last))
+            if stop_at_eos and _stops(token, tokenizer):
                 break
-            generated.append(token)
-            ids = torch.tensor([[token]], device=device)
+            reply.append(token)
+            feed, position = torch.full((1, 1), token, dtype=torch.long, device=device), position + width
     finally:
         dimmer.STATE.compressed = None
         dimmer.set_eviction(None)
-    return tokenizer.decode(generated, skip_special_tokens=True).strip(), first_logits
+    return tokenizer.decode(reply, skip_special_tokens=True).strip(), first_logits
 
 
 __all__ = ["ModelTables", "CompressedContext", "greedy_answer"]

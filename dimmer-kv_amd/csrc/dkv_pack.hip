@@ -167,6 +167,178 @@ extern "C" int dkv_pack_ladder(const uint8_t* codes, const uint16_t* low, const 
 }
 
 // ---------------------------------------------------------------------------
+// Byte storage.  One thread per (token, group, half): the half's 32 codes are
+// 4b bytes of the (token, group)'s code run, which starts at a byte boundary
+// (64 b-bit codes are 8b bytes), so halves never share a byte.  Storage
+// positions carry no alignment (the sections follow byte-sized rung ids), so
+// the storage side moves single bytes; the code/shift/scale side is aligned.
+// ---------------------------------------------------------------------------
+struct WireSpot {
+  long code, low, scale;  // byte positions of the half's codes and of the group's shift and scale
+  int b;                  // width, 0 = nothing to move
+};
+
+DKV_DEVICE int width_index(int b) { return b == 2 ? 0 : (b == 4 ? 1 : 2); }
+
+DKV_DEVICE WireSpot wire_spot(const int16_t* __restrict__ rung, const dkv_ladder_t& lad, const dkv_wire_t& w, int t,
+                              int g, int h) {
+  WireSpot s{0, 0, 0, 0};
+  const int G = lad.groups;
+  const int r = rung[t];
+  if (r < 0 || r >= lad.rungs) return s;
+  const int b = lad.bits[(long)r * G + g];
+  if (b != 2 && b != 4 && b != 8) return s;
+  const int wi = width_index(b);
+  const long cnt = w.count[r], nw = w.nwidth[3 * r + wi];
+  const long k = w.rank[t], j = w.slot[(long)r * G + g];
+  if (k < 0 || k >= cnt || j < 0 || j >= nw) return s;
+  const long base = w.section[3 * r + wi];
+  const long item = k * nw + j;
+  s.code = base + item * 8 * b + 4 * b * h;
+  s.low = base + cnt * nw * 8 * b + item * 2;
+  s.scale = base + cnt * nw * (8 * b + 2) + item * 2;
+  if (base < 0 || s.scale + 2 > w.bytes) return s;  // outside the storage buffer: leave it alone
+  s.b = b;
+  return s;
+}
+
+__global__ __launch_bounds__(256) void wire_pack_kernel(const uint8_t* __restrict__ codes,
+                                                        const uint16_t* __restrict__ low,
+                                                        const uint16_t* __restrict__ scale,
+                                                        const int16_t* __restrict__ rung, int n, dkv_ladder_t lad,
+                                                        dkv_wire_t w, uint8_t* __restrict__ out) {
+  const int G = lad.groups;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)n * G * 2) return;
+  const int h = (int)(id & 1);
+  const long tg = id >> 1;
+  const int t = (int)(tg / G), g = (int)(tg % G);
+  const WireSpot s = wire_spot(rung, lad, w, t, g, h);
+  if (s.b == 0) return;
+  const uint4* src = (const uint4*)(codes + tg * 64 + h * 32);
+  const uint4 c0 = src[0], c1 = src[1];
+  const uint32_t cw[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  uint32_t pw[8];
+  if (s.b == 8) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pw[k] = cw[k];
+  } else if (s.b == 4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      pw[k] = gather_nibbles(cw[2 * k] & 0x0f0f0f0fu) | (gather_nibbles(cw[2 * k + 1] & 0x0f0f0f0fu) << 16);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      uint32_t wv = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv |= gather_pairs(cw[4 * k + j] & 0x03030303u) << (8 * j);
+      pw[k] = wv;
+    }
+  }
+  uint8_t* dst = out + s.code;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)  // b words = 4b bytes
+    if (k < s.b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[4 * k + i] = (uint8_t)(pw[k] >> (8 * i));
+  if (h == 0) {
+    const uint16_t lo = low[tg], sc = scale[tg];
+    out[s.low] = (uint8_t)lo;
+    out[s.low + 1] = (uint8_t)(lo >> 8);
+    out[s.scale] = (uint8_t)sc;
+    out[s.scale + 1] = (uint8_t)(sc >> 8);
+  }
+}
+
+// The 32 codes of a half from its 4B storage bytes (code i at bit B*i), one code per byte of cw.
+template <int B>
+DKV_DEVICE void wire_codes_half(const uint8_t* __restrict__ src, uint32_t (&cw)[8]) {
+  uint32_t pw[B];
+#pragma unroll
+  for (int k = 0; k < B; ++k)
+    pw[k] = (uint32_t)src[4 * k] | ((uint32_t)src[4 * k + 1] << 8) | ((uint32_t)src[4 * k + 2] << 16) |
+            ((uint32_t)src[4 * k + 3] << 24);
+  constexpr uint32_t kMask = (1u << B) - 1u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {  // codes 4k .. 4k+3
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int bit = (4 * k + i) * B;
+      v |= ((pw[bit >> 5] >> (bit & 31)) & kMask) << (8 * i);
+    }
+    cw[k] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void wire_unpack_kernel(const uint8_t* __restrict__ in,
+                                                          const int16_t* __restrict__ rung, int n, dkv_ladder_t lad,
+                                                          dkv_wire_t w, uint8_t* __restrict__ codes,
+                                                          uint16_t* __restrict__ low, uint16_t* __restrict__ scale) {
+  const int G = lad.groups;
+  const long id = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (long)n * G * 2) return;
+  const int h = (int)(id & 1);
+  const long tg = id >> 1;
+  const int t = (int)(tg / G), g = (int)(tg % G);
+  const WireSpot s = wire_spot(rung, lad, w, t, g, h);
+  if (s.b == 0) return;
+  uint32_t cw[8];
+  if (s.b == 8) {
+    wire_codes_half<8>(in + s.code, cw);
+  } else if (s.b == 4) {
+    wire_codes_half<4>(in + s.code, cw);
+  } else {
+    wire_codes_half<2>(in + s.code, cw);
+  }
+  uint4* dst = (uint4*)(codes + tg * 64 + h * 32);
+  dst[0] = make_uint4(cw[0], cw[1], cw[2], cw[3]);
+  dst[1] = make_uint4(cw[4], cw[5], cw[6], cw[7]);
+  if (h == 0) {
+    low[tg] = (uint16_t)(in[s.low] | (in[s.low + 1] << 8));
+    scale[tg] = (uint16_t)(in[s.scale] | (in[s.scale + 1] << 8));
+  }
+}
+
+static int check_wire(const dkv_wire_t& w, int32_t n, const char* what) {
+  if (!w.section || !w.count || !w.slot || !w.nwidth || (n > 0 && !w.rank) || w.bytes < 0) {
+    dkv::set_error("%s: storage tables must be non-null and bytes >= 0", what);
+    return DKV_EINVAL;
+  }
+  return DKV_OK;
+}
+
+extern "C" int dkv_wire_pack(const uint8_t* codes, const uint16_t* low, const uint16_t* scale, const int16_t* rung,
+                             int32_t n, dkv_ladder_t ladder, dkv_wire_t wire, uint8_t* out, void* stream) {
+  DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_wire_pack: n < 0");
+  int rc = dkv::check_ladder(ladder, "dkv_wire_pack");
+  if (rc) return rc;
+  if ((rc = check_wire(wire, n, "dkv_wire_pack"))) return rc;
+  DKV_REQUIRE(codes && low && scale && rung && out, DKV_EINVAL, "dkv_wire_pack: null pointer");
+  if (n == 0) return DKV_OK;
+  const long blocks = ((long)n * ladder.groups * 2 + 255) / 256;
+  DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_wire_pack: too many tokens");
+  hipLaunchKernelGGL(wire_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), codes, low, scale,
+                     rung, n, ladder, wire, out);
+  return dkv::check_launch("dkv_wire_pack");
+}
+
+extern "C" int dkv_wire_unpack(const uint8_t* in, const int16_t* rung, int32_t n, dkv_ladder_t ladder,
+                               dkv_wire_t wire, uint8_t* codes, uint16_t* low, uint16_t* scale, void* stream) {
+  DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_wire_unpack: n < 0");
+  int rc = dkv::check_ladder(ladder, "dkv_wire_unpack");
+  if (rc) return rc;
+  if ((rc = check_wire(wire, n, "dkv_wire_unpack"))) return rc;
+  DKV_REQUIRE(in && rung && codes && low && scale, DKV_EINVAL, "dkv_wire_unpack: null pointer");
+  if (n == 0) return DKV_OK;
+  const long blocks = ((long)n * ladder.groups * 2 + 255) / 256;
+  DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_wire_unpack: too many tokens");
+  hipLaunchKernelGGL(wire_unpack_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), in, rung, n,
+                     ladder, wire, codes, low, scale);
+  return dkv::check_launch("dkv_wire_unpack");
+}
+
+// ---------------------------------------------------------------------------
 // K1: one thread per (token, group, half): 32 coefficients.
 // ---------------------------------------------------------------------------
 // Ladder streams: code * scale + low in fp32 (scripts/kvtc.py:78), then the

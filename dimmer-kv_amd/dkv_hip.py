@@ -28,7 +28,7 @@ EXPORTS = [
     "dkv_attend_layer",
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
-    "dkv_gather_cold",
+    "dkv_gather_cold", "dkv_wire_pack", "dkv_wire_unpack",
 ]
 
 c_i32, c_i64, c_f32, c_vp, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
@@ -46,6 +46,12 @@ class Ladder(ctypes.Structure):
 class Stream(ctypes.Structure):
     _fields_ = [("blob", c_vp), ("tok_off", c_vp), ("pieces", c_vp), ("order", Order), ("format", c_i32),
                 ("ladder", Ladder)]
+
+
+class Wire(ctypes.Structure):
+    """Where each (rung, width) section of the byte-storage layout lies (dkv_wire_t)."""
+    _fields_ = [("section", c_vp), ("count", c_vp), ("rank", c_vp), ("slot", c_vp), ("nwidth", c_vp),
+                ("bytes", c_i64)]
 
 
 class AttendArgs(ctypes.Structure):
@@ -135,6 +141,20 @@ def pack_ladder(codes, low, scale, rung, ladder: Ladder, blob, tok_off) -> None:
     _check(lib().dkv_pack_ladder(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(scale)), c_vp(ptr(rung)), c_i32(n),
                                  ladder, c_vp(ptr(blob)), c_vp(ptr(tok_off)), c_vp(stream_handle())),
            "dkv_pack_ladder")
+
+
+def wire_pack(codes, low, scale, rung, ladder: Ladder, wire: Wire, out) -> None:
+    """codes u8 [n, G, 64], shifts/scales (int16 views of fp16) [n, G], rung int16 [n] -> storage sections."""
+    _check(lib().dkv_wire_pack(c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(scale)), c_vp(ptr(rung)),
+                               c_i32(rung.numel()), ladder, wire, c_vp(ptr(out)), c_vp(stream_handle())),
+           "dkv_wire_pack")
+
+
+def wire_unpack(data, rung, ladder: Ladder, wire: Wire, codes, low, scale) -> None:
+    """Storage sections -> codes u8 [n, G, 64], shifts/scales (int16 views of fp16) [n, G]."""
+    _check(lib().dkv_wire_unpack(c_vp(ptr(data)), c_vp(ptr(rung)), c_i32(rung.numel()), ladder, wire,
+                                 c_vp(ptr(codes)), c_vp(ptr(low)), c_vp(ptr(scale)), c_vp(stream_handle())),
+           "dkv_wire_unpack")
 
 
 def unpack_dequant(stream: Stream, t0: int, nt: int, out: torch.Tensor) -> None:

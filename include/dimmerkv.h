@@ -124,6 +124,40 @@ int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const uint16_t* s
 int dkv_pack_ladder(const uint8_t* codes, const uint16_t* low, const uint16_t* scale, const int16_t* rung,
                     int32_t n, dkv_ladder_t ladder, uint8_t* blob, const int64_t* tok_off, void* stream);
 
+/* ---- byte storage (replaces the per-rung code sections of
+ *      scripts/kvtc_storage.py:56-75 encode_bytes and :98-119 decode_bytes) ---
+ * The storage layout of one stream's compressed tokens: for every rung (in
+ * increasing order) and every width w in 2, 4, 8 that the rung uses, one
+ * section holding, for the tokens of the rung in increasing order and the
+ * groups of width w in increasing order, first all the codes (64 per group,
+ * w bits each, LSB-first: code j at bit w*j), then all the fp16 shifts, then
+ * all the fp16 scales.  The section of (rung r, width index i = 0, 1, 2 for
+ * w = 2, 4, 8) starts at byte section[3r + i]; it holds count[r] tokens x
+ * nwidth[3r + i] groups.  Token t (rung rung[t]) is the rank[t]-th token of
+ * its rung; group g is the slot[r*G + g]-th group of its width in rung r.
+ * Every access is checked against `bytes`, the size of the storage buffer;
+ * tokens whose rung lies outside the ladder, and groups with 0 bits, are
+ * skipped. */
+typedef struct dkv_wire {
+  const int64_t* section; /* [rungs][3] */
+  const int32_t* count;   /* [rungs] */
+  const int32_t* rank;    /* [n] */
+  const int16_t* slot;    /* [rungs][G] */
+  const int16_t* nwidth;  /* [rungs][3] */
+  int64_t bytes;
+} dkv_wire_t;
+
+/* codes u8 [n][G][64], shifts/scales f16 [n][G], rung [n] -> the storage
+ * sections in `out` (scripts/kvtc_storage.py:63-75). */
+int dkv_wire_pack(const uint8_t* codes, const uint16_t* low, const uint16_t* scale, const int16_t* rung, int32_t n,
+                  dkv_ladder_t ladder, dkv_wire_t wire, uint8_t* out, void* stream);
+
+/* The inverse (scripts/kvtc_storage.py:109-118, without the dequantize):
+ * storage sections -> codes u8 [n][G][64], shifts/scales f16 [n][G].  Groups
+ * that are skipped are left as the caller initialised them. */
+int dkv_wire_unpack(const uint8_t* in, const int16_t* rung, int32_t n, dkv_ladder_t ladder, dkv_wire_t wire,
+                    uint8_t* codes, uint16_t* low, uint16_t* scale, void* stream);
+
 /* ---- K1: unpack + dequantize (replaces scripts/progressive.py:47-55
  *      dequantize applied to TokenStore rows at their hot prefix, :196-201;
  *      for ladder streams scripts/kvtc.py:62-79 quantize_groups' dequantized
