@@ -44,6 +44,8 @@ def parse():
                         "dkvtc@b:snap:floor1 (kvtc ladder codes; cfg1/cfg2)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-question", action="store_true", help="skip the question stage (score, select, gather)")
+    p.add_argument("--cold-tier", choices=("device", "host"), default="device",
+                   help="where the prog@ cold planes live: device memory, or pinned host memory fetched per question")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     p.add_argument("--traffic-file", default=None,
                    help="rocprofv3 FETCH/WRITE summary of K2 for this workload "
@@ -142,7 +144,8 @@ def question_stage(w):
     torch.cuda.synchronize()
     out = {"query_tokens": int(q.queries.shape[3]), "plane_cap": q.plane_cap, "selected": q.count,
            "score_ms": round(ev[0].elapsed_time(ev[1]) / reps, 3), "topk_ms": round(ev[1].elapsed_time(ev[2]) / reps, 3),
-           "gather_ms": round(ev[2].elapsed_time(ev[3]), 3), "fetched_bytes": fetched}
+           "gather_ms": round(ev[2].elapsed_time(ev[3]), 3), "fetched_bytes": fetched,
+           "cold_tier": "host" if w.streams["key"].cold_on_host else "device"}
     print(f"[bench] question: {out}", file=sys.stderr, flush=True)
     return out
 
@@ -176,7 +179,8 @@ def main():
         w = workloads.build_ragged(device=dev)
     else:
         w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline,
-                                   refine_fraction=0.01 if args.config == "cfg2" and not args.no_question else 0.0)
+                                   refine_fraction=0.01 if args.config == "cfg2" and not args.no_question else 0.0,
+                                   cold_tier=args.cold_tier)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
     print(f"[bench] built {args.config} in {build_s:.1f}s: {w.middle_total} compressed tokens, "

@@ -84,6 +84,23 @@ class PackedStream:
         self.refined = 0
         self.version = 0  # bumped whenever tokens change (refine), so decoded copies know to refresh
         self.initial_pieces = pieces.clone()
+        self._stage_off = None  # host cold tier: device offsets of the staged cold blobs, by token
+
+    @property
+    def cold_on_host(self) -> bool:
+        return self.cold is not None and not self.cold.is_cuda
+
+    def move_cold_to_host(self) -> None:
+        """Keep the cold tier in pinned host memory (frees its device copy); ``refine`` then copies
+        only the selected tokens' cold blobs to the device."""
+        if self.cold is None or self.cold_on_host:
+            return
+        host = torch.empty(self.cold.numel(), dtype=torch.uint8, pin_memory=True)
+        host.copy_(self.cold)
+        self.cold = host
+        self.cold_off = self.cold_off.cpu()
+        self._cold_size0 = (self.tables.full_bytes - self.tables.prefix64[self.initial_pieces.long()]).cpu()
+        self._stage_off = torch.zeros(self.n, dtype=torch.int64, device=self.blob.device)
 
     @property
     def n(self) -> int:
@@ -91,8 +108,12 @@ class PackedStream:
 
     @classmethod
     def pack(cls, codes: torch.Tensor, low: torch.Tensor, span: torch.Tensor, pieces: torch.Tensor,
-             tables: OrderTables, refine_capacity: int = 0, with_cold: bool = True) -> "PackedStream":
-        """codes u8 [n, G, 64], low/span f16 [n, G], pieces [n] -> packed tiers (GPU pack kernel)."""
+             tables: OrderTables, refine_capacity: int = 0, with_cold: bool = True,
+             cold_tier: str = "device") -> "PackedStream":
+        """codes u8 [n, G, 64], low/span f16 [n, G], pieces [n] -> packed tiers (GPU pack kernel).
+        ``cold_tier`` "host" keeps the cold planes in pinned host memory."""
+        if cold_tier not in ("device", "host"):
+            raise ValueError(f"cold_tier must be 'device' or 'host' (got {cold_tier!r})")
         device = codes.device
         n = codes.shape[0]
         pieces = pieces.to(device=device, dtype=torch.int16).contiguous()
@@ -110,7 +131,10 @@ class PackedStream:
             dkv_hip.pack_planes(codes.contiguous(), low.contiguous().view(torch.int16),
                                 span.contiguous().view(torch.int16), pieces, tables.c_order(), blob, tok_off,
                                 cold, cold_off)
-        return cls(tables, blob, tok_off, pieces, cold, cold_off, hot_total, refine_capacity)
+        stream = cls(tables, blob, tok_off, pieces, cold, cold_off, hot_total, refine_capacity)
+        if cold_tier == "host":
+            stream.move_cold_to_host()
+        return stream
 
     def c_stream(self) -> dkv_hip.Stream:
         return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(),
@@ -147,11 +171,32 @@ class PackedStream:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
         fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
         base = self.hot_used + self.refined * self.tables.full_bytes
-        dkv_hip.gather_cold(self.c_stream(), self.cold, self.cold_off, rows, base, self.blob, self.tok_off,
-                            self.pieces)
+        cold, cold_off = self.cold, self.cold_off
+        if self.cold_on_host:
+            cold, cold_off = self._stage_cold(rows)
+        dkv_hip.gather_cold(self.c_stream(), cold, cold_off, rows, base, self.blob, self.tok_off, self.pieces)
         self.refined += k
         self.version += 1
         return int(fetched)
+
+    def _stage_cold(self, rows: torch.Tensor):
+        """Host cold tier: gather the cold blobs of ``rows`` into one pinned buffer, copy it to the
+        device (one host-to-device transfer), and point each row's cold offset into the copy."""
+        rows_h = rows.cpu().long()
+        start = self.cold_off[rows_h].numpy()
+        size = self._cold_size0[rows_h].numpy()
+        dst = np.zeros(size.size, np.int64)
+        np.cumsum(size[:-1], out=dst[1:])
+        staged = torch.empty(max(int(size.sum()), 16), dtype=torch.uint8, pin_memory=True)
+        cold_np, staged_np = self.cold.numpy(), staged.numpy()
+        for a, d, n in zip(start.tolist(), dst.tolist(), size.tolist()):  # one slice copy per token
+            staged_np[d:d + n] = cold_np[a:a + n]
+        dst = torch.from_numpy(dst)
+        device = self.blob.device
+        staged_dev = staged.to(device, non_blocking=True)
+        self._stage_off[rows.long()] = dst.to(device, non_blocking=True)
+        self._staged = (staged, staged_dev)  # both stay alive until the next refine
+        return staged_dev, self._stage_off
 
 
 LADDER_GROUP = 64

@@ -164,7 +164,8 @@ class QuestionStage:
         return sum(self.w.streams[k].refine(rows) for k in ("key", "value"))
 
 
-def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, refine_capacity: int = 0) -> dict:
+def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, refine_capacity: int = 0,
+                  cold_tier: str = "device") -> dict:
     order = plane_major_order(shape.groups)
     otab = OrderTables(order.planes, order.prefix_bytes, device)
     streams = {}
@@ -172,7 +173,7 @@ def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, re
         codes, low, span = quantize8(coefs[kind].to(device), 64)
         pieces = torch.from_numpy(planes[kind] * shape.groups).to(device)
         streams[kind] = PackedStream.pack(codes, low, span, pieces, otab, refine_capacity=refine_capacity,
-                                          with_cold=refine_capacity > 0)
+                                          with_cold=refine_capacity > 0, cold_tier=cold_tier)
         del codes, low, span
     return streams
 
@@ -180,10 +181,11 @@ def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, re
 def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
                  shape: synth.ModelShape | None = None, tokens: int | None = None, budget: float | None = None,
                  query_dtype: torch.dtype | None = None, keep_host_basis: bool = False,
-                 refine_fraction: float = 0.0) -> DecodeWorkload:
+                 refine_fraction: float = 0.0, cold_tier: str = "device") -> DecodeWorkload:
     """A single-conversation decode workload (configs 0-2).  ``keep_host_basis`` keeps float32
     host copies of the bases (for the CPU baseline); ``refine_fraction`` > 0 keeps a cold tier
-    and room to refine that fraction of the tokens (the question stage)."""
+    (in device memory, or pinned host memory with ``cold_tier="host"``) and room to refine that
+    fraction of the tokens (the question stage)."""
     if name in CONFIGS:
         s0, t0, b0, qd0 = CONFIGS[name]
         shape, tokens = shape or s0, tokens or t0
@@ -192,7 +194,7 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
     ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device,
                              budget_over_middle=name in BUDGET_OVER_MIDDLE)
     capacity = int(round(refine_fraction * ctx.middle)) + 1 if refine_fraction > 0 else 0
-    streams = _pack_streams(ctx.coef, ctx.planes, shape, device, capacity)
+    streams = _pack_streams(ctx.coef, ctx.planes, shape, device, capacity, cold_tier)
     cos, sin = synth.rope_tables(shape, tokens + max(q_len, 64), device)
     tables = ModelTables(ctx.basis["key"], ctx.basis["value"], ctx.mean["key"], ctx.mean["value"], shape.layers,
                          shape.kv_heads, shape.head_dim, cos, sin)

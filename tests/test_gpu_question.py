@@ -112,6 +112,39 @@ def test_refine_then_attend():
     assert sum(streams[k].refine(torch.from_numpy(rows).to(DEV)) for k in ("key", "value")) == 0
 
 
+def test_refine_from_host_cold_tier_matches_device_tier():
+    """A cold tier in pinned host memory (only the chosen tokens' planes copied over) refines to the
+    same bytes as the device-resident one, including rows refined twice and rows already full."""
+    from hot_tier import OrderTables, PackedStream
+
+    shape = synth.ModelShape(2, 8, 64, 32, 1024)
+    print("[case] host cold tier", flush=True)
+    case = build_case(shape, 1200, seed=78, query_scale=60.0)
+    otab = OrderTables(case.order.planes, case.order.prefix_bytes, DEV)
+    full_pieces = case.pieces["key"].copy()
+    full_pieces[[3, 9]] = case.order.pieces  # two tokens already at full precision
+    packs = {}
+    for tier in ("device", "host"):
+        packs[tier] = PackedStream.pack(torch.from_numpy(case.codes["key"]).to(DEV),
+                                        torch.from_numpy(case.low["key"]).to(DEV),
+                                        torch.from_numpy(case.span["key"]).to(DEV),
+                                        torch.from_numpy(full_pieces).to(DEV), otab, refine_capacity=64,
+                                        cold_tier=tier)
+    assert packs["host"].cold_on_host and not packs["device"].cold_on_host
+    assert torch.equal(packs["host"].cold.cuda()[:packs["device"].cold.numel()], packs["device"].cold)
+    for rows in ([0, 3, 5, 100, 777], [5, 9, 400, 1100, 0], [case.ctx.middle - 1]):
+        r = torch.tensor(rows, device=DEV)
+        fetched = [packs[t].refine(r) for t in ("device", "host")]
+        torch.cuda.synchronize()
+        assert fetched[0] == fetched[1]
+        a, b = packs["device"], packs["host"]
+        assert torch.equal(a.tok_off, b.tok_off) and torch.equal(a.pieces, b.pieces)
+        assert torch.equal(a.blob, b.blob)
+    got = packs["host"].dequantize().cpu().numpy()
+    want = packs["device"].dequantize().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def test_varlen_matches_per_sequence_oracle():
     """Three conversations in one packed buffer, one fused decode step (cu_seqlens, cu_exact)."""
     from compressed_attention import CompressedContext, ModelTables
