@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--traffic-file", default=None,
                    help="rocprofv3 FETCH/WRITE summary of K2 for this workload "
                         "(default profiles/keys_scores_<config>[_dkvtc]_traffic.txt)")
+    p.add_argument("--storage", action="store_true",
+                   help="measure kvtc byte storage at cfg2 (dkvtc): encode, DEFLATE, restore; one JSON line")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -99,8 +101,10 @@ def cpu_baseline(w, seconds: float):
     times = []
     with threadpool_limits(limits=cores):
         t_start = time.perf_counter()
-        layer = 0
-        while layer < s.layers and (not times or time.perf_counter() - t_start < seconds):
+        step = 0
+        # every layer once, then around again until the time bound
+        while step < s.layers or time.perf_counter() - t_start < seconds:
+            layer = step % s.layers
             q = w.queries[layer].float().cpu().numpy()
             ke = w.key_exact[layer][None].cpu().numpy()
             ve = w.value_exact[layer][None].cpu().numpy()
@@ -111,12 +115,12 @@ def cpu_baseline(w, seconds: float):
             t0 = time.perf_counter()
             attention_ref.attend(q, coef["key"], coef["value"], bk, bv, mk, mv, cos, sin, ke, ve)
             times.append(time.perf_counter() - t0)
-            layer += 1
+            step += 1
     per_layer = sum(times) / len(times)
     return {"value": 1.0 / (per_layer * s.layers), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} of {s.layers} layers of the same workload through the numpy fp32 oracle "
-                      f"(oracle/attention_ref.attend over K1-decoded coefficients), {per_layer * 1e3:.0f} ms/layer, "
-                      f"scaled x{s.layers}"}
+            "sample": f"{len(times)} layer passes ({s.layers} layers, cycled for {sum(times):.1f} s) of the same "
+                      f"workload through the numpy fp32 oracle (oracle/attention_ref.attend over K1-decoded "
+                      f"coefficients), {per_layer * 1e3:.0f} ms/layer, scaled x{s.layers}"}
 
 
 def question_stage(w):
@@ -150,10 +154,123 @@ def question_stage(w):
     return out
 
 
+def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
+    """kvtc byte storage at the cfg2 shape (Llama-3.2-3B, 16,384 tokens, dkvtc@0.03:snap:floor1):
+    GPU encode (quantize + dkv_wire_pack + one device-to-host copy), the two storage kernels alone
+    (HIP events on their stream), host DEFLATE / INFLATE (zlib level 6), ``restore_context`` (one
+    host-to-device copy + dkv_wire_unpack + ladder packing) and ``decode_bytes`` (FP16 rebuild).
+    CPU baseline: the numpy oracle's encode + decode of the first ``cpu_tokens`` compressed tokens
+    of the same cache, scaled to the stored bytes."""
+    import numpy as np
+    import torch
+
+    import dkv_hip
+    import kvtc
+    import kvtc_storage
+    import methods
+    import synth
+    import workloads
+    from oracle import storage_ref
+
+    dev = "cuda"
+    shape, tokens, budget, _ = workloads.CONFIGS["cfg2"]
+    ctx = synth.make_context(shape, tokens, 2024, device=dev)
+    model = synth.RopeModel(shape, dev)
+    m = methods.Methods("synthetic/llama-3.2", device=dev, model=model, kvtc=synth.kvtc_checkpoint(ctx))
+    keys, values = synth.prefill_cache(ctx, device=dev, dtype=torch.float16, compute_device=dev)
+    g = torch.Generator("cpu").manual_seed(2024 + 80)
+    scores = {"snap": [torch.rand(shape.kv_heads, tokens, generator=g).to(dev) for _ in range(shape.layers)]}
+    m.apply(f"dkvtc@{budget}:snap:floor1", keys, values, scores)
+    codec = m.codec("kvtc")
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = fn()
+        torch.cuda.synchronize()
+        return out, (time.perf_counter() - t0) / reps * 1e3
+
+    data, encode_ms = timed(lambda: kvtc_storage.encode_bytes(codec, keys, values, codec.last_choice, m.recent))
+    packed, deflate_ms = timed(lambda: kvtc_storage.deflate(data))
+    _, inflate_ms = timed(lambda: kvtc_storage.inflate(packed))
+    _, restore_ms = timed(lambda: kvtc_storage.restore_context(codec, data, model))
+    _, decode_ms = timed(lambda: kvtc_storage.decode_bytes(codec, data))
+    # the storage kernels alone, on the values stream (the larger rung mix is the same for keys)
+    parsed = kvtc_storage._Parsed(codec, data)
+    rungs_np = parsed.choice["value"].cpu().numpy()
+    features = shape.layers * shape.kv_heads * shape.head_dim
+    base = kvtc_storage.HEADER_BYTES  # section offsets as if values were the first stream (same sizes)
+    layout = kvtc_storage._StreamLayout(codec.streams["value"].rungs.cpu().numpy().astype(np.int64), rungs_np,
+                                        features, tokens - parsed.middle, base)
+    wire = torch.zeros(layout.end, dtype=torch.uint8, device=dev)
+    w, keep = layout.device_tables(dev, layout.end)
+    ladder = kvtc_storage._full_ladder(codec, "value")
+    codes, low, scale = parsed.codes["value"]
+    rung16 = parsed.choice["value"].to(torch.int16).contiguous()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    for _ in range(2):
+        dkv_hip.wire_pack(codes, low.view(torch.int16), scale.view(torch.int16), rung16, ladder.c_ladder(), w, wire)
+        dkv_hip.wire_unpack(wire, rung16, ladder.c_ladder(), w, codes, low.view(torch.int16), scale.view(torch.int16))
+    ev[0].record()
+    for _ in range(reps):
+        dkv_hip.wire_pack(codes, low.view(torch.int16), scale.view(torch.int16), rung16, ladder.c_ladder(), w, wire)
+    ev[1].record()
+    for _ in range(reps):
+        dkv_hip.wire_unpack(wire, rung16, ladder.c_ladder(), w, codes, low.view(torch.int16), scale.view(torch.int16))
+    ev[2].record()
+    torch.cuda.synchronize()
+    pack_us = ev[0].elapsed_time(ev[1]) / reps * 1e3
+    unpack_us = ev[1].elapsed_time(ev[2]) / reps * 1e3
+    section_bytes = layout.exact_tokens - (base + parsed.middle)
+    code_bytes = codes.numel() + 4 * low.numel()
+    del keep
+    # CPU baseline: the oracle over the first cpu_tokens compressed tokens
+    start, end = codec.last_span
+    n = min(cpu_tokens, end - start)
+    cos, sin = kvtc.rope_tables(model, tokens, dev)
+    streams, metas = [], []
+    for kind, tensors in (("key", keys), ("value", values)):
+        stream = codec.streams[kind]
+        matrix = codec.to_matrix(tensors, kind, cos, sin)[start:start + n]
+        coef = (matrix - stream.mean) @ stream.basis
+        streams.append({"rungs": codec.last_choice[kind][:n].cpu().numpy(), "bits": stream.rungs.cpu().numpy(),
+                        "coefficients": coef.cpu().numpy(), "matrix_rows": matrix.cpu().numpy(),
+                        "exact_tokens": np.zeros((0, features), np.float32), "features": features})
+        metas.append({"bits": stream.rungs.cpu().numpy(), "rank": stream.basis.shape[1], "features": features})
+    t0 = time.perf_counter()
+    sample = storage_ref.encode(n, 0, n, streams, codec.group)
+    t1 = time.perf_counter()
+    storage_ref.decode(sample, metas, codec.group)
+    t2 = time.perf_counter()
+    mb = len(data) / 1e6
+    result = {
+        "metric": "kvtc byte storage, cfg2 dkvtc@0.03:snap:floor1 (3B shape, 16K tokens)",
+        "value": round(mb / (restore_ms / 1e3), 1), "unit": "MB/s restored into a CompressedContext",
+        "higher_is_better": True, "data": "synthetic",
+        "stored_bytes": len(data), "fp16_fraction": round(len(data) / (4 * features * tokens), 5),
+        "deflated_bytes": len(packed),
+        "encode_ms": round(encode_ms, 2), "deflate_ms": round(deflate_ms, 1), "inflate_ms": round(inflate_ms, 1),
+        "restore_context_ms": round(restore_ms, 2), "decode_bytes_ms": round(decode_ms, 2),
+        "wire_pack_us": round(pack_us, 1), "wire_unpack_us": round(unpack_us, 1),
+        "wire_kernel_bytes": {"sections": int(section_bytes), "codes_and_affine": int(code_bytes),
+                              "note": "values stream, per launch"},
+        "cpu_baseline": {"value": round(len(sample) / 1e6 / (t2 - t0), 2), "unit": "MB/s encode+decode",
+                         "encode_s": round(t1 - t0, 3), "decode_s": round(t2 - t1, 3), "cores": 1, "kind": "port",
+                         "sample": f"oracle/storage_ref encode + decode (numpy) of the first {n} compressed tokens "
+                                   f"({len(sample)} B) of the same cache"},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.storage:
+        storage_bench()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): this build runs the decode path on a "
