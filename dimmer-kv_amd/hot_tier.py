@@ -12,7 +12,9 @@ include/dimmerkv.h / oracle/packing_ref.py.
 ``PackedStream.refine`` is the cold-plane gather (K4c): selected tokens get
 full blobs in a refine area at the end of the hot allocation, and their
 offsets/piece counts are redirected there, so the attention kernels see the
-refined tokens with no other change.
+refined tokens with no other change.  The cold tier lives in device memory, or
+(``cold_tier="host"``) in pinned host memory, from which a refine copies only
+the chosen tokens' cold blobs.
 
 ``LadderStream`` holds the kvtc ladder codes of the ``dkvtc@`` entry point
 (scripts/kvtc.py:62-79, scripts/kvtc_storage.py:21-75) in the same
@@ -85,6 +87,7 @@ class PackedStream:
         self.version = 0  # bumped whenever tokens change (refine), so decoded copies know to refresh
         self.initial_pieces = pieces.clone()
         self._stage_off = None  # host cold tier: device offsets of the staged cold blobs, by token
+        self._staged = None     # host cold tier: the last staging buffer (pinned) and its device copy
 
     @property
     def cold_on_host(self) -> bool:

@@ -18,6 +18,8 @@ answer-time path so that the HIP kernels can be checked against it:
                     ladder layout this build defines (byte totals follow
                     scripts/progressive.py:185-194, 232 and scripts/kvtc.py:82-85;
                     ladder code bits LSB-first as scripts/kvtc_storage.py:21-27)
+- ``storage_ref``   the kvtc byte-storage layout, encode_bytes / decode_bytes
+                    (scripts/kvtc_storage.py:21-135)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker. The product
