@@ -97,6 +97,8 @@ class CompressedContext:
         self.q_heads = q_heads
         device = key.blob.device
         self.positions = positions.to(device=device, dtype=torch.int32).contiguous()
+        if not self.positions.numel():  # no compressed token: still a non-null pointer for the C ABI
+            self.positions = torch.zeros(1, dtype=torch.int32, device=device)[:0]
         if cu_seqlens is None:
             cu_seqlens = torch.tensor([0, key.n], dtype=torch.int32)
         self.cu_host = cu_seqlens.to(torch.int32).cpu().contiguous()
@@ -264,7 +266,7 @@ class CompressedContext:
         a.key, a.value = self.key.c_stream(), self.value.c_stream()
         a.cu_seqlens = self.cu.data_ptr()
         a.cu_seqlens_host = self.cu_host.data_ptr()
-        a.positions = self.positions.data_ptr()
+        a.positions = dkv_hip.addr(self.positions)
         a.key_basis, a.value_basis = t.key_basis.data_ptr(), t.value_basis.data_ptr()
         a.mean_k, a.mean_v = t.mean_k.data_ptr(), t.mean_v.data_ptr()
         a.rope_cos, a.rope_sin, a.rope_rows = t.rope_cos.data_ptr(), t.rope_sin.data_ptr(), t.rope_cos.shape[0]

@@ -107,6 +107,15 @@ def _check(rc: int, what: str) -> None:
     raise DkvError(msg)
 
 
+def addr(t: torch.Tensor) -> int:
+    """Address of ``t``'s first element.  torch reports 0 for every empty tensor; an empty view of an
+    allocation gets the address its storage gives it, so arrays of zero tokens still pass the C ABI's
+    non-null checks (nothing is read through them)."""
+    if t.numel():
+        return t.data_ptr()
+    return t.untyped_storage().data_ptr() + t.storage_offset() * t.element_size()
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     if t is None:
         return None
@@ -114,7 +123,7 @@ def ptr(t: torch.Tensor | None) -> int | None:
         raise ValueError("dimmer-kv HIP kernels need GPU tensors (no CPU path)")
     if not t.is_contiguous():
         raise ValueError("dimmer-kv HIP kernels need contiguous tensors")
-    return t.data_ptr()
+    return addr(t)
 
 
 def stream_handle() -> int:

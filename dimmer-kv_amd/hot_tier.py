@@ -66,8 +66,14 @@ class OrderTables:
                              self.cold_off.data_ptr(), self.prefix.data_ptr())
 
 
+def _nonnull(t: torch.Tensor) -> torch.Tensor:
+    """``t`` itself, or for an empty tensor an empty view of a one-element allocation: the C ABI takes
+    every array as a non-null pointer, and an empty torch tensor has none."""
+    return t if t.numel() else torch.zeros(1, dtype=t.dtype, device=t.device)[:0]
+
+
 def _exclusive_cumsum(sizes: torch.Tensor) -> tuple[torch.Tensor, int]:
-    off = torch.zeros(sizes.numel(), dtype=torch.int64, device=sizes.device)
+    off = _nonnull(torch.zeros(sizes.numel(), dtype=torch.int64, device=sizes.device))
     if sizes.numel() > 1:
         off[1:] = torch.cumsum(sizes[:-1], 0)
     total = int(sizes.sum()) if sizes.numel() else 0
@@ -119,7 +125,7 @@ class PackedStream:
             raise ValueError(f"cold_tier must be 'device' or 'host' (got {cold_tier!r})")
         device = codes.device
         n = codes.shape[0]
-        pieces = pieces.to(device=device, dtype=torch.int16).contiguous()
+        pieces = _nonnull(pieces.to(device=device, dtype=torch.int16).contiguous())
         p64 = pieces.long()
         hot_sizes = tables.prefix64[p64] if n else torch.zeros(0, dtype=torch.int64, device=device)
         tok_off, hot_total = _exclusive_cumsum(hot_sizes)
@@ -140,7 +146,7 @@ class PackedStream:
         return stream
 
     def c_stream(self) -> dkv_hip.Stream:
-        return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(),
+        return dkv_hip.Stream(self.blob.data_ptr(), dkv_hip.addr(self.tok_off), dkv_hip.addr(self.pieces),
                               self.tables.c_order(), dkv_hip.DKV_FMT_PLANES)
 
     def dequantize(self, t0: int = 0, nt: int | None = None, dtype=torch.float32) -> torch.Tensor:
@@ -262,7 +268,7 @@ class LadderStream:
         rung = rung.to(device=device, dtype=torch.int64)
         if rung.numel() and (int(rung.min()) < -1 or int(rung.max()) >= tables.empty):
             raise ValueError(f"rung ids must lie in -1..{tables.empty - 1}")
-        rung = torch.where(rung < 0, torch.full_like(rung, tables.empty), rung).to(torch.int16).contiguous()
+        rung = _nonnull(torch.where(rung < 0, torch.full_like(rung, tables.empty), rung).to(torch.int16).contiguous())
         sizes = tables.sizes64[rung.long()] if rung.numel() else torch.zeros(0, dtype=torch.int64, device=device)
         tok_off, total = _exclusive_cumsum(sizes)
         blob = torch.zeros(max(total, 16), dtype=torch.uint8, device=device)
@@ -272,7 +278,7 @@ class LadderStream:
         return cls(tables, blob, tok_off, rung, total)
 
     def c_stream(self) -> dkv_hip.Stream:
-        return dkv_hip.Stream(self.blob.data_ptr(), self.tok_off.data_ptr(), self.pieces.data_ptr(), dkv_hip.Order(),
+        return dkv_hip.Stream(self.blob.data_ptr(), dkv_hip.addr(self.tok_off), dkv_hip.addr(self.pieces), dkv_hip.Order(),
                               dkv_hip.DKV_FMT_LADDER, self.tables.c_ladder())
 
     def dequantize(self, t0: int = 0, nt: int | None = None, dtype=torch.float32) -> torch.Tensor:

@@ -86,7 +86,8 @@ class _StreamLayout:
             "slot": torch.as_tensor(self.slot).to(device),
             "nwidth": torch.as_tensor(self.nwidth).to(device),
         }
-        wire = dkv_hip.Wire(t["section"].data_ptr(), t["count"].data_ptr(), t["rank"].data_ptr(),
+        t["rank"] = torch.zeros(1, dtype=torch.int32, device=device)[:0] if not self.rank.size else t["rank"]
+        wire = dkv_hip.Wire(t["section"].data_ptr(), t["count"].data_ptr(), dkv_hip.addr(t["rank"]),
                             t["slot"].data_ptr(), t["nwidth"].data_ptr(), total)
         return wire, t  # the tensors must outlive the kernel launch
 

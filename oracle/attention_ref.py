@@ -32,7 +32,7 @@ def layer_keys(coef_k: np.ndarray, basis_k_layer: np.ndarray, mean_k_layer: np.n
     """compressed_attention.py:105-111 -> [Hkv, n, d]."""
     n = coef_k.shape[0]
     flat = coef_k.astype(dtype) @ basis_k_layer.astype(dtype) + mean_k_layer.astype(dtype)
-    heads_first = flat.reshape(n, heads, -1).transpose(1, 0, 2)
+    heads_first = flat.reshape(n, heads, flat.shape[1] // heads).transpose(1, 0, 2)
     return rerotate(heads_first, cos.astype(dtype), sin.astype(dtype)).astype(dtype)
 
 

@@ -77,7 +77,7 @@ def dequantize_codes(codes: np.ndarray, low: np.ndarray, scale: np.ndarray, bits
     out = (prod + low.astype(np.float32)[..., None]).astype(np.float32)
     b = np.broadcast_to(bits, low.shape)
     out[b == 0] = 0.0
-    return out.reshape(codes.shape[0], -1)
+    return out.reshape(codes.shape[0], codes.shape[1] * codes.shape[2])
 
 
 def rung_bytes(bits: np.ndarray, group: int) -> int:

@@ -57,7 +57,7 @@ def dequantize(codes: np.ndarray, low: np.ndarray, span: np.ndarray, planes: np.
     prod = ((index.astype(np.float32) + np.float32(0.5)) * span.astype(np.float32)[..., None]).astype(np.float32)
     value = (low.astype(np.float32)[..., None] + (prod / bins).astype(np.float32)).astype(np.float32)
     out = np.where(m > 0, value, np.float32(0)).astype(np.float32)
-    return out.reshape(codes.shape[0], -1)
+    return out.reshape(codes.shape[0], codes.shape[1] * codes.shape[2])
 
 
 class Order:

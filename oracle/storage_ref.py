@@ -131,8 +131,8 @@ def decode(data: bytes, metas: list[dict], group: int) -> dict:
                 n_codes = count * chosen.size * group
                 packed = read(np.uint8, packed_length(n_codes, width)).tobytes()
                 codes[:, chosen] = unpack_codes(packed, width, n_codes).reshape(count, chosen.size, group)
-                low[:, chosen] = read("<f2", count * chosen.size).reshape(count, -1)
-                scale[:, chosen] = read("<f2", count * chosen.size).reshape(count, -1)
+                low[:, chosen] = read("<f2", count * chosen.size).reshape(count, chosen.size)
+                scale[:, chosen] = read("<f2", count * chosen.size).reshape(count, chosen.size)
             coefficients[rows] = kvtc_ref.dequantize_codes(codes, low, scale, row_bits)
         exact_tokens = read("<f2", (tokens - middle) * features).reshape(tokens - middle, features).copy()
         out.append({"rungs": rungs, "coefficients": coefficients, "exact_rows": exact_rows,

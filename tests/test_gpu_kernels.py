@@ -128,6 +128,21 @@ def test_attend_special_cases():
     assert_close(got, ref, what="zero query", base=value_mean_base(case2, 1))
 
 
+def test_attend_with_no_compressed_tokens():
+    """A 36-token conversation (4 sinks + 32 recent) leaves nothing to compress: the kernels skip the
+    compressed part and the output is attention over the exact tokens alone."""
+    shape = synth.ModelShape(2, 8, 64, 32, 1024)
+    print("[case] attend with no compressed tokens", flush=True)
+    case = build_case(shape, 36, seed=97, query_scale=40.0)
+    assert case.ctx.middle == 0
+    ctx, _, _ = gpu_context(case)
+    for layer in range(shape.layers):
+        got = gpu_attend(case, ctx, layer)
+        err, fro = assert_close(got, oracle_attend(case, layer), what=f"all-exact layer {layer}",
+                                base=value_mean_base(case, layer))
+        print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+
+
 def test_topk_exact():
     import dkv_hip
     from oracle import scoring_ref

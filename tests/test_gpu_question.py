@@ -145,18 +145,20 @@ def test_refine_from_host_cold_tier_matches_device_tier():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-def test_varlen_matches_per_sequence_oracle():
-    """Three conversations in one packed buffer, one fused decode step (cu_seqlens, cu_exact)."""
+@pytest.mark.parametrize("lengths", [(700, 1333, 300), (700, 36, 300), (36, 36)],
+                         ids=["ragged", "one-all-exact", "all-exact"])
+def test_varlen_matches_per_sequence_oracle(lengths):
+    """Conversations in one packed buffer, one fused decode step (cu_seqlens, cu_exact); a
+    conversation of 36 tokens (4 sinks + 32 recent) has no compressed token at all."""
     from compressed_attention import CompressedContext, ModelTables
     from hot_tier import OrderTables, PackedStream
 
     shape = synth.ModelShape(2, 8, 128, 24, 2048)
-    print("[case] varlen x3", flush=True)
+    print(f"[case] varlen {lengths}", flush=True)
     basis = {"key": synth.orthonormal_basis(shape.features, shape.rank, 901),
              "value": synth.orthonormal_basis(shape.features, shape.rank, 902)}
     g = torch.Generator("cpu").manual_seed(903)
     mean = {k: torch.randn(shape.features, generator=g) * 0.01 for k in ("key", "value")}
-    lengths = (700, 1333, 300)
     rope_rows = max(lengths) + 1
     cases = [build_case(shape, T, seed=500 + 17 * i, query_scale=80.0, basis=basis, mean=mean, rope_rows=rope_rows)
              for i, T in enumerate(lengths)]
