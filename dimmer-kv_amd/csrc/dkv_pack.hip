@@ -87,9 +87,9 @@ extern "C" int dkv_pack_planes(const uint8_t* codes, const uint16_t* low, const 
   DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_pack_planes: n < 0");
   int rc = dkv::check_order(order, "dkv_pack_planes");
   if (rc) return rc;
+  if (n == 0) return DKV_OK;
   DKV_REQUIRE(codes && low && span && pieces && hot && hot_off, DKV_EINVAL, "dkv_pack_planes: null pointer");
   DKV_REQUIRE(!cold || (cold_off && order.cold_off), DKV_EINVAL, "dkv_pack_planes: cold needs cold offsets");
-  if (n == 0) return DKV_OK;
   const long waves = (long)n * order.groups;
   const long blocks = (waves + 3) / 4;
   DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_pack_planes: too many tokens");
@@ -156,8 +156,8 @@ extern "C" int dkv_pack_ladder(const uint8_t* codes, const uint16_t* low, const 
   DKV_REQUIRE(n >= 0, DKV_ESHAPE, "dkv_pack_ladder: n < 0");
   int rc = dkv::check_ladder(ladder, "dkv_pack_ladder");
   if (rc) return rc;
-  DKV_REQUIRE(codes && low && scale && rung && blob && tok_off, DKV_EINVAL, "dkv_pack_ladder: null pointer");
   if (n == 0) return DKV_OK;
+  DKV_REQUIRE(codes && low && scale && rung && blob && tok_off, DKV_EINVAL, "dkv_pack_ladder: null pointer");
   const long threads = (long)n * ladder.groups * 2;
   const long blocks = (threads + 255) / 256;
   DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_pack_ladder: too many tokens");
@@ -314,8 +314,8 @@ extern "C" int dkv_wire_pack(const uint8_t* codes, const uint16_t* low, const ui
   int rc = dkv::check_ladder(ladder, "dkv_wire_pack");
   if (rc) return rc;
   if ((rc = check_wire(wire, n, "dkv_wire_pack"))) return rc;
-  DKV_REQUIRE(codes && low && scale && rung && out, DKV_EINVAL, "dkv_wire_pack: null pointer");
   if (n == 0) return DKV_OK;
+  DKV_REQUIRE(codes && low && scale && rung && out, DKV_EINVAL, "dkv_wire_pack: null pointer");
   const long blocks = ((long)n * ladder.groups * 2 + 255) / 256;
   DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_wire_pack: too many tokens");
   hipLaunchKernelGGL(wire_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), codes, low, scale,
@@ -329,8 +329,8 @@ extern "C" int dkv_wire_unpack(const uint8_t* in, const int16_t* rung, int32_t n
   int rc = dkv::check_ladder(ladder, "dkv_wire_unpack");
   if (rc) return rc;
   if ((rc = check_wire(wire, n, "dkv_wire_unpack"))) return rc;
-  DKV_REQUIRE(in && rung && codes && low && scale, DKV_EINVAL, "dkv_wire_unpack: null pointer");
   if (n == 0) return DKV_OK;
+  DKV_REQUIRE(in && rung && codes && low && scale, DKV_EINVAL, "dkv_wire_unpack: null pointer");
   const long blocks = ((long)n * ladder.groups * 2 + 255) / 256;
   DKV_REQUIRE(blocks < (1L << 31), DKV_ESHAPE, "dkv_wire_unpack: too many tokens");
   hipLaunchKernelGGL(wire_unpack_kernel, dim3((unsigned)blocks), dim3(256), 0, dkv::as_stream(stream), in, rung, n,
