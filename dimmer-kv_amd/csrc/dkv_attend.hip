@@ -40,7 +40,7 @@ struct K2Args {
   const float* rope_cos;
   const float* rope_sin;
   const void* query;
-  float* scores;
+  float* scores;         // f32 [R][n_total]: written when probs is NULL (question scoring) or RH > 4
   uint16_t* probs;  // fp16 exp(score - tile max), [R][n_slots]; NULL when only scores are needed
   float* tile_max;
   float* tile_sum;
@@ -297,7 +297,8 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
         const int n = tq * 64 + tb * 32 + l32;
         x[tb] = n < count ? full * a.scaling : -INFINITY;
         xs[hw][r][tb] = x[tb];
-        if (tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
+        // fp32 scores are for question scoring (no probabilities then); decoding reads only the probabilities
+        if (!a.probs && tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
       const float mx = max32(fmaxf(x[0], x[1]));
       float sm = 0.0f;
