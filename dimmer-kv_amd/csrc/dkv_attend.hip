@@ -358,7 +358,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 // [256][64] are fetched into registers one group ahead and stored into a
 // double-buffered, padded LDS tile; 32x32x16 fp16 MFMAs accumulate the keys.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool SMALL>
 __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   constexpr int HPW = 256 / D;      // heads per workgroup
   constexpr int DB = D / 32;        // 32-row blocks per head
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int RH = (a.Hq / a.Hkv) * a.q_len;
 
   // the decode epilogue's positions and query rows are fetched now, behind the main loop
-  if (RH <= kSmallRows) {
+  if constexpr (SMALL) {
     if (tid < kTileTok) pos_s[tid] = a.positions[tok0 + min(tid, count - 1)];
     const int gq = a.Hq / a.Hkv;
     for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
@@ -501,10 +501,10 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   const int gq = a.Hq / a.Hkv;
   const int half_d = D / 2;
-  if (RH <= kSmallRows) {
+  if constexpr (SMALL) {
     keys_scores_small_epilogue<D>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s);
     return;
-  }
+  } else {
 
   // ---- epilogue 1 (many query rows): RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8]
   half_t* Kl = lds;
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     }
     __syncthreads();
   }
-
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1266,10 +1266,20 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.total_wg = L.ntiles * (a->kv_heads / HPW);
   k.per_xcd = (k.total_wg + 7) / 8;
   const dim3 grid(8 * k.per_xcd);
-  if (a->head_dim == 128)
-    hipLaunchKernelGGL(keys_scores_kernel<128>, grid, dim3(kK2Threads), 0, st, k);
-  else
-    hipLaunchKernelGGL(keys_scores_kernel<64>, grid, dim3(kK2Threads), 0, st, k);
+  // decoding (at most kSmallRows query rows per KV head) and question scoring are separate
+  // instantiations, so neither epilogue's registers weigh on the other's main loop
+  const bool small = (a->q_heads / a->kv_heads) * a->q_len <= kSmallRows;
+  if (a->head_dim == 128) {
+    if (small)
+      hipLaunchKernelGGL((keys_scores_kernel<128, true>), grid, dim3(kK2Threads), 0, st, k);
+    else
+      hipLaunchKernelGGL((keys_scores_kernel<128, false>), grid, dim3(kK2Threads), 0, st, k);
+  } else {
+    if (small)
+      hipLaunchKernelGGL((keys_scores_kernel<64, true>), grid, dim3(kK2Threads), 0, st, k);
+    else
+      hipLaunchKernelGGL((keys_scores_kernel<64, false>), grid, dim3(kK2Threads), 0, st, k);
+  }
   return dkv::check_launch("keys_scores");
 }
 
