@@ -31,7 +31,7 @@ from __future__ import annotations
 import torch
 
 import dkv_hip
-from hot_tier import LadderStream, LadderTables, PackedStream
+from hot_tier import LadderStream, LadderTables
 
 # Exact tokens one sequence may hold in the shared softmax (the kernels' exact-token split).
 MAX_EXACT_TOKENS = 1024
