@@ -7,7 +7,7 @@ the new token exact), key and value PCA bases of rank 2048, bf16 decode
 query.  One step = one decode token = 28 layers of attention over the codes
 (K2 key rebuild + scoring, K3 value weighting + basis), timed with HIP events.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg1|cfg0|cfg3]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3b-16k-3pct|1b-8k-2pct|1b-1500|3b-ragged-32]
 
 Prints one JSON line.  ``roofline`` is for the dominant kernel (K2,
 keys_scores): algorithmic MFMA flops per launch / its average duration,
@@ -38,10 +38,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="cfg2", choices=["cfg0", "cfg1", "cfg2", "cfg3"])
+    p.add_argument("--workload", default="3b-16k-3pct", choices=["1b-1500", "1b-8k-2pct", "3b-16k-3pct", "3b-ragged-32"])
     p.add_argument("--method", default="prog", choices=["prog", "dkvtc"],
                    help="entry point whose cache is decoded: prog@b:r0.01 (bit planes, default) or "
-                        "dkvtc@b:snap:floor1 (kvtc ladder codes; cfg1/cfg2)")
+                        "dkvtc@b:snap:floor1 (kvtc ladder codes; 1b-8k-2pct / 3b-16k-3pct)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-question", action="store_true", help="skip the question stage (score, select, gather)")
     p.add_argument("--cold-tier", choices=("device", "host"), default="device",
@@ -51,7 +51,7 @@ def parse():
                    help="rocprofv3 FETCH/WRITE summary of K2 for this workload "
                         "(default profiles/keys_scores_<config>[_dkvtc]_traffic.txt)")
     p.add_argument("--storage", action="store_true",
-                   help="measure kvtc byte storage at cfg2 (dkvtc): encode, DEFLATE, restore; one JSON line")
+                   help="measure kvtc byte storage at 3b-16k-3pct (dkvtc): encode, DEFLATE, restore; one JSON line")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -155,7 +155,7 @@ def question_stage(w):
 
 
 def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
-    """kvtc byte storage at the cfg2 shape (Llama-3.2-3B, 16,384 tokens, dkvtc@0.03:snap:floor1):
+    """kvtc byte storage at the 3b-16k-3pct workload (Llama-3.2-3B shape, 16,384 tokens, dkvtc@0.03:snap:floor1):
     GPU encode (quantize + dkv_wire_pack + one device-to-host copy), the two storage kernels alone
     (HIP events on their stream), host DEFLATE / INFLATE (zlib level 6), ``restore_context`` (one
     host-to-device copy + dkv_wire_unpack + ladder packing) and ``decode_bytes`` (FP16 rebuild).
@@ -173,7 +173,7 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
     from oracle import storage_ref
 
     dev = "cuda"
-    shape, tokens, budget, _ = workloads.CONFIGS["cfg2"]
+    shape, tokens, budget, _ = workloads.WORKLOADS["3b-16k-3pct"]
     ctx = synth.make_context(shape, tokens, 2024, device=dev)
     model = synth.RopeModel(shape, dev)
     m = methods.Methods("synthetic/llama-3.2", device=dev, model=model, kvtc=synth.kvtc_checkpoint(ctx))
@@ -246,7 +246,7 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
     t2 = time.perf_counter()
     mb = len(data) / 1e6
     result = {
-        "metric": "kvtc byte storage, cfg2 dkvtc@0.03:snap:floor1 (3B shape, 16K tokens)",
+        "metric": "kvtc byte storage, dkvtc@0.03:snap:floor1 (3B shape, 16K tokens)",
         "value": round(mb / (restore_ms / 1e3), 1), "unit": "MB/s restored into a CompressedContext",
         "higher_is_better": True, "data": "synthetic",
         "stored_bytes": len(data), "fp16_fraction": round(len(data) / (4 * features * tokens), 5),
@@ -284,23 +284,23 @@ def main():
     dev = "cuda"
     if args.traffic_file is None:
         suffix = "_dkvtc" if args.method == "dkvtc" else ""
-        args.traffic_file = str(ROOT / "profiles" / f"keys_scores_{args.config}{suffix}_traffic.txt")
+        args.traffic_file = str(ROOT / "profiles" / f"keys_scores_{args.workload}{suffix}_traffic.txt")
     t_build = time.perf_counter()
     if args.method == "dkvtc":
-        if args.config not in ("cfg1", "cfg2"):
-            print("--method dkvtc runs at cfg1 or cfg2", file=sys.stderr)
+        if args.workload not in ("1b-8k-2pct", "3b-16k-3pct"):
+            print("--method dkvtc runs at 1b-8k-2pct or 3b-16k-3pct", file=sys.stderr)
             sys.exit(2)
-        w = workloads.build_dkvtc(args.config, device=dev)
+        w = workloads.build_dkvtc(args.workload, device=dev)
         args.no_cpu_baseline = True
-    elif args.config == "cfg3":
+    elif args.workload == "3b-ragged-32":
         w = workloads.build_ragged(device=dev)
     else:
-        w = workloads.build_decode(args.config, device=dev, keep_host_basis=not args.no_cpu_baseline,
-                                   refine_fraction=0.01 if args.config == "cfg2" and not args.no_question else 0.0,
+        w = workloads.build_decode(args.workload, device=dev, keep_host_basis=not args.no_cpu_baseline,
+                                   refine_fraction=0.01 if args.workload == "3b-16k-3pct" and not args.no_question else 0.0,
                                    cold_tier=args.cold_tier)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t_build
-    print(f"[bench] built {args.config} in {build_s:.1f}s: {w.middle_total} compressed tokens, "
+    print(f"[bench] built {args.workload} in {build_s:.1f}s: {w.middle_total} compressed tokens, "
           f"{w.hot_code_bytes() / 2**20:.1f} MiB hot codes", file=sys.stderr, flush=True)
     question = question_stage(w) if hasattr(w, "question") else None
 
@@ -362,12 +362,12 @@ def main():
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": {"cfg2": "Llama-3.2-3B shape, 16384-token context at 3% budget, 28-layer decode",
-                         "cfg1": "Llama-3.2-1B shape, 8192-token context at 2% budget, 16-layer decode",
-                         "cfg0": "Llama-3.2-1B shape, 1500-token context, 16-layer decode",
-                         "cfg3": "32 ragged Llama-3.2-3B conversations U[2K,16K] at 3%, one varlen decode"}[args.config]
+            "workload": {"3b-16k-3pct": "Llama-3.2-3B shape, 16384-token context at 3% budget, 28-layer decode",
+                         "1b-8k-2pct": "Llama-3.2-1B shape, 8192-token context at 2% budget, 16-layer decode",
+                         "1b-1500": "Llama-3.2-1B shape, 1500-token context, 16-layer decode",
+                         "3b-ragged-32": "32 ragged Llama-3.2-3B conversations U[2K,16K] at 3%, one varlen decode"}[args.workload]
                         + (f", {w.name.split(':', 1)[1]} (kvtc ladder codes)" if args.method == "dkvtc" else ""),
-            "config": args.config,
+            "name": args.workload,
             "method": "dkvtc@b:snap:floor1" if args.method == "dkvtc" else "prog@b:r0.01",
             "compressed_tokens": w.middle_total,
             "exact_tokens_per_seq": list(w.exact_lengths)[:4],
@@ -400,7 +400,7 @@ def main():
     }
     if question is not None:
         result["question"] = question
-    if not args.no_cpu_baseline and args.config != "cfg3":
+    if not args.no_cpu_baseline and args.workload != "3b-ragged-32":
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

@@ -21,16 +21,16 @@ from compressed_attention import CompressedContext, ModelTables
 from hot_tier import OrderTables, PackedStream
 from progressive import plane_major_order, quantize8
 
-CONFIGS = {
-    # name: (shape, tokens, budget, query dtype)
-    "cfg0": (synth.SHAPE_1B, 1500, None, torch.float32),
-    "cfg1": (synth.SHAPE_1B, 8192, 0.02, torch.bfloat16),
-    "cfg2": (synth.SHAPE_3B, 16384, 0.03, torch.bfloat16),
+WORKLOADS = {
+    # name: (shape, tokens, budget, query dtype); the ragged batch is "3b-ragged-32" (build_ragged)
+    "1b-1500": (synth.SHAPE_1B, 1500, None, torch.float32),
+    "1b-8k-2pct": (synth.SHAPE_1B, 8192, 0.02, torch.bfloat16),
+    "3b-16k-3pct": (synth.SHAPE_3B, 16384, 0.03, torch.bfloat16),
 }
 # At 8K tokens the 36 exact tokens alone take 22 % of a 2 % budget, which leaves less than the
-# 2-plane floor (640 B/token K+V at rank 1024); config 1 quotes its budget per compressed token
+# 2-plane floor (640 B/token K+V at rank 1024); the 1B 8K workload quotes its budget per compressed token
 # (655.36 B/token = the floor plus top-ups), so its plane maps are drawn against that.
-BUDGET_OVER_MIDDLE = {"cfg1"}
+BUDGET_OVER_MIDDLE = {"1b-8k-2pct"}
 
 
 @dataclass
@@ -178,7 +178,7 @@ def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, re
     return streams
 
 
-def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
+def build_decode(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
                  shape: synth.ModelShape | None = None, tokens: int | None = None, budget: float | None = None,
                  query_dtype: torch.dtype | None = None, keep_host_basis: bool = False,
                  refine_fraction: float = 0.0, cold_tier: str = "device") -> DecodeWorkload:
@@ -186,8 +186,8 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
     host copies of the bases (for the CPU baseline); ``refine_fraction`` > 0 keeps a cold tier
     (in device memory, or pinned host memory with ``cold_tier="host"``) and room to refine that
     fraction of the tokens (the question stage)."""
-    if name in CONFIGS:
-        s0, t0, b0, qd0 = CONFIGS[name]
+    if name in WORKLOADS:
+        s0, t0, b0, qd0 = WORKLOADS[name]
         shape, tokens = shape or s0, tokens or t0
         budget = b0 if budget is None else budget
         query_dtype = query_dtype or qd0
@@ -224,7 +224,7 @@ def build_decode(name: str = "cfg2", seed: int = 2024, device="cuda", q_len: int
     return w
 
 
-def build_dkvtc(name: str = "cfg2", seed: int = 2024, device="cuda", budget: float | None = None,
+def build_dkvtc(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", budget: float | None = None,
                 method: str | None = None, query_dtype: torch.dtype | None = None) -> DecodeWorkload:
     """The ``dkvtc@<budget>:snap:floor1`` decode workload at a config's shape, built through the
     reference entry points: a synthetic prefill cache (fp16), ``Methods.apply`` (KVTCCodec.compress
@@ -234,7 +234,7 @@ def build_dkvtc(name: str = "cfg2", seed: int = 2024, device="cuda", budget: flo
     and one new token."""
     import methods
 
-    shape, tokens, b0, qd0 = CONFIGS[name]
+    shape, tokens, b0, qd0 = WORKLOADS[name]
     budget = b0 if budget is None else budget
     query_dtype = query_dtype or qd0
     method = method or f"dkvtc@{budget}:snap:floor1"
@@ -324,7 +324,7 @@ def build_ragged(count: int = 32, lo: int = 2048, hi: int = 16384, budget: float
     queries = (queries * torch.linspace(0.5, 1.5, count, device=device).to(query_dtype)[None, :, None, None, None])
     queries = queries.contiguous()
     outs = torch.empty(shape.layers, count, 1, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
-    w = DecodeWorkload("cfg3", shape, context, tables, streams, queries, key_exact, value_exact, outs,
+    w = DecodeWorkload("3b-ragged-32", shape, context, tables, streams, queries, key_exact, value_exact, outs,
                        tokens=sum(lengths), middle=cu[-1], exact_lengths=tuple(exact_len), batch=count)
     w.args = [context.layer_args(l, queries[l], outs[l], key_exact[l], value_exact[l], None, tuple(exact_len))
               for l in range(shape.layers)]

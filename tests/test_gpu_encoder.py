@@ -112,7 +112,7 @@ def test_encode_then_attend_over_codes():
     assert_close(out.cpu().numpy(), ref, what="encode->attend", base=base)
 
 
-def test_cfg4_fullsize_encode_bit_exact():
+def test_3b_16k_encode_bit_exact():
     """Config 4 at full size: Llama-3.2-3B shape, 16,384 tokens, 3 % budget, 2-plane floor.  quantize8
     bit for bit, the error table to float32 summation order, the allocation bit for bit on the GPU's
     errors (floor offset as scripts/kvtc.py:209-219), packed tiers byte for byte on sampled tokens,
@@ -124,7 +124,7 @@ def test_cfg4_fullsize_encode_bit_exact():
 
     shape = synth.SHAPE_3B
     tokens = 16384
-    print("[case] cfg4 full-size encode (3B, 16384 tokens, 3 %, 2-plane floor)", flush=True)
+    print("[case] full-size encode (3B, 16384 tokens, 3 %, 2-plane floor)", flush=True)
     ctx = synth.make_context(shape, tokens, seed=4040, device=DEV)
     model = synth.RopeModel(shape, DEV)
     codec = progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), synth.order_checkpoint(shape), DEV, model)

@@ -14,14 +14,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def test_cfg2_question_then_decode_matches_oracle():
+def test_3b_16k_question_then_decode_matches_oracle():
     import workloads
     from helpers import assert_close
     from oracle import attention_ref, scoring_ref
     from oracle import progressive_ref as pr
 
-    print("[case] full-size cfg2: question stage + decode step", flush=True)
-    w = workloads.build_decode("cfg2", device=DEV, keep_host_basis=True, refine_fraction=0.01)
+    print("[case] full size 3b-16k-3pct: question stage + decode step", flush=True)
+    w = workloads.build_decode("3b-16k-3pct", device=DEV, keep_host_basis=True, refine_fraction=0.01)
     s = w.shape
     # byte accounting of the packed hot tier (progressive.py:185-188) fits the 3 % budget
     hot = w.context.key.hot_bytes() + w.context.value.hot_bytes()
@@ -69,16 +69,16 @@ def test_cfg2_question_then_decode_matches_oracle():
                                ref.shape)
         # the benchmark's decode writes bf16 (the model's dtype): elementwise bar on that output;
         # the same layer with an fp32 output must also meet the relative Frobenius bar
-        assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"cfg2 layer {layer} (bf16 out)", rel_fro=1e9)
+        assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"3b-16k layer {layer} (bf16 out)", rel_fro=1e9)
         out32 = torch.empty(1, 1, s.q_heads, s.head_dim, dtype=torch.float32, device=DEV)
         args = w.context.layer_args(layer, w.queries[layer], out32, w.key_exact[layer], w.value_exact[layer])
         w.context.run_layer(args)
         torch.cuda.synchronize()
-        err, fro = assert_close(out32.cpu().numpy(), ref, what=f"cfg2 layer {layer}", base=base)
+        err, fro = assert_close(out32.cpu().numpy(), ref, what=f"3b-16k layer {layer}", base=base)
         print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
 
 
-def test_cfg2_dkvtc_decode_matches_oracle():
+def test_3b_16k_dkvtc_decode_matches_oracle():
     """The dkvtc@0.03:snap:floor1 entry point at full size: prefill -> Methods.apply ->
     CompressedContext(codec, keys, values, model) -> 28-layer decode over the ladder codes,
     deterministic, and equal to the oracle's attention over codec.last_coefficients on layers
@@ -87,8 +87,8 @@ def test_cfg2_dkvtc_decode_matches_oracle():
     from helpers import assert_close
     from oracle import attention_ref
 
-    print("[case] full-size cfg2: dkvtc decode step", flush=True)
-    w = workloads.build_dkvtc("cfg2", device=DEV)
+    print("[case] full size 3b-16k-3pct: dkvtc decode step", flush=True)
+    w = workloads.build_dkvtc("3b-16k-3pct", device=DEV)
     s, codec, ctx = w.shape, w.codec, w.context
     start, _ = codec.last_span
     choice_k = codec.last_choice["key"].cpu().numpy()

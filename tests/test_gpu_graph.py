@@ -12,8 +12,8 @@ pytestmark = pytest.mark.gpu
 def test_graph_replay_matches_eager():
     import workloads
 
-    print("[case] graph replay of a cfg0 decode step", flush=True)
-    w = workloads.build_decode("cfg0", device="cuda")
+    print("[case] graph replay of a 1b-1500 decode step", flush=True)
+    w = workloads.build_decode("1b-1500", device="cuda")
     w.step()
     torch.cuda.synchronize()
     eager = w.outs.clone()

@@ -10,7 +10,7 @@
   tokens agree to float32 rounding);
 - ``restore_context`` rebuilds ladder streams byte-identical to the in-memory
   ``CompressedContext``'s and answers identically (bit for bit without exact-rung tokens);
-- at the cfg2 shape (Llama-3.2-3B, 16,384 tokens, dkvtc@0.03:snap:floor1) the bytes survive
+- at the 3b-16k-3pct workload (Llama-3.2-3B shape, 16,384 tokens, dkvtc@0.03:snap:floor1) the bytes survive
   DEFLATE and restore to byte-identical streams; encode / restore timings are printed.
 """
 
@@ -137,13 +137,13 @@ def test_restore_context_matches_in_memory(name, seed):
             assert err <= 1e-2 * float(outs[1].abs().max()) + 1e-3
 
 
-def test_cfg2_storage_round_trip_fullsize():
+def test_3b_16k_storage_round_trip():
     import kvtc_storage
     import workloads
     from compressed_attention import CompressedContext
 
-    print("[case] storage cfg2 full size (3B shape, 16384 tokens, dkvtc@0.03:snap:floor1)", flush=True)
-    shape, tokens, budget, _ = workloads.CONFIGS["cfg2"]
+    print("[case] storage full size (3B shape, 16384 tokens, dkvtc@0.03:snap:floor1)", flush=True)
+    shape, tokens, budget, _ = workloads.WORKLOADS["3b-16k-3pct"]
     _, model, m, codec, keys, values, _ = _case(f"dkvtc@{budget}:snap:floor1", 2024, shape=shape, tokens=tokens)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
