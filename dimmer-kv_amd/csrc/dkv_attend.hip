@@ -91,7 +91,7 @@ struct DecodeArgs {
   dkv_stream_t s;
   const int32_t* cu_seqlens;
   uint16_t* coef;  // keys: fp16 in MFMA fragment order (see decode_keys_kernel)
-  int batch, ntiles, n_slots, G, plane_cap;
+  int batch, n_total, ntiles, n_slots, G, plane_cap;
 };
 
 constexpr int kDecodeTok = 128;  // slots per decode block
@@ -108,10 +108,11 @@ DKV_DEVICE int2 decode_block(int G, int nblocks) {
 DKV_DEVICE int slot_token(const DecodeArgs& a, int slot) {
   const int tile = slot / kTileTok;
   if (tile >= a.ntiles) return -1;
-  const int2 bt = find_tile(a.cu_seqlens, a.batch, kTileTok, tile);
-  const int tok0 = a.cu_seqlens[bt.x] + bt.y * kTileTok;
+  const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, bt.x);
+  const int tok0 = sr.x + bt.y * kTileTok;
   const int n = slot - tile * kTileTok;
-  return n < a.cu_seqlens[bt.x + 1] - tok0 ? tok0 + n : -1;
+  return n < sr.y - tok0 ? tok0 + n : -1;
 }
 
 // The value side's per-step buffers are blocked by 16 slots so that a wave's
@@ -375,10 +376,11 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   if (lin >= a.total_wg) return;
   const int nhg = a.Hkv / HPW;
   const int tile = lin / nhg, hg = lin % nhg;
-  const int2 bt = find_tile(a.cu_seqlens, a.batch, kTileTok, tile);
+  const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
   const int b = bt.x;
-  const int tok0 = a.cu_seqlens[b] + bt.y * kTileTok;
-  const int count = min(kTileTok, a.cu_seqlens[b + 1] - tok0);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int tok0 = sr.x + bt.y * kTileTok;
+  const int count = min(kTileTok, sr.y - tok0);
   const int h0 = hg * HPW;
   const int G = a.G;
 
@@ -799,10 +801,11 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   const int rbk = bid % a.row_blocks;
   const int g = (bid / a.row_blocks) % a.G;
   const int sp = bid / (a.row_blocks * a.G);
-  const int2 bs = find_tile(a.cu_seqlens, a.batch, kSplitTok, sp);
+  const int2 bs = find_tile(a.cu_seqlens, a.batch, a.n_total, kSplitTok, sp);
   const int b = bs.x;
-  const int tok0 = a.cu_seqlens[b] + bs.y * kSplitTok;
-  const int count = min(kSplitTok, a.cu_seqlens[b + 1] - tok0);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int tok0 = sr.x + bs.y * kSplitTok;
+  const int count = min(kSplitTok, sr.y - tok0);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -837,7 +840,7 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   const float mt = (row_ok && wt0 < count) ? a.tile_max[(long)my_row * a.ntiles + tile] : -INFINITY;
   *(float4*)&saff[wave][2 * lane] = aff2;
   if (tid < 256) {
-    const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
+    const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
     const int r = rbk * 32 + (tid >> 3);
     const float m = rows_max8(a.tile_max, a.ntiles, tb0, ntb, r, r < a.R_total, tid & 7);
     if ((tid & 7) == 0) Mrow[tid >> 3] = m;
@@ -894,30 +897,212 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// K3b: per (sequence, KV head, 128-component chunk): sum the partials over the
-// sequence's splits, multiply once by the value-basis chunk [128][D].
+// K3b: two kinds of workgroup in one launch.
+// - Row workgroups (the last batch * R_total, 4 waves each), one per
+//   (sequence, output row): merge the tiles' softmax statistics of the
+//   compressed part with the exact tokens (sinks, recent window, new tokens)
+//   in one softmax, and write the row's final affine form
+//     out = scale * (sum of its chunk partials) + base,
+//   scale = e_c / L, base = (e_c * L_c * mean_v + sum_e p_e * v_e) / L.
+//   This is all latency (dependent round trips to memory), so it runs beside
+//   the chunk workgroups instead of after them.
+// - Chunk workgroups, one per (sequence, KV head, 128-component chunk): sum
+//   the partials over the sequence's splits, multiply once by the value-basis
+//   chunk [128][D].
 // ---------------------------------------------------------------------------
 constexpr int kMaxExact = 1024;
+
+struct RowMergeArgs {
+  const int32_t* cu_seqlens;
+  const int32_t* cu_exact;
+  const float* tile_max;
+  const float* tile_sum;
+  const float* mean_v;
+  const float* key_exact;
+  const float* value_exact;
+  const float* mask;
+  const void* query;
+  float* row_scale;  // [batch * R_total]
+  float* row_base;   // [batch * R_total][D]
+  float scaling;
+  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles;
+  int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
+};
 
 struct K3bArgs {
   const int32_t* cu_seqlens;
   const float* w_part;
   const uint16_t* value_basis;
   float* out_part;
-  int batch, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
+  int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
+  RowMergeArgs m;
 };
 
+constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
+
+__device__ void row_merge(const RowMergeArgs& a, int wg) {
+  __shared__ float q[128];
+  __shared__ float se[kMaxExact];
+  __shared__ float wred[2][4];
+  __shared__ float buf[256];
+  __shared__ float bc[2];
+  const int row = wg % a.R_total;
+  const int b = wg / a.R_total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int D = a.D;
+  const int gq = a.Hq / a.Hkv;
+  const int qh = row / a.q_len, qi = row % a.q_len;
+  const int h = qh / gq;
+  const int e0 = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
+  const int E = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
+  const int d = tid % D, part = tid / D, parts = 256 / D;
+  // Every global load of the first 64 exact tokens goes out in one round, before any wait: each
+  // dependent round trip to memory costs microseconds here, and this work is nothing but them.
+  // (1) the tiles' softmax statistics (wave 0; 4 tiles per lane at once), (2) the query, (3) a
+  // quarter key row (token tid / 4, 32 dimensions), (4) exact values.
+  float mm = -INFINITY, ll = 0.0f;
+  if (wave == 0) {
+    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+    const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+    const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
+    const float* tm = a.tile_max + (long)row * a.ntiles + tb0;
+    const float* ts = a.tile_sum + (long)row * a.ntiles + tb0;
+    float m4[4], s4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = min(lane + 64 * k, max(ntb - 1, 0));
+      m4[k] = ntb > 0 ? tm[t] : -INFINITY;
+      s4[k] = ntb > 0 ? ts[t] : 0.0f;
+    }
+    auto merge = [&](float mt, float st) {  // online merge of this lane's tiles
+      if (mt == -INFINITY) return;
+      if (mt > mm) {
+        ll = ll * __expf(mm - mt) + st;
+        mm = mt;
+      } else {
+        ll += st * __expf(mt - mm);
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
+    for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
+  }
+  if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
+  const int kj = tid >> 2, ks = tid & 3;
+  const bool kslice = ks * 32 < D;
+  float4 k4[8];
+  float mval = 0.0f;
+  if (E > 0) {
+    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
+                                       min(ks * 32, D - 32));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
+  }
+  float vv[kExactVB];
+#pragma unroll
+  for (int i = 0; i < kExactVB; ++i)
+    vv[i] = E > 0 ? a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d] : 0.0f;
+  if (wave == 0) {
+    const float m = wave_max(mm);
+    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
+    if (lane == 0) {
+      bc[0] = m;
+      bc[1] = l;
+    }
+  }
+  __syncthreads();
+  // exact scores: four lanes per token, 32 dimensions each, 64 tokens per pass
+  float me = -INFINITY;
+  const int E64 = (E + 63) & ~63;
+  for (int j = kj; j < E64; j += 64) {
+    if (j != kj && j < E) {
+      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+      if (a.mask) mval = a.mask[(long)qi * E + j];
+    }
+    float dot = 0.0f;
+    if (kslice) {
+      const float* qr = q + ks * 32;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
+    }
+    dot += lane_xor1(dot);
+    dot += lane_xor2(dot);
+    if (j < E) {
+      const float sc = dot * a.scaling + mval;
+      if (ks == 0) se[j] = sc;
+      me = fmaxf(me, sc);
+    }
+  }
+  me = wave_max(me);
+  if (lane == 0) wred[0][wave] = me;
+  __syncthreads();
+  const float Mc = bc[0], Lc = bc[1];
+  const float Me = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+  const float M = fmaxf(Mc, Me);
+  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
+  float le = 0.0f;
+  for (int j = tid; j < E; j += 256) {
+    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
+    se[j] = wgt;
+    le += wgt;
+  }
+  le = wave_sum(le);
+  if (lane == 0) wred[1][wave] = le;
+  __syncthreads();
+  const float Le = wred[1][0] + wred[1][1] + wred[1][2] + wred[1][3];
+  const float denom = ec * Lc + Le;
+  // exact values: thread (d, part) takes tokens part, part + parts, ...
+  float ve = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kExactVB; ++i) {
+    const int j = part + i * parts;
+    if (j < E) ve += se[j] * vv[i];
+  }
+  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
+    float v8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = j0 + i * parts;
+      if (j < E) ve += se[j] * v8[i];
+    }
+  }
+  buf[tid] = ve;
+  __syncthreads();
+  if (tid < D) {
+    float ves = 0.0f;
+    for (int p = 0; p < parts; ++p) ves += buf[p * D + tid];
+    const float cm = ec * Lc * a.mean_v[((long)a.layer * a.Hkv + h) * D + tid];
+    a.row_base[(long)wg * D + tid] = denom > 0.0f ? (cm + ves) / denom : 0.0f;
+    if (tid == 0) a.row_scale[wg] = denom > 0.0f ? ec / denom : 0.0f;
+  }
+}
+
 __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
+  // the row workgroups come after the chunk workgroups (measured faster than before them)
+  const int chunk_wgs = (int)gridDim.x - a.batch * a.R_total;
+  if ((int)blockIdx.x >= chunk_wgs) {
+    row_merge(a.m, blockIdx.x - chunk_wgs);
+    return;
+  }
   __shared__ float W[8][kChunk];
   __shared__ float red[4][8][130];
-  const int c = blockIdx.x % a.nchunks;
-  const int h = (blockIdx.x / a.nchunks) % a.Hkv;
-  const int b = blockIdx.x / (a.nchunks * a.Hkv);
+  const int bid = blockIdx.x;
+  const int c = bid % a.nchunks;
+  const int h = (bid / a.nchunks) % a.Hkv;
+  const int b = bid / (a.nchunks * a.Hkv);
   const int tid = threadIdx.x;
   const int gq = a.Hq / a.Hkv;
   const int RH = gq * a.q_len;
   const int sp0 = tiles_before(a.cu_seqlens, b, kSplitTok);
-  const int nsp = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kSplitTok - 1) / kSplitTok;
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int nsp = (sr.y - sr.x + kSplitTok - 1) / kSplitTok;
   const int D = a.D;
   const int npair = D / 2;
   const int parts = 256 / npair;  // 4 (D=128) or 8 (D=64)
@@ -992,174 +1177,39 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// K3c: one workgroup (4 waves) per (sequence, output row): exact tokens in the
-// same softmax as the compressed part, sum(p) * mean_v, normalisation.
+// K3c: one thread per (sequence, output row, dimension):
+// out = scale * (sum of the row's chunk partials, in chunk order) + base.
 // ---------------------------------------------------------------------------
 struct K3cArgs {
-  const int32_t* cu_seqlens;
-  const int32_t* cu_exact;
-  const float* tile_max;
-  const float* tile_sum;
-  const float* out_part;
-  const float* mean_v;
-  const float* key_exact;
-  const float* value_exact;
-  const float* mask;
-  const void* query;
+  const float* out_part;   // [nchunks][batch * R_total][D]
+  const float* row_scale;  // [batch * R_total]
+  const float* row_base;   // [batch * R_total][D]
   void* out;
-  float scaling;
-  int batch, layer, Hkv, Hq, q_len, D, R_total, nchunks, E_total, query_dtype, out_dtype, ntiles;
+  int batch, Hq, q_len, D, R_total, nchunks, out_dtype;
 };
 
-constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
+constexpr int kFinishThreads = 64;
 
-__global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
-  __shared__ float q[128];
-  __shared__ float se[kMaxExact];
-  __shared__ float wred[2][4];
-  __shared__ float buf[2][256];
-  __shared__ float bc[2];
-  const int row = blockIdx.x % a.R_total;
-  const int b = blockIdx.x / a.R_total;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int D = a.D;
-  const int gq = a.Hq / a.Hkv;
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(K3cArgs a) {
+  const long n = (long)a.batch * a.R_total * a.D;
+  const long i = (long)blockIdx.x * kFinishThreads + threadIdx.x;
+  if (i >= n) return;
+  const int d = (int)(i % a.D);
+  const long br = i / a.D;
+  const int row = (int)(br % a.R_total);
+  const int b = (int)(br / a.R_total);
+  const float scale = a.row_scale[br];
+  const float base = a.row_base[i];
+  float s = 0.0f;
+  for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = a.out_part[(long)min(c0 + k, a.nchunks - 1) * n + i];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s += c0 + k < a.nchunks ? v[k] : 0.0f;
+  }
   const int qh = row / a.q_len, qi = row % a.q_len;
-  const int h = qh / gq;
-  const int e0 = a.cu_exact ? a.cu_exact[b] : 0;
-  const int E = a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
-  const int d = tid % D, part = tid / D, parts = 256 / D;
-  // Every global load of the first 64 exact tokens goes out in one round, before any wait: each
-  // dependent round trip to memory costs microseconds here, and this kernel is nothing but them.
-  // (1) the tiles' softmax statistics (wave 0), (2) the query, (3) this thread's share of the
-  // chunk partials, (4) a quarter key row (token tid / 4, 32 dimensions), (5) exact values.
-  float mm = -INFINITY, ll = 0.0f;
-  if (wave == 0) {
-    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-    const int ntb = (a.cu_seqlens[b + 1] - a.cu_seqlens[b] + kTileTok - 1) / kTileTok;
-    const float* tm = a.tile_max + (long)row * a.ntiles + tb0;
-    const float* ts = a.tile_sum + (long)row * a.ntiles + tb0;
-    for (int t = lane; t < ntb; t += 64) {  // online merge of this lane's tiles
-      const float mt = tm[t], st = ts[t];
-      if (mt == -INFINITY) continue;
-      if (mt > mm) {
-        ll = ll * __expf(mm - mt) + st;
-        mm = mt;
-      } else {
-        ll += st * __expf(mt - mm);
-      }
-    }
-  }
-  if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
-  const int my_chunks = (a.nchunks - part + parts - 1) / parts;
-  float vparts[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = part + min(i, max(my_chunks - 1, 0)) * parts;
-    vparts[i] = my_chunks > 0 ? a.out_part[(((long)c * a.batch + b) * a.R_total + row) * D + d] : 0.0f;
-  }
-  const int kj = tid >> 2, ks = tid & 3;
-  const bool kslice = ks * 32 < D;
-  float4 k4[8];
-  float mval = 0.0f;
-  if (E > 0) {
-    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
-                                       min(ks * 32, D - 32));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
-    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
-  }
-  float vv[kExactVB];
-#pragma unroll
-  for (int i = 0; i < kExactVB; ++i)
-    vv[i] = E > 0 ? a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d] : 0.0f;
-  // the chunk partials beyond the first batch (many components only)
-  float vc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) vc += i < my_chunks ? vparts[i] : 0.0f;
-  for (int i = 8; i < my_chunks; ++i) vc += a.out_part[(((long)(part + i * parts) * a.batch + b) * a.R_total + row) * D + d];
-  if (wave == 0) {
-    const float m = wave_max(mm);
-    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
-    if (lane == 0) {
-      bc[0] = m;
-      bc[1] = l;
-    }
-  }
-  __syncthreads();
-  // exact scores: four lanes per token, 32 dimensions each, 64 tokens per pass
-  float me = -INFINITY;
-  const int E64 = (E + 63) & ~63;
-  for (int j = kj; j < E64; j += 64) {
-    if (j != kj && j < E) {
-      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
-      if (a.mask) mval = a.mask[(long)qi * E + j];
-    }
-    float dot = 0.0f;
-    if (kslice) {
-      const float* qr = q + ks * 32;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
-    }
-    dot += lane_xor1(dot);
-    dot += lane_xor2(dot);
-    if (j < E) {
-      const float sc = dot * a.scaling + mval;
-      if (ks == 0) se[j] = sc;
-      me = fmaxf(me, sc);
-    }
-  }
-  me = wave_max(me);
-  if (lane == 0) wred[0][wave] = me;
-  __syncthreads();
-  const float Mc = bc[0], Lc = bc[1];
-  const float Me = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
-  const float M = fmaxf(Mc, Me);
-  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
-  float le = 0.0f;
-  for (int j = tid; j < E; j += 256) {
-    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
-    se[j] = wgt;
-    le += wgt;
-  }
-  le = wave_sum(le);
-  if (lane == 0) wred[1][wave] = le;
-  __syncthreads();
-  const float Le = wred[1][0] + wred[1][1] + wred[1][2] + wred[1][3];
-  const float denom = ec * Lc + Le;
-  // exact values: thread (d, part) takes tokens part, part + parts, ...
-  float ve = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kExactVB; ++i) {
-    const int j = part + i * parts;
-    if (j < E) ve += se[j] * vv[i];
-  }
-  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
-    float v8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = j0 + i * parts;
-      if (j < E) ve += se[j] * v8[i];
-    }
-  }
-  buf[0][tid] = vc;
-  buf[1][tid] = ve;
-  __syncthreads();
-  if (tid < D) {
-    float vcs = 0.0f, ves = 0.0f;
-    for (int p = 0; p < parts; ++p) {
-      vcs += buf[0][p * D + tid];
-      ves += buf[1][p * D + tid];
-    }
-    vcs += Lc * a.mean_v[((long)a.layer * a.Hkv + h) * D + tid];
-    const float o = denom > 0.0f ? (ec * vcs + ves) / denom : 0.0f;
-    store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * D + tid, a.out_dtype, o);
-  }
+  store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * a.D + d, a.out_dtype, scale * s + base);
 }
 
 // ---------------------------------------------------------------------------
@@ -1167,13 +1217,13 @@ __global__ __launch_bounds__(256) void finish_kernel(K3cArgs a) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
-  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, total;
+  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, row_scale, row_base, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
-// [split partials][chunk partials].
+// [split partials][chunk partials][row scales][row bases].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
@@ -1207,6 +1257,10 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)L.nsplits * L.R_total * a->rank * 4);
   L.out_part = off;
   off += align256((size_t)L.nchunks * a->batch * L.R_total * a->head_dim * 4);
+  L.row_scale = off;
+  off += align256((size_t)a->batch * L.R_total * 4);
+  L.row_base = off;
+  off += align256((size_t)a->batch * L.R_total * a->head_dim * 4);
   L.total = off;
   return L;
 }
@@ -1308,6 +1362,7 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   d.cu_seqlens = a->cu_seqlens;
   d.coef = (uint16_t*)((char*)workspace + L.coef);
   d.batch = a->batch;
+  d.n_total = L.n_total;
   d.ntiles = L.ntiles;
   d.n_slots = L.n_slots;
   d.G = dkv::stream_groups(a->key);
@@ -1399,6 +1454,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.value_basis = a->value_basis;
   kb.out_part = (float*)(ws + L.out_part);
   kb.batch = a->batch;
+  kb.n_total = L.n_total;
   kb.layer = a->layer;
   kb.Hkv = a->kv_heads;
   kb.Hq = a->q_heads;
@@ -1407,35 +1463,51 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.rank = a->rank;
   kb.R_total = L.R_total;
   kb.nchunks = L.nchunks;
-  hipLaunchKernelGGL(basis_apply_kernel, dim3(a->batch * a->kv_heads * L.nchunks), dim3(256), 0, st, kb);
+  RowMergeArgs& m = kb.m;
+  m.cu_seqlens = a->cu_seqlens;
+  m.cu_exact = a->cu_exact;
+  m.tile_max = (const float*)(ws + L.tile_max);
+  m.tile_sum = (const float*)(ws + L.tile_sum);
+  m.ntiles = L.ntiles;
+  m.mean_v = a->mean_v;
+  m.key_exact = a->key_exact;
+  m.value_exact = a->value_exact;
+  m.mask = a->mask;
+  m.query = a->query;
+  m.row_scale = (float*)(ws + L.row_scale);
+  m.row_base = (float*)(ws + L.row_base);
+  m.scaling = a->scaling;
+  m.batch = a->batch;
+  m.n_total = L.n_total;
+  m.e0_single = a->cu_exact ? a->cu_exact_host[0] : 0;
+  m.e_single = a->cu_exact ? a->cu_exact_host[1] - a->cu_exact_host[0] : 0;
+  m.layer = a->layer;
+  m.Hkv = a->kv_heads;
+  m.Hq = a->q_heads;
+  m.q_len = a->q_len;
+  m.D = a->head_dim;
+  m.R_total = L.R_total;
+  m.E_total = E_total;
+  m.query_dtype = a->query_dtype;
+  const long k3b_blocks = (long)a->batch * L.R_total + (long)a->batch * a->kv_heads * L.nchunks;
+  hipLaunchKernelGGL(basis_apply_kernel, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
   rc = dkv::check_launch("basis_apply");
   if (rc) return rc;
   K3cArgs kc{};
-  kc.cu_seqlens = a->cu_seqlens;
-  kc.cu_exact = a->cu_exact;
-  kc.tile_max = (const float*)(ws + L.tile_max);
-  kc.tile_sum = (const float*)(ws + L.tile_sum);
-  kc.ntiles = L.ntiles;
   kc.out_part = (const float*)(ws + L.out_part);
-  kc.mean_v = a->mean_v;
-  kc.key_exact = a->key_exact;
-  kc.value_exact = a->value_exact;
-  kc.mask = a->mask;
-  kc.query = a->query;
+  kc.row_scale = (const float*)(ws + L.row_scale);
+  kc.row_base = (const float*)(ws + L.row_base);
   kc.out = a->out;
-  kc.scaling = a->scaling;
   kc.batch = a->batch;
-  kc.layer = a->layer;
-  kc.Hkv = a->kv_heads;
   kc.Hq = a->q_heads;
   kc.q_len = a->q_len;
   kc.D = a->head_dim;
   kc.R_total = L.R_total;
   kc.nchunks = L.nchunks;
-  kc.E_total = E_total;
-  kc.query_dtype = a->query_dtype;
   kc.out_dtype = a->out_dtype;
-  hipLaunchKernelGGL(finish_kernel, dim3(a->batch * L.R_total), dim3(256), 0, st, kc);
+  const long outs = (long)a->batch * L.R_total * a->head_dim;
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((outs + kFinishThreads - 1) / kFinishThreads)),
+                     dim3(kFinishThreads), 0, st, kc);
   return dkv::check_launch("finish");
 }
 

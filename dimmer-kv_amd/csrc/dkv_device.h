@@ -231,8 +231,10 @@ DKV_DEVICE void ladder_half_f16(const uint32_t (&cw)[8], uint32_t header, uint32
 
 // Sequence/tile lookup from cu_seqlens without a host-built table: returns
 // the sequence b and the tile index inside it for a global tile id, where
-// sequence b has ceil(len_b / tile) tiles.
-DKV_DEVICE int2 find_tile(const int32_t* cu, int batch, int tile, int gid) {
+// sequence b has ceil(len_b / tile) tiles.  One sequence (n_total tokens)
+// needs no load.
+DKV_DEVICE int2 find_tile(const int32_t* cu, int batch, int n_total, int tile, int gid) {
+  if (batch == 1) return make_int2(gid < (n_total + tile - 1) / tile ? 0 : -1, gid);
   int base = 0;
   for (int b = 0; b < batch; ++b) {
     const int len = cu[b + 1] - cu[b];
@@ -241,6 +243,13 @@ DKV_DEVICE int2 find_tile(const int32_t* cu, int batch, int tile, int gid) {
     base += nt;
   }
   return make_int2(-1, 0);
+}
+
+// First and one-past-last token of sequence b.  With one sequence they are 0
+// and n_total from the kernel arguments, so the first data loads do not wait
+// on a load of cu_seqlens.
+DKV_DEVICE int2 seq_range(const int32_t* cu, int batch, int n_total, int b) {
+  return batch == 1 ? make_int2(0, n_total) : make_int2(cu[b], cu[b + 1]);
 }
 
 // ---------------------------------------------------------------------------

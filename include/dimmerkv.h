@@ -194,7 +194,9 @@ int dkv_prepare_value_basis(const float* basis, int32_t layers, int32_t kv_heads
  * Sequences: `batch` conversations share the packed streams; sequence b owns
  * compressed tokens [cu_seqlens[b], cu_seqlens[b+1]) and exact tokens
  * [cu_exact[b], cu_exact[b+1]) (both int32 device arrays, batch+1 entries;
- * cu_seqlens_host mirrors cu_seqlens on the host to size the launch). */
+ * cu_seqlens_host mirrors cu_seqlens on the host to size the launch; with
+ * batch == 1 the kernels take the lengths from the host mirrors, so a
+ * captured graph replays with the lengths it was captured with). */
 typedef struct dkv_attend_args {
   int32_t batch, q_len;
   int32_t layers, layer, kv_heads, head_dim, q_heads, rank;

@@ -66,9 +66,10 @@ def attend(query, coef_k, coef_v, basis_k_layer, basis_v_layer, mean_k_layer, me
     probabilities = _softmax(np.concatenate(parts, axis=-1).astype(np.float32)).astype(dtype)
     p_c, p_e = probabilities[..., :middle], probabilities[..., middle:]
     out = p_c.sum(axis=-1, keepdims=True) * mean_v_layer.astype(dtype).reshape(1, heads, 1, 1, dim)
-    weighted = np.einsum("bhgqn,nr->bhgqr", p_c, coef_v.astype(dtype))
-    layer_basis = basis_v_layer.astype(dtype).reshape(-1, heads, dim)
-    out = out + np.einsum("bhgqr,rhd->bhgqd", weighted, layer_basis)
+    if middle > 0:  # no einsum over an empty token axis: its result is not reliably zero-filled
+        weighted = np.einsum("bhgqn,nr->bhgqr", p_c, coef_v.astype(dtype))
+        layer_basis = basis_v_layer.astype(dtype).reshape(-1, heads, dim)
+        out = out + np.einsum("bhgqr,rhd->bhgqd", weighted, layer_basis)
     if p_e.shape[-1] > 0:
         out = out + np.einsum("bhgqn,bhnd->bhgqd", p_e, value_exact.astype(dtype))
     return out.reshape(batch, q_heads, q_len, dim).transpose(0, 2, 1, 3).astype(dtype)

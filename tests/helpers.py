@@ -118,6 +118,8 @@ def assert_close(got: np.ndarray, ref: np.ndarray, atol=2e-3, rtol=1e-2, rel_fro
     catches structural mistakes the loose absolute bound would hide."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
+    assert np.isfinite(ref).all(), f"{what}: the oracle's output is not finite"
+    assert np.isfinite(got).all(), f"{what}: the GPU output is not finite"
     err = np.abs(got - ref)
     ok = err <= atol + rtol * np.abs(ref)
     fro = np.linalg.norm(got - ref) / max(np.linalg.norm(ref - base), 1e-30)

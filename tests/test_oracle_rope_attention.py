@@ -138,6 +138,19 @@ def test_zero_query_gives_plain_average():
         np.testing.assert_allclose(got[0, :, qh], np.broadcast_to(want[qh // 3], (2, dim)), rtol=1e-5, atol=1e-6)
 
 
+def test_no_compressed_tokens_is_plain_attention_over_the_exact_tokens():
+    """A conversation shorter than sinks + recent has no compressed token: the output is textbook
+    softmax attention over the exact tokens (torch's SDPA in float64, GQA by repeating KV heads)."""
+    p = _problem(6, n=0)
+    got = ar.attend(**p)
+    assert np.isfinite(got).all()
+    K = torch.from_numpy(np.repeat(p["key_exact"].astype(np.float64), 3, axis=1))
+    V = torch.from_numpy(np.repeat(p["value_exact"].astype(np.float64), 3, axis=1))
+    out = torch.nn.functional.scaled_dot_product_attention(torch.from_numpy(p["query"].astype(np.float64)), K, V,
+                                                           attn_mask=torch.from_numpy(p["mask"].astype(np.float64)))
+    np.testing.assert_allclose(got, out.transpose(1, 2).numpy(), rtol=1e-5, atol=1e-6)
+
+
 def test_single_token_gives_its_value():
     p = _problem(5, n=1)
     p["key_exact"] = p["value_exact"] = p["mask"] = None
