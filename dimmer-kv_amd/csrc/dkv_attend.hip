@@ -473,7 +473,9 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   // Branch-free loop (group indices past the end are clamped; the surplus
   // basis block lands in a buffer nobody reads); sched_barrier keeps the
-  // compiler from sinking the loads below the MFMAs.
+  // compiler from sinking the loads below the MFMAs.  A wave in its MFMA
+  // block runs at raised priority, so the SIMD's other wave does not take
+  // issue slots from it there (measured 0.4 % faster per decode step).
   DKV_K2_ISSUE_A(0, af0);
   DKV_K2_ISSUE_B(0);
   DKV_K2_FINISH(0);
@@ -483,14 +485,18 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     DKV_K2_ISSUE_B(g + 1);
     DKV_K2_ISSUE_A(g + 1, af1);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(0, af0);
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
     DKV_K2_FINISH(1);
     __syncthreads();
     DKV_K2_ISSUE_B(g2);
     DKV_K2_ISSUE_A(g2, af0);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(1, af1);
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
     DKV_K2_FINISH(0);
   }
