@@ -403,13 +403,15 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   // Coefficient operands come straight from the decoded buffer (one 16-byte
   // load per lane per MFMA operand); the basis block [256][64] goes global ->
-  // registers -> padded, double-buffered LDS.  Both are fetched one group ahead.
+  // registers -> padded, double-buffered LDS, each row half by its own waves.
+  // Both are fetched ahead (coefficients three segments, basis two).
   const half8* coef_frag = (const half8*)a.coef + ((long)(tile * 8 + tq * 2) * 4) * 64 + lane;
   const long coef_group_stride = (long)(a.n_slots / 32) * 4 * 64;  // in half8 units
   const uint16_t* basis_layer = a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h0 * D * 64;
   const long basis_group_stride = (long)a.Hkv * D * 64;
 
   half_t* B0 = lds;  // basis [2][256][72]
+  const int gt = tid & 255;  // thread within its row half
 
   const float* mean_rows = a.mean_k + ((long)a.layer * a.Hkv + h0) * D + hs * 128 + 4 * lhi;
   floatx16 acc[2][4];
@@ -438,15 +440,15 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
 #define DKV_K2_ISSUE_B(g_)                                                            \
   do {                                                                                \
-    const uint4* src_ = (const uint4*)(basis_layer + (long)(g_) * basis_group_stride); \
-    br0 = src_[0 * kK2Threads + tid];                                                 \
-    br1 = src_[1 * kK2Threads + tid];                                                 \
-    br2 = src_[2 * kK2Threads + tid];                                                 \
-    br3 = src_[3 * kK2Threads + tid];                                                 \
+    const uint4* src_ = (const uint4*)(basis_layer + (long)(g_) * basis_group_stride) + hs * 1024; \
+    br0 = src_[0 * 256 + gt];                                                         \
+    br1 = src_[1 * 256 + gt];                                                         \
+    br2 = src_[2 * 256 + gt];                                                         \
+    br3 = src_[3 * 256 + gt];                                                         \
   } while (0)
 
 #define DKV_K2_STORE(dst_, j_, v_) \
-  *(uint4*)((dst_) + (((j_) * kK2Threads + tid) >> 3) * kStride + (tid & 7) * 8) = (v_)
+  *(uint4*)((dst_) + (hs * 128 + (((j_) * 256 + gt) >> 3)) * kStride + (gt & 7) * 8) = (v_)
 
 #define DKV_K2_FINISH(buf_)                                \
   do {                                                     \
@@ -472,34 +474,46 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   } while (0)
 
   // Branch-free loop (group indices past the end are clamped; the surplus
-  // basis block lands in a buffer nobody reads); sched_barrier keeps the
-  // compiler from sinking the loads below the MFMAs.  A wave in its MFMA
-  // block runs at raised priority, so the SIMD's other wave does not take
-  // issue slots from it there (measured 0.4 % faster per decode step).
+  // basis block lands in a buffer nobody reads).  Ping-pong: the two row
+  // halves (waves 0-3 and 4-7, one of each on every SIMD) each load and read
+  // only their own 128 basis rows, and alternate MFMA segments with memory
+  // segments (LDS writes of the next block, next loads), one barrier apart:
+  // half 1 starts one barrier late and half 0 ends one barrier late, so every
+  // wave executes the same number of barriers and, between two barriers, one
+  // wave of a SIMD runs MFMAs while the other does its memory work.
+  // sched_barrier keeps the compiler from moving loads into the MFMA
+  // segments; a wave in its MFMA segment runs at raised priority.
   DKV_K2_ISSUE_A(0, af0);
   DKV_K2_ISSUE_B(0);
   DKV_K2_FINISH(0);
+  DKV_K2_ISSUE_B(1);
+  DKV_K2_ISSUE_A(1, af1);
+  __syncthreads();
+  if (hs == 1) __builtin_amdgcn_s_barrier();
   for (int g = 0; g < G; g += 2) {  // G is a multiple of 4 (rank is a multiple of 256)
-    const int g2 = min(g + 2, G - 1);
-    __syncthreads();
-    DKV_K2_ISSUE_B(g + 1);
-    DKV_K2_ISSUE_A(g + 1, af1);
+    const int g2 = min(g + 2, G - 1), g3 = min(g + 3, G - 1);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(0, af0);
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
-    DKV_K2_FINISH(1);
     __syncthreads();
+    DKV_K2_FINISH(1);
     DKV_K2_ISSUE_B(g2);
     DKV_K2_ISSUE_A(g2, af0);
+    __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(1, af1);
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
     DKV_K2_FINISH(0);
+    DKV_K2_ISSUE_B(g3);
+    DKV_K2_ISSUE_A(g3, af1);
+    __syncthreads();
   }
+  if (hs == 0) __builtin_amdgcn_s_barrier();
 #undef DKV_K2_ISSUE_A
 #undef DKV_K2_ISSUE_B
 #undef DKV_K2_MFMA
