@@ -46,6 +46,10 @@ struct K2Args {
   float* tile_sum;
   float scaling;
   int batch, layer, Hkv, Hq, q_len, G, n_total, n_slots, ntiles, total_wg, per_xcd, query_dtype;
+  // rank split (decoding with few workgroups): each workgroup rebuilds its keys from g_per_split
+  // of the 64-component groups and writes partial scores [ksplit][R_total][ntiles * 256]
+  float* split_scores;
+  int ksplit, g_per_split;
 };
 
 DKV_DEVICE uint16_t f16_bits(float v) {
@@ -190,10 +194,11 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs 
 // ---------------------------------------------------------------------------
 constexpr int kSmallRows = 4;
 
-template <int D>
+template <int D, bool SPLIT>
 DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
                                            float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
-                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs) {
+                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs,
+                                           int split) {
   constexpr int HPW = 256 / D;
   constexpr int DB = D / 32;
   constexpr int HALF_BLK = DB / 2;
@@ -298,9 +303,16 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
         const int n = tq * 64 + tb * 32 + l32;
         x[tb] = n < count ? full * a.scaling : -INFINITY;
         xs[hw][r][tb] = x[tb];
+        if constexpr (SPLIT) {  // RoPE and the dot are linear in the key: partial scores add up
+          if (tb == lhi && n < count)
+            a.split_scores[((long)split * a.Hq * a.q_len + h * RH + r) * ((long)a.ntiles * kTileTok) +
+                           (long)tile * kTileTok + n] = x[tb];
+          continue;
+        }
         // fp32 scores are for question scoring (no probabilities then); decoding reads only the probabilities
         if (!a.probs && tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
+      if constexpr (SPLIT) continue;
       const float mx = max32(fmaxf(x[0], x[1]));
       float sm = 0.0f;
       if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
@@ -311,6 +323,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       }
     }
   }
+  if constexpr (SPLIT) return;  // the merge kernel writes statistics and probabilities
   __syncthreads();
   if (tid < HPW * kSmallRows) {
     const int hl = tid / kSmallRows, r = tid % kSmallRows;
@@ -359,7 +372,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 // [256][64] are fetched into registers one group ahead and stored into a
 // double-buffered, padded LDS tile; 32x32x16 fp16 MFMAs accumulate the keys.
 // ---------------------------------------------------------------------------
-template <int D, bool SMALL>
+template <int D, bool SMALL, bool SPLIT = false>
 __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   constexpr int HPW = 256 / D;      // heads per workgroup
   constexpr int DB = D / 32;        // 32-row blocks per head
@@ -375,7 +388,10 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int lin = (bid & 7) * a.per_xcd + (bid >> 3);
   if (lin >= a.total_wg) return;
   const int nhg = a.Hkv / HPW;
-  const int tile = lin / nhg, hg = lin % nhg;
+  // with a rank split, consecutive ids (one XCD) are the head groups of one (tile, split): they
+  // read the same coefficient groups
+  const int tile = SPLIT ? lin / (nhg * a.ksplit) : lin / nhg, hg = lin % nhg;
+  const int split = SPLIT ? (lin / nhg) % a.ksplit : 0;
   const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
   const int b = bt.x;
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
@@ -383,6 +399,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int count = min(kTileTok, sr.y - tok0);
   const int h0 = hg * HPW;
   const int G = a.G;
+  const int gb = SPLIT ? split * a.g_per_split : 0;  // this workgroup's groups: gb .. ge - 1
+  const int ge = SPLIT ? gb + a.g_per_split : G;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tq = wave & 3, hs = wave >> 2;
@@ -419,7 +437,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
-      const float4 m4 = *(const float4*)(mean_rows + j * 32 + 8 * v4);
+      // the key mean enters once: in the first rank slice only
+      const float4 m4 = split == 0 ? *(const float4*)(mean_rows + j * 32 + 8 * v4) : make_float4(0.f, 0.f, 0.f, 0.f);
       acc[0][j][4 * v4 + 0] = acc[1][j][4 * v4 + 0] = m4.x;
       acc[0][j][4 * v4 + 1] = acc[1][j][4 * v4 + 1] = m4.y;
       acc[0][j][4 * v4 + 2] = acc[1][j][4 * v4 + 2] = m4.z;
@@ -483,15 +502,15 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // wave of a SIMD runs MFMAs while the other does its memory work.
   // sched_barrier keeps the compiler from moving loads into the MFMA
   // segments; a wave in its MFMA segment runs at raised priority.
-  DKV_K2_ISSUE_A(0, af0);
-  DKV_K2_ISSUE_B(0);
+  DKV_K2_ISSUE_A(gb, af0);
+  DKV_K2_ISSUE_B(gb);
   DKV_K2_FINISH(0);
-  DKV_K2_ISSUE_B(1);
-  DKV_K2_ISSUE_A(1, af1);
+  DKV_K2_ISSUE_B(gb + 1);
+  DKV_K2_ISSUE_A(gb + 1, af1);
   __syncthreads();
   if (hs == 1) __builtin_amdgcn_s_barrier();
-  for (int g = 0; g < G; g += 2) {  // G is a multiple of 4 (rank is a multiple of 256)
-    const int g2 = min(g + 2, G - 1), g3 = min(g + 3, G - 1);
+  for (int g = gb; g < ge; g += 2) {  // ge - gb is even (the rank is a multiple of 256; a slice an even count)
+    const int g2 = min(g + 2, ge - 1), g3 = min(g + 3, ge - 1);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(0, af0);
@@ -524,7 +543,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int gq = a.Hq / a.Hkv;
   const int half_d = D / 2;
   if constexpr (SMALL) {
-    keys_scores_small_epilogue<D>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s);
+    keys_scores_small_epilogue<D, SPLIT>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s, split);
     return;
   } else {
 
@@ -797,6 +816,59 @@ DKV_DEVICE half8 codes_to_half8(uint32_t lo, uint32_t hi) {
   r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
   r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
   return r;
+}
+
+// ---------------------------------------------------------------------------
+// K2 merge (rank split only): one workgroup per (tile, output row) adds the
+// slices' partial scores of the tile's tokens in slice order, then writes the
+// tile's softmax statistics and the fp16 probabilities relative to the tile
+// maximum, as the unsplit decode epilogue does.
+// ---------------------------------------------------------------------------
+struct K2MergeArgs {
+  const int32_t* cu_seqlens;
+  const float* split_scores;  // [ksplit][R_total][ntiles * 256]
+  uint16_t* probs;
+  float* tile_max;
+  float* tile_sum;
+  int batch, n_total, ntiles, R_total, ksplit;
+};
+
+__global__ __launch_bounds__(kTileTok) void split_merge_kernel(K2MergeArgs a) {
+  __shared__ float red[2][kTileTok / 64];
+  const int tile = blockIdx.x / a.R_total, row = blockIdx.x % a.R_total;
+  const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, bt.x);
+  const int count = min(kTileTok, sr.y - (sr.x + bt.y * kTileTok));
+  const int n = threadIdx.x, lane = n & 63, wave = n >> 6;
+  const long slice = (long)a.R_total * a.ntiles * kTileTok;
+  const float* src = a.split_scores + ((long)row * a.ntiles + tile) * kTileTok + min(n, count - 1);
+  float x = 0.0f;
+  for (int s0 = 0; s0 < a.ksplit; s0 += 8) {  // the loads of 8 slices go out together
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, a.ksplit - 1) * slice];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x += s0 + k < a.ksplit ? v[k] : 0.0f;
+  }
+  if (n >= count) x = -INFINITY;
+  const float m = wave_max(x);
+  if (lane == 0) red[0][wave] = m;
+  __syncthreads();
+  float M = red[0][0];
+#pragma unroll
+  for (int w = 1; w < kTileTok / 64; ++w) M = fmaxf(M, red[0][w]);
+  const float pr = (x == -INFINITY) ? 0.0f : __expf(x - M);
+  const float sm = wave_sum(pr);
+  if (lane == 0) red[1][wave] = sm;
+  __syncthreads();
+  if (n == 0) {
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kTileTok / 64; ++w) S += red[1][w];
+    a.tile_max[(long)row * a.ntiles + tile] = M;
+    a.tile_sum[(long)row * a.ntiles + tile] = S;
+  }
+  a.probs[prob_index(row, (long)tile * kTileTok + n, a.R_total)] = f16_bits(pr);
 }
 
 // ---------------------------------------------------------------------------
@@ -1237,13 +1309,28 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(K3cArgs a) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
-  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, row_scale, row_base, total;
+  int ksplit;
+  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, row_scale, row_base, split_scores,
+      total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+constexpr int kCUs = 256;
+
+// K2 rank split for decodes with few workgroups: the largest power of two that keeps the
+// workgroups within one per CU and gives every slice an even number of 64-component groups.
+inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
+  if ((a->q_heads / a->kv_heads) * a->q_len > kSmallRows) return 1;
+  const int G = a->rank / 64;
+  const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
+  int k = 1;
+  while (wg * k * 2 <= kCUs && G % (4 * k) == 0) k *= 2;
+  return k;
+}
+
 // Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
-// [split partials][chunk partials][row scales][row bases].
+// [split partials][chunk partials][row scales][row bases][K2 rank-slice partial scores].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
@@ -1281,6 +1368,9 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)a->batch * L.R_total * 4);
   L.row_base = off;
   off += align256((size_t)a->batch * L.R_total * a->head_dim * 4);
+  L.ksplit = k2_split(a, L.ntiles);
+  L.split_scores = off;
+  if (L.ksplit > 1) off += align256((size_t)L.ksplit * L.R_total * L.ntiles * kTileTok * 4);
   L.total = off;
   return L;
 }
@@ -1343,6 +1433,33 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   // decoding (at most kSmallRows query rows per KV head) and question scoring are separate
   // instantiations, so neither epilogue's registers weigh on the other's main loop
   const bool small = (a->q_heads / a->kv_heads) * a->q_len <= kSmallRows;
+  if (probs && L.ksplit > 1) {  // decoding with few workgroups: rank slices, then the merge
+    k.ksplit = L.ksplit;
+    k.g_per_split = k.G / L.ksplit;
+    k.split_scores = (float*)(ws + L.split_scores);
+    k.total_wg *= L.ksplit;
+    k.per_xcd = (k.total_wg + 7) / 8;
+    const dim3 sgrid(8 * k.per_xcd);
+    if (a->head_dim == 128)
+      hipLaunchKernelGGL((keys_scores_kernel<128, true, true>), sgrid, dim3(kK2Threads), 0, st, k);
+    else
+      hipLaunchKernelGGL((keys_scores_kernel<64, true, true>), sgrid, dim3(kK2Threads), 0, st, k);
+    int rc = dkv::check_launch("keys_scores (rank slices)");
+    if (rc) return rc;
+    K2MergeArgs mg{};
+    mg.cu_seqlens = a->cu_seqlens;
+    mg.split_scores = k.split_scores;
+    mg.probs = k.probs;
+    mg.tile_max = k.tile_max;
+    mg.tile_sum = k.tile_sum;
+    mg.batch = a->batch;
+    mg.n_total = L.n_total;
+    mg.ntiles = L.ntiles;
+    mg.R_total = L.R_total;
+    mg.ksplit = L.ksplit;
+    hipLaunchKernelGGL(split_merge_kernel, dim3((unsigned)((long)L.ntiles * L.R_total)), dim3(kTileTok), 0, st, mg);
+    return dkv::check_launch("split_merge");
+  }
   if (a->head_dim == 128) {
     if (small)
       hipLaunchKernelGGL((keys_scores_kernel<128, true>), grid, dim3(kK2Threads), 0, st, k);
