@@ -9,10 +9,13 @@ spans the compressed tokens and a small exact cache (sinks, recent window,
 new tokens).
 
 What changes is where it runs: every step is a hand-written HIP kernel in
-libdimmerkv_hip.so (include/dimmerkv.h).  The coefficients are read straight
-from the packed bit-plane hot tier (hot_tier.PackedStream): the key codes are
-unpacked into LDS and multiplied on MFMA, so neither the FP16 key cache nor a
-coefficient matrix is materialised.
+libdimmerkv_hip.so (include/dimmerkv.h).  Once per decode step (and again
+after a refine) the packed hot tier (hot_tier.PackedStream) is decoded into a
+per-conversation workspace: the key coefficients as fp16 MFMA operands and the
+value codes as 8-bit codes with one affine pair per (token, group).  Every
+layer then rebuilds its keys from that operand buffer on MFMA, RoPE'd and
+scored in registers, so no layer's keys (the FP16 key cache) ever reach
+memory; the values are weighted in coefficient space.
 
 Both of the reference's entry points build a context: ``prog@`` through
 ``ProgressiveCache.context`` (packed bit planes), and ``dkvtc@`` through the
@@ -99,6 +102,9 @@ class CompressedContext:
         self.positions = positions.to(device=device, dtype=torch.int32).contiguous()
         if not self.positions.numel():  # no compressed token: still a non-null pointer for the C ABI
             self.positions = torch.zeros(1, dtype=torch.int32, device=device)[:0]
+        elif int(positions.min()) < 0 or int(positions.max()) >= tables.rope_cos.shape[0]:
+            raise ValueError(f"positions {int(positions.min())}..{int(positions.max())} fall outside the "
+                             f"{tables.rope_cos.shape[0]} rows of the RoPE tables")
         if cu_seqlens is None:
             cu_seqlens = torch.tensor([0, key.n], dtype=torch.int32)
         self.cu_host = cu_seqlens.to(torch.int32).cpu().contiguous()

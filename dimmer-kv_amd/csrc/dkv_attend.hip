@@ -4,20 +4,29 @@
 // attend) of SrikanthBalaaji/Dimmer-KV, applied to progressive codes
 // (scripts/progressive.py:47-55, 196-201):
 //
-//   K2  keys_scores  : per (256-token tile, head group) - unpack the key codes
-//                      of one 64-component group at a time into LDS as fp16,
-//                      multiply by the layer's key-basis slice on MFMA
-//                      (32x32x16 f16, fp32 accumulate), add the mean, apply
-//                      RoPE at the token positions, score against the GQA
-//                      query rows on MFMA, write fp32 scores and per-tile
-//                      (max, sum exp) statistics.  Keys never reach HBM.
-//   K3a value_weights: p~ = exp(s - M_c); per (token split, 4 groups) the
-//                      value codes are unpacked and p~ @ C_v accumulated on
-//                      MFMA -> partial coefficient-space outputs.
-//   K3b basis_apply  : sum the partials, multiply once by the value basis of
-//                      the KV head (per 128-component chunk).
-//   K3c finish       : merge with the exact tokens (sinks, recent, new) in the
-//                      same softmax, add sum(p) * mean_v, normalise, write.
+//   K1  decode_keys / decode_values (once per decode step, read by every
+//                      layer): the packed hot tier -> key coefficients as fp16
+//                      in the 32x32x16 MFMA operand order, and value codes as
+//                      8-bit codes blocked by 16 slots with one (scale,
+//                      offset) pair per (token, group).
+//   K2  keys_scores  : per (256-token tile, head group) - multiply the decoded
+//                      key coefficients (one 16-byte operand load per lane)
+//                      by the layer's key-basis slice (double-buffered in LDS)
+//                      on MFMA (32x32x16 f16, fp32 accumulate, starting at
+//                      the key mean), apply RoPE at the token positions and
+//                      score against the GQA query rows in registers, write
+//                      fp16 probabilities relative to the tile maximum and
+//                      per-tile (max, sum exp) statistics.  The rebuilt keys
+//                      never reach memory.
+//   K3a value_weights: per (1024-token split, 64-component group, 32 rows):
+//                      p @ value codes on MFMA plus sum(p * offset) ->
+//                      coefficient-space partial sums.
+//   K3b basis_apply  : sum the partials over the splits and multiply once by
+//                      the value basis of the KV head (per 128-component
+//                      chunk); beside them, one workgroup per output row
+//                      merges the tiles' softmax statistics with the exact
+//                      tokens (sinks, recent, new) in one softmax.
+//   K3c finish       : out = row scale * (sum of chunk partials) + row base.
 #include <math.h>
 
 #include "dkv_device.h"
@@ -46,6 +55,7 @@ struct K2Args {
   float* tile_sum;
   float scaling;
   int batch, layer, Hkv, Hq, q_len, G, n_total, n_slots, ntiles, total_wg, per_xcd, query_dtype;
+  int rope_rows;  // rows of the RoPE tables: positions are clamped to 0 .. rope_rows - 1
   // rank split (decoding with few workgroups): each workgroup rebuilds its keys from g_per_split
   // of the 64-component groups and writes partial scores [ksplit][R_total][ntiles * 256]
   float* split_scores;
@@ -409,7 +419,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   // the decode epilogue's positions and query rows are fetched now, behind the main loop
   if constexpr (SMALL) {
-    if (tid < kTileTok) pos_s[tid] = a.positions[tok0 + min(tid, count - 1)];
+    if (tid < kTileTok) pos_s[tid] = min(max(a.positions[tok0 + min(tid, count - 1)], 0), a.rope_rows - 1);
     const int gq = a.Hq / a.Hkv;
     for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
       const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
@@ -553,7 +563,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   for (int tb = 0; tb < 2; ++tb) {
     const int n = tq * 64 + tb * 32 + l32;
     const bool valid = n < count;
-    const int pos = valid ? a.positions[tok0 + n] : 0;
+    const int pos = valid ? min(max(a.positions[tok0 + n], 0), a.rope_rows - 1) : 0;
     const float* cosr = a.rope_cos + (long)pos * half_d;
     const float* sinr = a.rope_sin + (long)pos * half_d;
 #pragma unroll
@@ -930,7 +940,21 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   // the row maxima are known)
   const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
   const float mt = (row_ok && wt0 < count) ? a.tile_max[(long)my_row * a.ntiles + tile] : -INFINITY;
-  *(float4*)&saff[wave][2 * lane] = aff2;
+  // Power-of-two operand scaling.  scale = span / 256 of a low-variance group (about 6e-5 at
+  // rank 2048) puts p * scale among fp16's subnormals, which keep only a few significant bits.
+  // p <= 1, so scaling the wave's scales by the 2^e that brings their maximum into [2^14, 2^15)
+  // keeps every operand in fp16's normal range (or exactly 0); the fp32 sums are multiplied by
+  // 2^-e before they leave the wave, which is exact.
+  int sexp = 0;
+  const int ta = wt0 + 2 * lane;  // the split-relative tokens of this lane's two affine pairs
+  const float smax = wave_max(fmaxf(ta < count ? fabsf(aff2.x) : 0.0f, ta + 1 < count ? fabsf(aff2.z) : 0.0f));
+  if (smax > 0.0f) {
+    int ex;
+    (void)frexpf(smax, &ex);  // smax = m * 2^ex, 0.5 <= m < 1
+    sexp = min(max(15 - ex, -126), 126);
+  }
+  const float sup = ldexpf(1.0f, sexp), sdown = ldexpf(1.0f, -sexp);
+  *(float4*)&saff[wave][2 * lane] = make_float4(aff2.x * sup, aff2.y, aff2.z * sup, aff2.w);
   if (tid < 256) {
     const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
     const int r = rbk * 32 + (tid >> 3);
@@ -968,11 +992,11 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1[st].x, c1[st].y), acc[1], 0, 0, 0);
   }
   osum = sum_xor32(osum);
-  // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3)
+  // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3); 2^-sexp undoes the operand scaling
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v];
+    for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v] * sdown;
   if (lhi == 0) ored[wave][l32] = osum;
   __syncthreads();
   for (int e = tid; e < 32 * 64; e += kK3Waves * 64) {
@@ -1394,6 +1418,7 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
                   a->rope_sin && a->query,
               DKV_EINVAL, "%s: null pointer in arguments", what);
   DKV_REQUIRE(a->query_dtype >= DKV_F32 && a->query_dtype <= DKV_BF16, DKV_EINVAL, "%s: bad query dtype", what);
+  DKV_REQUIRE(a->rope_rows > 0, DKV_ESHAPE, "%s: rope_rows must be > 0 (got %d)", what, a->rope_rows);
   DKV_REQUIRE(a->cu_seqlens_host[0] == 0, DKV_ESHAPE, "%s: cu_seqlens[0] must be 0", what);
   for (int b = 0; b < a->batch; ++b)
     DKV_REQUIRE(a->cu_seqlens_host[b + 1] >= a->cu_seqlens_host[b], DKV_ESHAPE, "%s: cu_seqlens not monotone", what);
@@ -1411,6 +1436,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.mean_k = a->mean_k;
   k.rope_cos = a->rope_cos;
   k.rope_sin = a->rope_sin;
+  k.rope_rows = a->rope_rows;
   k.query = a->query;
   k.scores = (float*)(ws + L.scores);
   k.probs = probs ? (uint16_t*)(ws + L.probs) : nullptr;
@@ -1533,6 +1559,7 @@ static int check_values(const dkv_attend_args_t* a, int& E_total) {
   E_total = 0;
   if (a->cu_exact) {
     DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "dkv_attend_values: cu_exact needs cu_exact_host");
+    DKV_REQUIRE(a->cu_exact_host[0] == 0, DKV_ESHAPE, "dkv_attend_values: cu_exact[0] must be 0");
     for (int b = 0; b < a->batch; ++b) {
       const int e = a->cu_exact_host[b + 1] - a->cu_exact_host[b];
       DKV_REQUIRE(e >= 0 && e <= kMaxExact, DKV_ESHAPE, "dkv_attend_values: %d exact tokens (max %d)", e, kMaxExact);
@@ -1616,7 +1643,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   m.scaling = a->scaling;
   m.batch = a->batch;
   m.n_total = L.n_total;
-  m.e0_single = a->cu_exact ? a->cu_exact_host[0] : 0;
+  m.e0_single = 0;  // cu_exact[0] == 0 (check_values)
   m.e_single = a->cu_exact ? a->cu_exact_host[1] - a->cu_exact_host[0] : 0;
   m.layer = a->layer;
   m.Hkv = a->kv_heads;
@@ -1931,6 +1958,7 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   int E = 0;
   if (a->cu_exact) {
     DKV_REQUIRE(a->cu_exact_host && a->key_exact, DKV_EINVAL, "dkv_score_layer: exact keys need host offsets");
+    DKV_REQUIRE(a->cu_exact_host[0] == 0, DKV_ESHAPE, "dkv_score_layer: cu_exact[0] must be 0");
     E = a->cu_exact_host[1] - a->cu_exact_host[0];
   }
   const ScoreLayout S = make_score_layout(a);

@@ -165,20 +165,27 @@ class PackedStream:
         return int((self.tables.full_bytes - self.tables.prefix64[self.pieces.long()]).sum())
 
     def refine(self, rows: torch.Tensor) -> int:
-        """K4c: fetch the cold pieces of ``rows`` (stream-local, unique) -> bytes fetched (progressive.py:232).
+        """K4c: fetch the cold pieces of ``rows`` (stream-local) -> bytes fetched (progressive.py:232).
 
-        Rows already at full precision cost nothing (their cold blob is empty) and are merged like
-        the others, so no host-side filtering is needed; the fetched count is the only value read
-        back."""
+        The fetched count is taken over ``rows`` as given, a repeated row counting each time as in
+        the reference's formula; the gather itself runs over the distinct rows, because the kernel
+        repoints each row's blob and two blocks working on one row could pair one's old pieces with
+        the other's new offset.  Rows already at full precision cost nothing (their cold blob is
+        empty) and are merged like the others, so no host-side filtering is needed; the fetched
+        count is the only value read back."""
         rows = rows.to(device=self.blob.device, dtype=torch.int32).contiguous()
-        k = rows.numel()
-        if k == 0:
+        if rows.numel() == 0:
             return 0
         if self.cold is None:
             raise ValueError("this stream was packed without a cold tier")
+        lo, hi = int(rows.min()), int(rows.max())
+        if lo < 0 or hi >= self.n:
+            raise ValueError(f"refine rows must lie in 0..{self.n - 1} (got {lo}..{hi})")
+        fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
+        rows = torch.unique(rows)
+        k = rows.numel()
         if self.refined + k > self.refine_capacity:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
-        fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
         base = self.hot_used + self.refined * self.tables.full_bytes
         cold, cold_off = self.cold, self.cold_off
         if self.cold_on_host:

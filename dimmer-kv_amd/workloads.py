@@ -225,7 +225,8 @@ def build_decode(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", q_l
 
 
 def build_dkvtc(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", budget: float | None = None,
-                method: str | None = None, query_dtype: torch.dtype | None = None) -> DecodeWorkload:
+                method: str | None = None, query_dtype: torch.dtype | None = None,
+                query_scale: float = 1.0) -> DecodeWorkload:
     """The ``dkvtc@<budget>:snap:floor1`` decode workload at a config's shape, built through the
     reference entry points: a synthetic prefill cache (fp16), ``Methods.apply`` (KVTCCodec.compress
     with per-token rungs, synthetic snap importance, floor at the finest affordable uniform rung),
@@ -265,7 +266,7 @@ def build_dkvtc(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", budg
         ve.append(torch.cat(parts_v, dim=1))
     key_exact = torch.stack(ke).contiguous()
     value_exact = torch.stack(ve).contiguous()
-    queries = synth.make_queries(shape, 1, seed + 60, device, query_dtype)
+    queries = synth.make_queries(shape, 1, seed + 60, device, query_dtype, query_scale)
     outs = torch.empty(shape.layers, 1, 1, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
     streams = {"key": context.key, "value": context.value}
     w = DecodeWorkload(name + ":" + method, shape, context, context.tables, streams, queries, key_exact, value_exact,
@@ -279,9 +280,13 @@ def build_dkvtc(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", budg
 
 def build_ragged(count: int = 32, lo: int = 2048, hi: int = 16384, budget: float = 0.03, seed: int = 3033,
                  device="cuda", shape: synth.ModelShape = synth.SHAPE_3B,
-                 query_dtype: torch.dtype = torch.bfloat16) -> DecodeWorkload:
-    """Config 3: ``count`` conversations with lengths U[lo, hi], independent plane maps, one packed
-    buffer per stream and cu_seqlens offsets; one fused varlen decode step covers all of them."""
+                 query_dtype: torch.dtype = torch.bfloat16, query_scale: float = 1.0,
+                 keep_host_basis: bool = False) -> DecodeWorkload:
+    """``count`` conversations with lengths U[lo, hi] (32 ragged 3B conversations of 2K-16K tokens
+    at 3 % by default), independent plane maps, one packed buffer per stream and cu_seqlens
+    offsets; one fused varlen decode step covers all of them.  Conversation b's query is the
+    shared N(0, query_scale^2) draw times 0.5 + b / (count - 1).  ``keep_host_basis`` keeps
+    float32 host copies of the bases."""
     lengths = synth.ragged_lengths(count, lo, hi, seed)
     basis = {"key": synth.orthonormal_basis(shape.features, shape.rank, seed + 1, device),
              "value": synth.orthonormal_basis(shape.features, shape.rank, seed + 2, device)}
@@ -314,13 +319,14 @@ def build_ragged(count: int = 32, lo: int = 2048, hi: int = 16384, budget: float
     del coefs
     tables = ModelTables(basis["key"], basis["value"], mean["key"], mean["value"], shape.layers, shape.kv_heads,
                          shape.head_dim, cos, sin)
+    host_basis = {k: v.cpu().numpy() for k, v in basis.items()} if keep_host_basis else None
     basis.clear()
     cu_t = torch.tensor(cu, dtype=torch.int32)
     context = CompressedContext(tables, streams["key"], streams["value"], torch.cat(positions), shape.q_heads,
                                 cu_seqlens=cu_t)
     key_exact = torch.cat(exact_k, dim=2).contiguous()  # [L, Hkv, E_total, d]
     value_exact = torch.cat(exact_v, dim=2).contiguous()
-    queries = synth.make_queries(shape, 1, seed + 7, device, query_dtype).expand(-1, count, -1, -1, -1)
+    queries = synth.make_queries(shape, 1, seed + 7, device, query_dtype, query_scale).expand(-1, count, -1, -1, -1)
     queries = (queries * torch.linspace(0.5, 1.5, count, device=device).to(query_dtype)[None, :, None, None, None])
     queries = queries.contiguous()
     outs = torch.empty(shape.layers, count, 1, shape.q_heads, shape.head_dim, dtype=query_dtype, device=device)
@@ -330,4 +336,7 @@ def build_ragged(count: int = 32, lo: int = 2048, hi: int = 16384, budget: float
               for l in range(shape.layers)]
     w.workspace = context.workspace(w.args[0])
     w.lengths = lengths
+    w.budget = budget
+    if host_basis is not None:
+        w.synthetic_basis_host = host_basis
     return w

@@ -204,17 +204,18 @@ typedef struct dkv_attend_args {
   dkv_stream_t key, value;
   const int32_t* cu_seqlens;      /* [batch+1] */
   const int32_t* cu_seqlens_host; /* host [batch+1] */
-  const int32_t* positions;       /* [n_total] RoPE position of each compressed token */
+  const int32_t* positions;       /* [n_total] RoPE position of each compressed token, 0 .. rope_rows-1
+                                     (the kernels clamp a position outside that range into it) */
   const uint16_t* key_basis;      /* fp16, dkv_prepare_key_basis layout */
   const uint16_t* value_basis;    /* fp16, dkv_prepare_value_basis layout */
   const float* mean_k;            /* [L][Hkv*d] */
   const float* mean_v;            /* [L][Hkv*d] */
   const float* rope_cos;          /* [P][d/2] f32 (first half of HF emb) */
   const float* rope_sin;          /* [P][d/2] */
-  int32_t rope_rows;              /* P */
+  int32_t rope_rows;              /* P (> 0) */
   const void* query;              /* [batch][Hq][q_len][d], query_dtype */
   int32_t query_dtype;
-  const int32_t* cu_exact;        /* [batch+1] or NULL (no exact tokens) */
+  const int32_t* cu_exact;        /* [batch+1] with cu_exact[0] == 0, or NULL (no exact tokens) */
   const int32_t* cu_exact_host;   /* host mirror of cu_exact (<= 1024 exact tokens per sequence) */
   const float* key_exact;         /* [Hkv][E_total][d] f32, RoPE applied */
   const float* value_exact;       /* [Hkv][E_total][d] f32 */
@@ -271,7 +272,9 @@ int dkv_topk(const float* scores, int32_t n, int32_t k, int32_t* idx_out, void* 
              void* stream);
 
 /* ---- K4c: cold-plane gather (scripts/progressive.py:224-236 refine) ------
- * For the k selected tokens idx [k] (stream-local), merge each token's hot
+ * For the k selected tokens idx [k] (stream-local, distinct, each in 0..n-1:
+ * one workgroup per entry repoints that token, so a repeated token races),
+ * merge each token's hot
  * blob with its cold blob (cold + cold_tok_off[t]) into a full blob written
  * at refined + r*full_bytes (r = 0..k-1), then point the stream at it:
  * tok_off[t] = refined_base_off + r*full_bytes, pieces[t] = order.pieces.

@@ -112,19 +112,26 @@ def gpu_attend(case: Case, ctx, layer: int, out_dtype=torch.float32, device="cud
     return out.float().cpu().numpy()
 
 
-def assert_close(got: np.ndarray, ref: np.ndarray, atol=2e-3, rtol=1e-2, rel_fro=1e-2, what="", base=0.0):
-    """The north-star bar (|err| <= atol + rtol*|ref|) plus a relative Frobenius bound on the
-    part of the output that attention moves (ref - base, base = e.g. the value mean), which
-    catches structural mistakes the loose absolute bound would hide."""
+def assert_close(got: np.ndarray, ref: np.ndarray, atol=2e-3, rtol=1e-2, rel_fro=1e-2, what="", base=0.0,
+                 rel_max=2e-2):
+    """The north-star bar (|err| <= atol + rtol*|ref|) plus two bars on the part of the output
+    that attention moves (ref - base, base = e.g. the value mean): a relative Frobenius bound and
+    an elementwise one (|err| <= rel_max * max|ref - base|).  The synthetic caches' outputs are of
+    order 1e-2, where the north-star absolute term alone would pass almost anything; the two
+    relative bars catch the structural mistakes it hides."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert np.isfinite(ref).all(), f"{what}: the oracle's output is not finite"
     assert np.isfinite(got).all(), f"{what}: the GPU output is not finite"
     err = np.abs(got - ref)
     ok = err <= atol + rtol * np.abs(ref)
+    moved = np.abs(ref - base)
     fro = np.linalg.norm(got - ref) / max(np.linalg.norm(ref - base), 1e-30)
     assert ok.all(), f"{what}: max abs err {err.max():.3e} (ref max {np.abs(ref).max():.3e})"
     assert fro <= rel_fro, f"{what}: relative Frobenius error {fro:.3e} > {rel_fro}"
+    if rel_max is not None and moved.max() > 0:
+        assert err.max() <= rel_max * moved.max(), \
+            f"{what}: max abs err {err.max():.3e} > {rel_max} x max|ref - base| = {moved.max():.3e}"
     return float(err.max()), float(fro)
 
 
@@ -134,3 +141,55 @@ def value_mean_base(case: Case, layer: int) -> np.ndarray:
     m = case.mean_slice("value", layer).reshape(s.kv_heads, 1, s.head_dim)
     m = np.repeat(m, s.gqa, axis=1).reshape(s.q_heads, s.head_dim)
     return np.broadcast_to(m[None, None], (1, case.q_len, s.q_heads, s.head_dim))
+
+
+def workload_oracle(w, coef: dict, layer: int, b: int = 0, query_zero: bool = False) -> np.ndarray:
+    """The oracle's output [1, q_len, Hq, d] for conversation ``b`` of a workloads.DecodeWorkload
+    built with ``keep_host_basis`` (its float32 host bases), over ``coef`` (per stream float32
+    [n_total, r]: every compressed token's coefficients).  ``query_zero`` replaces the query by 0,
+    which makes the softmax uniform: the output a kernel whose scores carried no information would
+    produce."""
+    from oracle import attention_ref
+
+    s = w.shape
+    cu = w.context.cu_host.numpy()
+    t0, t1 = int(cu[b]), int(cu[b + 1])
+    e_off = np.concatenate([[0], np.cumsum(w.exact_lengths)])
+    e0, e1 = int(e_off[b]), int(e_off[b + 1])
+    positions = w.context.positions[t0:t1].long().cpu()
+    cos = w.tables.rope_cos.cpu()[positions].numpy()
+    sin = w.tables.rope_sin.cpu()[positions].numpy()
+    cos, sin = np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
+    wd = s.kv_heads * s.head_dim
+    bk = w.synthetic_basis_host["key"][layer * wd:(layer + 1) * wd].T
+    bv = w.synthetic_basis_host["value"][layer * wd:(layer + 1) * wd].T
+    mk = w.tables.mean_k[layer].cpu().numpy()
+    mv = w.tables.mean_v[layer].cpu().numpy()
+    q = w.queries[layer][b:b + 1].float().cpu().numpy()
+    if query_zero:
+        q = np.zeros_like(q)
+    return attention_ref.attend(q, coef["key"][t0:t1], coef["value"][t0:t1], bk, bv, mk, mv, cos, sin,
+                                w.key_exact[layer][None, :, e0:e1].cpu().numpy(),
+                                w.value_exact[layer][None, :, e0:e1].cpu().numpy())
+
+
+def mean_base(shape, mean_v_layer: np.ndarray, out_shape) -> np.ndarray:
+    """mean_v of a layer broadcast to an attend output of shape [B, q_len, Hq, d]."""
+    m = np.repeat(np.asarray(mean_v_layer).reshape(shape.kv_heads, 1, -1), shape.gqa, axis=1)
+    return np.broadcast_to(m.reshape(1, 1, shape.q_heads, -1), out_shape)
+
+
+def assert_sensitive(ref: np.ndarray, uniform: np.ndarray, base, what="", rel_fro=1e-2, rel_max=2e-2,
+                     factor=20.0) -> float:
+    """The check is only as strong as the gap between the true output and the output of attention
+    whose scores carry nothing (uniform weights): that gap must exceed ``assert_close``'s relative
+    Frobenius bar ``factor`` times over, and its largest element must exceed the elementwise bar on
+    the moved part (``rel_max`` x max|ref - base|) ``factor`` times over."""
+    ref = np.asarray(ref, dtype=np.float64)
+    diff = np.asarray(uniform, np.float64) - ref
+    gap = np.linalg.norm(diff) / max(np.linalg.norm(ref - base), 1e-30)
+    assert gap > factor * rel_fro, f"{what}: uniform attention is only {gap:.3e} away (bar {rel_fro})"
+    moved = np.abs(ref - base).max()
+    assert np.abs(diff).max() > factor * rel_max * moved, \
+        f"{what}: uniform attention's largest difference {np.abs(diff).max():.3e} is within {factor} x the bar"
+    return float(gap)

@@ -2,7 +2,15 @@
 the question stage and a whole 28-layer decode step over the packed cache, checked against
 the oracle on layers spread over the model, plus size-independent properties (byte
 accounting within the budget, refined tokens decoding at full precision, the decode being
-deterministic step to step)."""
+deterministic step to step).
+
+The decode queries are peaked (N(0, 100^2) entries, score spread of order 1 over 16K
+tokens): with the unit-variance queries of the benchmark the attention is nearly uniform
+and its output nearly the value mean, so the check would barely depend on the scores.  Each
+checked layer first shows that uniform attention (the oracle with a zero query) misses the
+bar by a wide margin.  These are the cases that run the unsplit decode instantiations of
+K2: ``keys_scores_kernel<128, true>`` here, ``<64, true>`` in the 33K-token 1B case (at
+least 129 token tiles, so no rank split)."""
 
 from __future__ import annotations
 
@@ -12,16 +20,36 @@ import torch
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+PEAKED = 100.0
+
+
+def _check_layer(w, coef, layer, what, base):
+    """bf16 output of the workload's own step (elementwise bar) and an fp32 run of the same layer
+    (elementwise and relative Frobenius bars), after the sensitivity check."""
+    from helpers import assert_close, assert_sensitive, workload_oracle
+
+    s = w.shape
+    ref = workload_oracle(w, coef, layer)
+    gap = assert_sensitive(ref, workload_oracle(w, coef, layer, query_zero=True), base, what=what)
+    # the decode writes bf16 (the model's dtype): elementwise bar on that output
+    assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"{what} (bf16 out)", rel_fro=1e9)
+    out32 = torch.empty(1, 1, s.q_heads, s.head_dim, dtype=torch.float32, device=DEV)
+    args = w.context.layer_args(layer, w.queries[layer], out32, w.key_exact[layer], w.value_exact[layer])
+    w.context.run_layer(args)
+    torch.cuda.synchronize()
+    err, fro = assert_close(out32.cpu().numpy(), ref, what=what, base=base)
+    print(f"  {what}: max abs err {err:.2e}, rel fro {fro:.2e} (uniform attention {gap:.2e} away)", flush=True)
 
 
 def test_3b_16k_question_then_decode_matches_oracle():
     import workloads
-    from helpers import assert_close
-    from oracle import attention_ref, scoring_ref
+    from helpers import mean_base
     from oracle import progressive_ref as pr
+    from oracle import scoring_ref
 
-    print("[case] full size 3b-16k-3pct: question stage + decode step", flush=True)
-    w = workloads.build_decode("3b-16k-3pct", device=DEV, keep_host_basis=True, refine_fraction=0.01)
+    print("[case] full size 3b-16k-3pct: question stage + decode step (peaked queries)", flush=True)
+    w = workloads.build_decode("3b-16k-3pct", device=DEV, keep_host_basis=True, refine_fraction=0.01,
+                               query_scale=PEAKED)
     s = w.shape
     # byte accounting of the packed hot tier (progressive.py:185-188) fits the 3 % budget
     hot = w.context.key.hot_bytes() + w.context.value.hot_bytes()
@@ -52,30 +80,9 @@ def test_3b_16k_question_then_decode_matches_oracle():
     torch.cuda.synchronize()
     assert torch.equal(first, w.outs)
     coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
-    positions = w.context.positions.long().cpu()
-    cos = w.tables.rope_cos.cpu()[positions].numpy()
-    sin = w.tables.rope_sin.cpu()[positions].numpy()
-    cos, sin = np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
-    wd = s.kv_heads * s.head_dim
     for layer in (0, 13, 27):
-        bk = w.synthetic_basis_host["key"][layer * wd:(layer + 1) * wd].T
-        bv = w.synthetic_basis_host["value"][layer * wd:(layer + 1) * wd].T
-        mk = w.tables.mean_k[layer].cpu().numpy()
-        mv = w.tables.mean_v[layer].cpu().numpy()
-        ref = attention_ref.attend(w.queries[layer].float().cpu().numpy(), coef["key"], coef["value"], bk, bv, mk, mv,
-                                   cos, sin, w.key_exact[layer][None].cpu().numpy(),
-                                   w.value_exact[layer][None].cpu().numpy())
-        base = np.broadcast_to(np.repeat(mv.reshape(s.kv_heads, 1, -1), s.gqa, axis=1).reshape(1, 1, s.q_heads, -1),
-                               ref.shape)
-        # the benchmark's decode writes bf16 (the model's dtype): elementwise bar on that output;
-        # the same layer with an fp32 output must also meet the relative Frobenius bar
-        assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"3b-16k layer {layer} (bf16 out)", rel_fro=1e9)
-        out32 = torch.empty(1, 1, s.q_heads, s.head_dim, dtype=torch.float32, device=DEV)
-        args = w.context.layer_args(layer, w.queries[layer], out32, w.key_exact[layer], w.value_exact[layer])
-        w.context.run_layer(args)
-        torch.cuda.synchronize()
-        err, fro = assert_close(out32.cpu().numpy(), ref, what=f"3b-16k layer {layer}", base=base)
-        print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+        base = mean_base(s, w.tables.mean_v[layer].cpu().numpy(), (1, 1, s.q_heads, s.head_dim))
+        _check_layer(w, coef, layer, f"3b-16k layer {layer}", base)
 
 
 def test_3b_16k_dkvtc_decode_matches_oracle():
@@ -84,11 +91,11 @@ def test_3b_16k_dkvtc_decode_matches_oracle():
     deterministic, and equal to the oracle's attention over codec.last_coefficients on layers
     spread over the model."""
     import workloads
-    from helpers import assert_close
+    from helpers import assert_close, assert_sensitive, mean_base
     from oracle import attention_ref
 
-    print("[case] full size 3b-16k-3pct: dkvtc decode step", flush=True)
-    w = workloads.build_dkvtc("3b-16k-3pct", device=DEV)
+    print("[case] full size 3b-16k-3pct: dkvtc decode step (peaked queries)", flush=True)
+    w = workloads.build_dkvtc("3b-16k-3pct", device=DEV, query_scale=PEAKED)
     s, codec, ctx = w.shape, w.codec, w.context
     start, _ = codec.last_span
     choice_k = codec.last_choice["key"].cpu().numpy()
@@ -111,16 +118,44 @@ def test_3b_16k_dkvtc_decode_matches_oracle():
     for layer in (0, 13, 27):
         basis = {k: codec.streams[k].basis[layer * wd:(layer + 1) * wd].T.cpu().numpy() for k in ("key", "value")}
         mean = {k: codec.streams[k].mean[layer * wd:(layer + 1) * wd].cpu().numpy() for k in ("key", "value")}
-        ref = attention_ref.attend(w.queries[layer].float().cpu().numpy(), coef["key"], coef["value"], basis["key"],
-                                   basis["value"], mean["key"], mean["value"], cos, sin,
-                                   w.key_exact[layer][None, :, n_extra:].cpu().numpy(),
-                                   w.value_exact[layer][None, :, n_extra:].cpu().numpy())
-        base = np.broadcast_to(np.repeat(mean["value"].reshape(s.kv_heads, 1, -1), s.gqa, axis=1)
-                               .reshape(1, 1, s.q_heads, -1), ref.shape)
+        q = w.queries[layer].float().cpu().numpy()
+        exact = (w.key_exact[layer][None, :, n_extra:].cpu().numpy(), w.value_exact[layer][None, :, n_extra:].cpu().numpy())
+
+        def oracle(query):
+            return attention_ref.attend(query, coef["key"], coef["value"], basis["key"], basis["value"], mean["key"],
+                                        mean["value"], cos, sin, *exact)
+
+        ref = oracle(q)
+        base = mean_base(s, mean["value"], ref.shape)
+        gap = assert_sensitive(ref, oracle(np.zeros_like(q)), base, what=f"dkvtc layer {layer}")
         assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"dkvtc layer {layer} (bf16 out)", rel_fro=1e9)
         out32 = torch.empty(1, 1, s.q_heads, s.head_dim, dtype=torch.float32, device=DEV)
         args = ctx.layer_args(layer, w.queries[layer], out32, w.key_exact[layer], w.value_exact[layer])
         ctx.run_layer(args)
         torch.cuda.synchronize()
         err, fro = assert_close(out32.cpu().numpy(), ref, what=f"dkvtc layer {layer}", base=base)
-        print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+        print(f"  dkvtc layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e} (uniform attention {gap:.2e} away)",
+              flush=True)
+
+
+def test_1b_33k_unsplit_head_dim_64_matches_oracle():
+    """Llama-3.2-1B shape (head_dim 64), two layers, 33,004 tokens: 129 token tiles x 2 head groups
+    = 258 K2 workgroups, more than one per CU, so the decode runs the unsplit
+    ``keys_scores_kernel<64, true>`` (the rank split only starts at <= 128 workgroups)."""
+    import synth
+    import workloads
+    from helpers import mean_base
+
+    shape = synth.ModelShape(2, 8, 64, 32, 1024)
+    tokens = 33_004
+    print(f"[case] 1B shape, 2 layers, {tokens} tokens: unsplit K2 at head_dim 64 (peaked queries)", flush=True)
+    w = workloads.build_decode("1b-33k", shape=shape, tokens=tokens, device=DEV, keep_host_basis=True,
+                               query_dtype=torch.bfloat16, query_scale=PEAKED)
+    tiles = -(-w.middle // 256)
+    assert tiles * (shape.kv_heads // (256 // shape.head_dim)) > 256
+    w.step()
+    torch.cuda.synchronize()
+    coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
+    for layer in range(shape.layers):
+        base = mean_base(shape, w.tables.mean_v[layer].cpu().numpy(), (1, 1, shape.q_heads, shape.head_dim))
+        _check_layer(w, coef, layer, f"1b-33k layer {layer}", base)
