@@ -29,6 +29,8 @@
 //   K3c finish       : out = row scale * (sum of chunk partials) + row base.
 #include <math.h>
 
+#include <mutex>
+
 #include "dkv_device.h"
 #include "dkv_host.h"
 
@@ -2017,4 +2019,70 @@ extern "C" int dkv_topk(const float* scores, int32_t n, int32_t k, int32_t* idx_
   if (k == 0) return DKV_OK;
   hipLaunchKernelGGL(topk_kernel, dim3(1), dim3(kTopkThreads), 0, dkv::as_stream(stream), scores, n, k, idx_out);
   return dkv::check_launch("dkv_topk");
+}
+
+// ===========================================================================
+// Allocation-free variant of dkv_attend_prepare + dkv_attend_layer, for
+// callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid it).  The workspace is the
+// file-scope device array below, `kStaticScratchBytes` per GPU, held by every
+// GPU the library runs on until the process ends.  Every call on one GPU
+// shares that GPU's array: each call decodes the codes again and rewrites
+// every area it then reads (no area needs to start at zero: the decode writes
+// every slot, K2 every tile statistic and probability the later kernels
+// read, and K3a/K3b every partial), so calls in sequence are independent,
+// but calls that overlap on one GPU (different streams or threads) race.
+// ===========================================================================
+namespace {
+
+constexpr size_t kStaticScratchBytes = DKV_NOALLOC_MAX_BYTES;  // 64 MiB
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each GPU (null until looked up)
+
+// The current device's address of `scratch`, looked up once per device with that device
+// current (in host code the array's name is not a device address).
+int scratch_address(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  DKV_REQUIRE(e == hipSuccess, DKV_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  DKV_REQUIRE(dev >= 0 && dev < kMaxDevices, DKV_EINVAL, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    DKV_REQUIRE(e == hipSuccess && p, DKV_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", what,
+                hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DKV_OK;
+}
+
+}  // namespace
+
+extern "C" int dkv_attend_layer_noalloc(const dkv_attend_args_t* a, void* stream) {
+  int rc = check_attend(a, "dkv_attend_layer_noalloc");
+  if (rc) return rc;
+  int E_total = 0;
+  rc = check_values(a, E_total);
+  if (rc) return rc;
+  const Layout L = make_layout(a);
+  DKV_REQUIRE(L.total <= kStaticScratchBytes, DKV_EWORKSPACE,
+              "dkv_attend_layer_noalloc: this context needs %zu B of scratch; the static maximum is %zu B "
+              "(use dkv_attend_prepare + dkv_attend_layer with a caller workspace)",
+              L.total, kStaticScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_address(&ws, "dkv_attend_layer_noalloc");
+  if (rc) return rc;
+  rc = dkv_attend_prepare(a, 8, ws, kStaticScratchBytes, stream);
+  if (rc) return rc;
+  return dkv_attend_layer(a, ws, kStaticScratchBytes, stream);
 }

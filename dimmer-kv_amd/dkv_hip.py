@@ -28,8 +28,9 @@ EXPORTS = [
     "dkv_attend_layer",
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
-    "dkv_gather_cold", "dkv_wire_pack", "dkv_wire_unpack",
+    "dkv_gather_cold", "dkv_wire_pack", "dkv_wire_unpack", "dkv_attend_layer_noalloc",
 ]
+NOALLOC_MAX_BYTES = 64 << 20  # DKV_NOALLOC_MAX_BYTES: the static workspace of dkv_attend_layer_noalloc
 
 c_i32, c_i64, c_f32, c_vp, c_sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
 
@@ -205,6 +206,13 @@ def attend_prepare(args: AttendArgs, workspace: torch.Tensor, plane_cap: int = 8
 def attend_layer(args: AttendArgs, workspace: torch.Tensor) -> None:
     _check(lib().dkv_attend_layer(ctypes.byref(args), c_vp(ptr(workspace)), c_sz(workspace.numel()),
                                   c_vp(stream_handle())), "dkv_attend_layer")
+
+
+def attend_layer_noalloc(args: AttendArgs) -> None:
+    """K1 decode + one layer with the library's static workspace (no allocation anywhere, for
+    callers that cannot allocate).  Contexts whose workspace exceeds NOALLOC_MAX_BYTES are refused;
+    calls that overlap on one GPU share that workspace and race."""
+    _check(lib().dkv_attend_layer_noalloc(ctypes.byref(args), c_vp(stream_handle())), "dkv_attend_layer_noalloc")
 
 
 def attend_scores(args: AttendArgs, workspace: torch.Tensor) -> None:

@@ -271,6 +271,20 @@ size_t dkv_topk_workspace_bytes(int32_t n);
 int dkv_topk(const float* scores, int32_t n, int32_t k, int32_t* idx_out, void* workspace, size_t workspace_bytes,
              void* stream);
 
+/* ---- allocation-free decode of one layer ---------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation).  Does what dkv_attend_prepare(a, 8, ...) followed by
+ * dkv_attend_layer(a, ...) do, with the workspace in a file-scope device array
+ * of DKV_NOALLOC_MAX_BYTES that every GPU the library runs on holds until the
+ * process ends; calls nothing that allocates.  A context whose workspace
+ * (dkv_attend_workspace_bytes) exceeds the maximum is rejected with
+ * DKV_EWORKSPACE before anything is launched.  Every call decodes the codes
+ * again (the array keeps only the last call's contents); calls in sequence are
+ * independent, calls that overlap on one GPU race. */
+#define DKV_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int dkv_attend_layer_noalloc(const dkv_attend_args_t* a, void* stream);
+
 /* ---- K4c: cold-plane gather (scripts/progressive.py:224-236 refine) ------
  * For the k selected tokens idx [k] (stream-local, distinct, each in 0..n-1:
  * one workgroup per entry repoints that token, so a repeated token races),

@@ -63,3 +63,25 @@ def test_cpu_tensors_are_refused():
 
     with pytest.raises(ValueError, match="GPU"):
         dkv_hip.ptr(torch.zeros(3))
+
+
+def test_noalloc_refuses_contexts_beyond_its_static_workspace():
+    """A 3B-shaped context of 100,000 compressed tokens needs far more than the static workspace:
+    refused by the host-side checks, before any device work."""
+    lib = dkv_hip.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check comes first
+    order = dkv_hip.Order(32, 256, fake, fake, fake, fake)
+    stream = dkv_hip.Stream(fake, fake, fake, order, dkv_hip.DKV_FMT_PLANES, dkv_hip.Ladder())
+    cu_host = (ctypes.c_int32 * 2)(0, 100_000)
+    a = dkv_hip.AttendArgs()
+    a.batch, a.q_len, a.layers, a.layer, a.kv_heads, a.head_dim, a.q_heads, a.rank = 1, 1, 28, 0, 8, 128, 24, 2048
+    a.scaling = 128 ** -0.5
+    a.key, a.value = stream, stream
+    a.cu_seqlens = a.positions = a.key_basis = a.value_basis = a.mean_k = a.mean_v = 256
+    a.rope_cos = a.rope_sin = a.query = a.out = 256
+    a.rope_rows = 100_001
+    a.cu_seqlens_host = ctypes.cast(cu_host, ctypes.c_void_p).value
+    assert lib.dkv_attend_workspace_bytes(ctypes.byref(a)) > dkv_hip.NOALLOC_MAX_BYTES
+    rc = lib.dkv_attend_layer_noalloc(ctypes.byref(a), None)
+    assert rc == -3  # DKV_EWORKSPACE
+    assert b"static maximum" in lib.dkv_last_error()
