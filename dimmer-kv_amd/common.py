@@ -1,55 +1,28 @@
-"""Shared helpers (mirror of scripts/common.py, the parts the answer path uses).
+"""Cache helpers the answer path shares (the part of scripts/common.py it uses).
 
-``choose_device`` and ``build_cache`` follow scripts/common.py:26-31, 70-76.
-Model loading (``load_model``, :34-47) and WikiText chunks (:79-107) need a
-network download and are not part of this build; ``load_model`` raises.
+``build_cache`` keeps the reference's one-line construction (scripts/common.py:70-76): the exact
+tail that HF's attention layers update is an ordinary ``DynamicCache``.  Model loading and the
+WikiText reader of that file need downloads and are not part of this build.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-
 import torch
-
-DEFAULT_MODEL = "meta-llama/Llama-3.2-1B-Instruct"
-
-
-@dataclass(frozen=True)
-class KVConfig:
-    """Cache geometry derived from the model configuration (scripts/common.py:13-23)."""
-
-    layers: int
-    kv_heads: int
-    head_dim: int
-
-    def fp16_bytes_per_token(self) -> int:
-        return self.layers * self.kv_heads * self.head_dim * 2 * 2
 
 
 def choose_device() -> torch.device:
-    """The HIP kernels need a GPU; there is no CPU path for the compressed cache."""
-    if torch.cuda.is_available():
-        return torch.device("cuda")
-    raise RuntimeError("dimmer-kv's compressed-cache path runs on an AMD GPU (no GPU visible)")
+    """The compressed cache lives on an AMD GPU; with none visible there is nothing to run on."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("dimmer-kv's compressed-cache path runs on an AMD GPU (no GPU visible)")
+    return torch.device("cuda")
 
 
-def load_model(model_id: str = DEFAULT_MODEL):
-    raise RuntimeError(f"loading {model_id} needs a model download, which this build does not perform")
-
-
-def kv_config(model) -> KVConfig:
-    config = model.config
-    head_dim = getattr(config, "head_dim", None) or (config.hidden_size // config.num_attention_heads)
-    return KVConfig(layers=config.num_hidden_layers,
-                    kv_heads=getattr(config, "num_key_value_heads", config.num_attention_heads), head_dim=head_dim)
-
-
-def cache_tensors(cache):
-    """Per-layer keys and values [batch, kv_heads, tokens, head_dim] of a DynamicCache (:62-67)."""
-    layers = getattr(cache, "layers", None)
-    if not layers:
-        raise RuntimeError("The model did not return a DynamicCache with .layers.")
-    return [layer.keys for layer in layers], [layer.values for layer in layers]
+def cache_tensors(cache) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
+    """(keys, values): the per-layer [batch, kv_heads, tokens, head_dim] tensors a DynamicCache holds."""
+    per_layer = list(getattr(cache, "layers", None) or [])
+    if not per_layer:
+        raise RuntimeError("expected a DynamicCache with per-layer entries (cache.layers)")
+    return [entry.keys for entry in per_layer], [entry.values for entry in per_layer]
 
 
 def build_cache(keys: list[torch.Tensor], values: list[torch.Tensor], model):

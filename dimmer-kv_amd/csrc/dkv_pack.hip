@@ -464,6 +464,70 @@ extern "C" int dkv_dequantize_codes(const uint8_t* codes, const uint16_t* low, c
 }
 
 // ---------------------------------------------------------------------------
+// Encoder: quantize8 (progressive.py:37-44) and the per-group squared error at
+// 0..8 planes (progressive.py:152-158) in one pass over the coefficients.  One
+// wave per (token, group), one lane per member: the group's min and max are
+// wave reductions; low = f16(min), span = f16(max(max - low, 1e-8)),
+// code = clamp(floor((x - low) / span * 256), 0, 255) with the division
+// correctly rounded (a NaN from a zero fp16 span gives code 0); then every
+// lane's squared error against the reference's dequantize at each plane count,
+// summed over the wave.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize8_kernel(const float* __restrict__ coef, long ngroups,
+                                                        uint8_t* __restrict__ codes, uint16_t* __restrict__ low,
+                                                        uint16_t* __restrict__ span, float* __restrict__ errors) {
+  const long tg = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (tg >= ngroups) return;
+  const float x = coef[tg * 64 + lane];
+  const float amin = -wave_max(-x), amax = wave_max(x);
+  const half_t lo_h = (half_t)amin;
+  const float lo = (float)lo_h;
+  const half_t sp_h = (half_t)fmaxf(amax - lo, 1e-8f);
+  const float sp = (float)sp_h;
+  float q;
+  {
+#pragma clang fp contract(off)
+    q = floorf(((x - lo) / sp) * 256.0f);
+  }
+  q = (q != q) ? 0.0f : fminf(fmaxf(q, 0.0f), 255.0f);
+  const uint32_t code = (uint32_t)q;
+  codes[tg * 64 + lane] = (uint8_t)code;
+  if (lane == 0) {
+    uint16_t lb, sb;
+    __builtin_memcpy(&lb, &lo_h, 2);
+    __builtin_memcpy(&sb, &sp_h, 2);
+    low[tg] = lb;
+    span[tg] = sb;
+  }
+  if (!errors) return;
+  float mine = 0.0f;  // this lane ends up holding the error at (lane) planes, lane < 9
+#pragma unroll
+  for (int m = 0; m <= 8; ++m) {
+    float d;
+    {
+#pragma clang fp contract(off)
+      d = x - dequant_exact(code, m, lo, sp, __builtin_ldexpf(1.0f, -m));
+      d = d * d;
+    }
+    const float e = wave_sum(d);
+    mine = lane == m ? e : mine;
+  }
+  if (lane <= 8) errors[tg * 9 + lane] = mine;
+}
+
+extern "C" int dkv_quantize8(const float* coef, int32_t n, int32_t groups, uint8_t* codes, uint16_t* low,
+                             uint16_t* span, float* errors, void* stream) {
+  DKV_REQUIRE(coef && codes && low && span, DKV_EINVAL, "dkv_quantize8: null pointer");
+  DKV_REQUIRE(n >= 0 && groups > 0, DKV_ESHAPE, "dkv_quantize8: bad shape (n=%d groups=%d)", n, groups);
+  if (n == 0) return DKV_OK;
+  const long ngroups = (long)n * groups;
+  hipLaunchKernelGGL(quantize8_kernel, dim3((unsigned)((ngroups + 3) / 4)), dim3(256), 0, dkv::as_stream(stream),
+                     coef, ngroups, codes, low, span, errors);
+  return dkv::check_launch("dkv_quantize8");
+}
+
+// ---------------------------------------------------------------------------
 // K4c: merge hot + cold segments of selected tokens into full blobs.
 // One workgroup per selected token; one thread per group.
 // ---------------------------------------------------------------------------

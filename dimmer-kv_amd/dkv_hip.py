@@ -29,6 +29,7 @@ EXPORTS = [
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
     "dkv_gather_cold", "dkv_wire_pack", "dkv_wire_unpack", "dkv_attend_layer_noalloc",
+    "dkv_quantize8",
 ]
 NOALLOC_MAX_BYTES = 64 << 20  # DKV_NOALLOC_MAX_BYTES: the static workspace of dkv_attend_layer_noalloc
 
@@ -170,6 +171,13 @@ def wire_unpack(data, rung, ladder: Ladder, wire: Wire, codes, low, scale) -> No
 def unpack_dequant(stream: Stream, t0: int, nt: int, out: torch.Tensor) -> None:
     _check(lib().dkv_unpack_dequant(ctypes.byref(stream), c_i32(t0), c_i32(nt), c_vp(ptr(out)),
                                     c_i32(dtype_code(out.dtype)), c_vp(stream_handle())), "dkv_unpack_dequant")
+
+
+def quantize8(coef, codes, low, span, errors=None) -> None:
+    """coef f32 [n, 64G] -> codes u8 [n, G, 64], low/span f16 bits [n, G], errors f32 [n, G, 9] or None."""
+    n, groups = codes.shape[0], codes.shape[1]
+    _check(lib().dkv_quantize8(c_vp(ptr(coef)), c_i32(n), c_i32(groups), c_vp(ptr(codes)), c_vp(ptr(low)),
+                               c_vp(ptr(span)), c_vp(ptr(errors)), c_vp(stream_handle())), "dkv_quantize8")
 
 
 def dequantize_codes(codes, low, span, planes, out) -> None:

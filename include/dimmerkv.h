@@ -168,6 +168,14 @@ int dkv_wire_unpack(const uint8_t* in, const int16_t* rung, int32_t n, dkv_ladde
 int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt, void* out, int32_t out_dtype,
                        void* stream);
 
+/* Encoder (replaces scripts/progressive.py:37-44 quantize8 and the error table
+ * of :152-158): coefficients f32 [n][64G] -> codes u8 [n][G][64], low/span f16
+ * [n][G] (bit-identical to the reference's fp32 arithmetic) and, unless
+ * `errors` is NULL, errors f32 [n][G][9]: each group's squared error at 0..8
+ * planes (fp32 sums over the 64 members, in this kernel's order). */
+int dkv_quantize8(const float* coef, int32_t n, int32_t groups, uint8_t* codes, uint16_t* low, uint16_t* span,
+                  float* errors, void* stream);
+
 /* Reference dequantize on unpacked codes (scripts/progressive.py:47-55):
  * codes u8 [n][G][64], low/span f16 [n][G], planes u8 [n or 1][G] -> f32 [n][64G]. */
 int dkv_dequantize_codes(const uint8_t* codes, const uint16_t* low, const uint16_t* span, const uint8_t* planes,

@@ -136,3 +136,24 @@ def error_table(coefficients: np.ndarray, codes, low, span, group: int = 64) -> 
         rebuilt = dequantize(codes, low, span, np.full((1, groups), m)).reshape(grouped.shape)
         out[..., m] = np.square(grouped - rebuilt).sum(axis=-1, dtype=np.float32)
     return out
+
+
+def rung_errors(coefficients: np.ndarray, table: np.ndarray, order: Order, weights: np.ndarray | None = None):
+    """progressive.py:149-164: each token's error at every rung of ``order`` = the table's entries at
+    the rung's plane counts summed over the groups, over the stream's mean token energy (float32,
+    floored at 1e-12), times weights / mean(weights) when weights are given -> [tokens, rungs]."""
+    x = np.asarray(coefficients, dtype=np.float32)
+    energy = max(np.float32(np.square(x).sum(axis=1, dtype=np.float32).mean(dtype=np.float32)), np.float32(1e-12))
+    rung_planes = order.planes[np.asarray(order.rungs)].astype(np.int64)  # [rungs, groups]
+    groups = table.shape[1]
+    picked = table[:, np.arange(groups)[None, :], rung_planes]  # [tokens, rungs, groups]
+    out = (picked.sum(axis=2, dtype=np.float32) / energy).astype(np.float32)
+    if weights is not None:
+        w = np.asarray(weights, dtype=np.float32)
+        out = (out * (w / max(np.float32(w.mean(dtype=np.float32)), np.float32(1e-12)))[:, None]).astype(np.float32)
+    return out
+
+
+def level_bytes(order: Order) -> list[int]:
+    """progressive.py:166: bytes of each rung of ``order`` including the rung id."""
+    return [int(order.prefix_bytes[k]) + RUNG_ID_BYTES for k in order.rungs]

@@ -17,7 +17,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_symbols() -> list[str]:
     text = (ROOT / "include" / "dimmerkv.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(dkv_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(dkv_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_the_python_exports():

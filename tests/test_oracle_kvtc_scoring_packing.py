@@ -266,3 +266,45 @@ def test_pack_ladder_sizes_and_offsets():
             width = bits[rung[t], g]
             body = blob[s + 4:s + 4 + 8 * width].tobytes()
             assert body == packing_ref.pack_ladder_codes(masked[t, g], width)
+
+
+@pytest.mark.parametrize("order_kind", ["irregular", "plane_major"])
+def test_pack_fast_equals_pack(order_kind):
+    """The vectorised packer (used at full size) gives the loop packer's four results byte for byte,
+    including tokens with no hot piece and tokens with every piece."""
+    rng = np.random.default_rng(61)
+    groups, tokens = 3, 50
+    if order_kind == "irregular":
+        order = pr.order_from_sequence([0, 1, 0, 2, 1, 0, 2, 2, 1, 0, 0, 1, 2, 0, 1, 2, 0, 1, 2, 0], groups)
+    else:
+        order = pr.plane_major_order(groups)
+    codes = rng.integers(0, 256, (tokens, groups, 64)).astype(np.uint8)
+    low = rng.standard_normal((tokens, groups)).astype(np.float16)
+    span = np.abs(rng.standard_normal((tokens, groups))).astype(np.float16)
+    pieces = rng.integers(0, order.pieces + 1, tokens)
+    pieces[:2] = (0, order.pieces)
+    for a, b in zip(packing_ref.pack(codes, low, span, pieces, order),
+                    packing_ref.pack_fast(codes, low, span, pieces, order)):
+        assert a.dtype == b.dtype and np.array_equal(a, b)
+
+
+def test_rung_errors_equal_decode_at_each_rung():
+    """A rung's error from the table lookup (progressive.py:159-160) equals the squared error of the
+    token decoded at that rung's plane map, summed over groups, over the mean energy; weights scale
+    each token by w / mean(w)."""
+    rng = np.random.default_rng(62)
+    tokens, groups = 30, 4
+    x = (rng.standard_normal((tokens, groups * 64)) * np.repeat(rng.uniform(0.01, 2, groups), 64)).astype(np.float32)
+    order = pr.order_from_sequence([0, 1, 2, 3, 0, 0, 1, 2, 3, 3, 1, 2, 0, 1, 2, 3] * 2, groups,
+                                   rungs=[0, 3, 7, 16, 32])
+    codes, low, span = pr.quantize8(x, 64)
+    table = pr.error_table(x, codes, low, span)
+    got = pr.rung_errors(x, table, order)
+    energy = np.float64(np.square(x.astype(np.float64)).sum(axis=1).mean())
+    for j, k in enumerate(order.rungs):
+        deq = pr.dequantize(codes, low, span, order.planes[k][None].repeat(tokens, 0)).astype(np.float64)
+        want = np.square(x - deq).sum(axis=1) / energy
+        np.testing.assert_allclose(got[:, j], want, rtol=1e-5, atol=1e-9)
+    w = rng.uniform(0.1, 3.0, tokens).astype(np.float32)
+    np.testing.assert_allclose(pr.rung_errors(x, table, order, w), got * (w / w.mean())[:, None], rtol=1e-5)
+    assert pr.level_bytes(order) == [int(order.prefix_bytes[k]) + 1 for k in order.rungs]
