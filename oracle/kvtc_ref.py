@@ -9,8 +9,17 @@ Follows scripts/kvtc.py of the reference:
 - ``rung_bytes``      :82-85
 - ``allocate_rungs``  :277-298 (fp64 values, cummin along levels, *stable*
   descending sort, take the sorted prefix whose cumulative cost fits)
+- ``compress_choice`` :157-233 (``KVTCCodec.compress`` up to the rung choice:
+  span, budget split, per-token relative errors over the stream's energy,
+  importance weights, key weight, the eviction level, the floor, allocation
+  over the levels from the floor up)
 
-Pins (tests/test_oracle_kvtc_scoring_packing.py): allocate_rungs against an exhaustive
+Pins (tests/test_oracle_kvtc_scoring_packing.py, tests/test_oracle_compress_choice.py):
+compress_choice against a per-token plain-Python statement, the floor against
+enumeration of the uniform rungs, and invariants that a dropped term breaks
+(key-only rescaling by a power of two leaves the choice unchanged only with the
+energy normalisation; zero-importance tokens stay at the floor; evicted keys
+evict their values; bytes within the budget); allocate_rungs against an exhaustive
 brute force of the same greedy rule on tiny inputs, against the invariants
 (budget respected, per-slot upgrades form a prefix), and against torch's
 stable sort on random inputs; quantize_groups against its closed-form grid
@@ -105,3 +114,57 @@ def allocate_rungs(errors: np.ndarray, level_bytes: np.ndarray, middle: int, bud
     counts = np.zeros(slots, dtype=np.int64)
     np.add.at(counts, taken // (levels - 1), 1)
     return counts
+
+
+def compress_choice(matrices: dict, means: dict, bases: dict, rungs: dict, rung_bytes: dict, exact_bytes: int,
+                    sinks: int, exact_recent: int, budget: float, group: int = 64, weights=None, evict: bool = False,
+                    floor_share: float = 0.0, key_weight: float = 1.0, coefficients: dict | None = None) -> dict:
+    """The per-token rung choice of ``KVTCCodec.compress(..., per_token=True)`` (kvtc.py:157-233).
+
+    ``matrices[kind]`` float32 [tokens, features] are the token matrices (keys already without
+    RoPE, kvtc.py:188), ``means``/``bases`` the stream calibration, ``rungs[kind]`` [R, groups] bit
+    widths and ``rung_bytes[kind]`` their sizes.  ``coefficients[kind]`` [middle, rank], when given,
+    replaces the projection (X - mean) @ basis of the middle tokens (kvtc.py:189), so a caller can
+    feed the exact values another implementation projected.  Returns {"key", "value": int64
+    [middle] rungs (-1 evicted, R = exact), "span": (start, end), "budget_bytes", "remaining",
+    "first" (the floor level), "errors": float32 [2 * middle, levels]}."""
+    tokens = matrices["key"].shape[0]
+    start = min(sinks, tokens)  # kvtc.py:177-180
+    end = max(start, tokens - exact_recent)
+    middle = end - start
+    budget_bytes = int(budget * tokens * 2 * exact_bytes)  # kvtc.py:182-183
+    remaining = budget_bytes - (tokens - middle) * 2 * exact_bytes
+    errors = []
+    for kind in ("key", "value"):
+        centred = (matrices[kind][start:end].astype(np.float32) - means[kind].astype(np.float32)).astype(np.float32)
+        coef = coefficients[kind] if coefficients is not None else (centred @ bases[kind].astype(np.float32))
+        coef = np.asarray(coef, dtype=np.float32)
+        energy = np.float32(np.square(centred).sum(axis=1, dtype=np.float32).mean(dtype=np.float32)) if middle else \
+            np.float32(0)  # :190-191
+        per_rung = [np.square(coef - quantize_groups(coef, bits, group)).sum(axis=1, dtype=np.float32)
+                    for bits in np.asarray(rungs[kind])]
+        columns = [(np.stack(per_rung, axis=1) / energy).astype(np.float32), np.zeros((middle, 1), np.float32)]
+        if evict:  # :195-197, the whole centred vector is lost
+            columns.insert(0, (np.square(coef).sum(axis=1, dtype=np.float32) / energy)[:, None].astype(np.float32))
+        err = np.concatenate(columns, axis=1)
+        if weights is not None:  # :198-201
+            w = np.asarray(weights, dtype=np.float32)[start:end]
+            err = (err * (w / max(np.float32(w.mean(dtype=np.float32)), np.float32(1e-12)))[:, None]).astype(np.float32)
+        if kind == "key":  # :202-203
+            err = (err * np.float32(key_weight)).astype(np.float32)
+        errors.append(err)
+    level_bytes = {kind: list(rung_bytes[kind]) + [exact_bytes] for kind in ("key", "value")}  # :206
+    evict_bytes = [0] if evict else []
+    first = 0
+    if floor_share > 0:  # :209-214
+        fits = [r for r in range(len(level_bytes["key"]))
+                if middle * (level_bytes["key"][r] + level_bytes["value"][r]) <= floor_share * remaining]
+        first = len(evict_bytes) + (max(fits) if fits else 0)
+    levels = np.concatenate([np.asarray(evict_bytes + level_bytes[kind], dtype=np.float64)[first:]
+                             for kind in ("key", "value")])
+    all_errors = np.concatenate([e[:, first:] for e in errors])
+    chosen = allocate_rungs(all_errors, levels, middle, remaining) + first - len(evict_bytes)  # :215-219
+    key, value = chosen[:middle].copy(), chosen[middle:].copy()
+    value[key < 0] = -1  # :220-221
+    return {"key": key, "value": value, "span": (start, end), "budget_bytes": budget_bytes, "remaining": remaining,
+            "first": first, "errors": np.concatenate(errors)}
