@@ -704,6 +704,224 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
   return base;
 }
 
+// ---------------------------------------------------------------------------
+// K3c: one workgroup per (sequence, output row).  It merges the tiles'
+// softmax statistics of the compressed part with the exact tokens (sinks,
+// recent window, new tokens) in one softmax and writes the row's output
+//   out = (e_c * (sum of the chunk partials) + e_c * L_c * mean_v
+//          + sum_e p_e * v_e) / (e_c * L_c + L_e),  e_c = exp(M_c - M).
+// This is a chain of dependent steps, so every global load it needs (tile
+// statistics, query, exact keys and values, mean, chunk partials) is issued
+// in one round at the start, when the memory system is quiet: after the
+// bulk value streaming of K3a has drained.
+// ---------------------------------------------------------------------------
+constexpr int kMaxExact = 1024;
+
+struct RowMergeArgs {
+  const int32_t* cu_seqlens;
+  const int32_t* cu_exact;
+  const float* tile_max;
+  const float* tile_sum;
+  const float* mean_v;
+  const float* key_exact;
+  const float* value_exact;
+  const float* mask;
+  const void* query;
+  const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
+  void* out;              // [batch][q_len][Hq][D], out_dtype
+  float scaling;
+  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
+  int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
+};
+
+constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
+
+constexpr int kChunkLoads = 8;  // chunk partials per thread issued in the first round
+
+template <int NT>
+__device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
+  constexpr int NW = NT / 64;
+  float* q = smem;               // [128] the query row
+  float* se = q + 128;           // [kMaxExact] exact scores, then weights
+  float* wred = se + kMaxExact;  // [2][NW] per-wave maxima and sums
+  float* buf = wred + 2 * NW;    // [NT] per-thread exact value sums
+  float* bc = buf + NT;          // [2] the compressed part's (max, sum)
+  float* cbuf = bc + 2;          // [NT] per-thread chunk-partial sums
+  const int row = wg % a.R_total;
+  const int b = wg / a.R_total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int D = a.D;
+  const int gq = a.Hq / a.Hkv;
+  const int qh = row / a.q_len, qi = row % a.q_len;
+  const int h = qh / gq;
+  const int e0 = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
+  const int E = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
+  const int d = tid % D, part = tid / D, parts = NT / D;
+  // Every global load goes out in one round before any value is used: each dependent round trip
+  // to memory costs microseconds here, and this work is nothing but them.  Loads under a
+  // per-element condition compile to one branch and one wait per load, so they are
+  // unconditional (clamped indices, valid dummy addresses) or under one uniform branch.
+  // (1) the tiles' softmax statistics (wave 0, 4 tiles per lane), (2) the query, (3) a quarter key
+  // row (token tid / 4, 32 dimensions), (4) exact values, (5) chunk partials and the mean.
+  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
+  const float* tm = ntb > 0 ? a.tile_max + (long)row * a.ntiles + tb0 : a.mean_v;
+  const float* ts = ntb > 0 ? a.tile_sum + (long)row * a.ntiles + tb0 : a.mean_v;
+  float m4[4], s4[4];
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = min(lane + 64 * k, max(ntb - 1, 0));
+      m4[k] = tm[t];
+      s4[k] = ts[t];
+    }
+  }
+  // the query element as the aligned 32-bit word that holds it (one load whatever the dtype; a
+  // 16-bit tensor has an even element count, so the word never passes its end), converted later
+  const long qidx = (((long)b * a.Hq + qh) * a.q_len + qi) * D + d;
+  const uint32_t qword = *(const uint32_t*)((const char*)a.query +
+                                            (a.query_dtype == DKV_F32 ? qidx * 4 : ((qidx * 2) & ~3L)));
+  const int kj = tid >> 2, ks = tid & 3;
+  const bool kslice = ks * 32 < D;
+  float4 k4[8];
+  float vv[kExactVB];
+  float mval = 0.0f;
+  if (E > 0) {
+    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
+                                       min(ks * 32, D - 32));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+#pragma unroll
+    for (int i = 0; i < kExactVB; ++i)
+      vv[i] = a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d];
+    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
+  } else {
+#pragma unroll
+    for (int i = 0; i < kExactVB; ++i) vv[i] = 0.0f;
+  }
+  // thread (d, part) sums the chunk partials part, part + parts, ... of output d
+  const long rows_all = (long)a.batch * a.R_total;
+  const float* cp = a.out_part + (long)wg * D + d;
+  float cv[kChunkLoads];
+#pragma unroll
+  for (int i = 0; i < kChunkLoads; ++i) cv[i] = cp[(long)min(part + i * parts, a.nchunks - 1) * rows_all * D];
+  const float mv = a.mean_v[((long)a.layer * a.Hkv + h) * D + d];
+  // now the values: the compressed part's online (max, sum) over this lane's tiles
+  float mm = -INFINITY, ll = 0.0f;
+  if (wave == 0) {
+    auto merge = [&](float mt, float st) {
+      if (mt == -INFINITY) return;
+      if (mt > mm) {
+        ll = ll * __expf(mm - mt) + st;
+        mm = mt;
+      } else {
+        ll += st * __expf(mt - mm);
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
+    for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
+  }
+  if (tid < D) {
+    const uint16_t q16 = (uint16_t)(qword >> ((qidx & 1) * 16));
+    q[tid] = a.query_dtype == DKV_F32 ? __uint_as_float(qword)
+           : a.query_dtype == DKV_BF16 ? bf16_bits_to_float(q16) : half_bits_to_float(q16);
+  }
+  if (wave == 0) {
+    const float m = wave_max(mm);
+    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
+    if (lane == 0) {
+      bc[0] = m;
+      bc[1] = l;
+    }
+  }
+  __syncthreads();
+  // exact scores: four lanes per token, 32 dimensions each, NT / 4 tokens per pass
+  float me = -INFINITY;
+  constexpr int TPP = NT / 4;
+  const int Epad = (E + TPP - 1) / TPP * TPP;
+  for (int j = kj; j < Epad; j += TPP) {
+    if (j != kj && j < E) {
+      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+      if (a.mask) mval = a.mask[(long)qi * E + j];
+    }
+    float dot = 0.0f;
+    if (kslice) {
+      const float* qr = q + ks * 32;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
+    }
+    dot += lane_xor1(dot);
+    dot += lane_xor2(dot);
+    if (j < E) {
+      const float sc = dot * a.scaling + mval;
+      if (ks == 0) se[j] = sc;
+      me = fmaxf(me, sc);
+    }
+  }
+  me = wave_max(me);
+  if (lane == 0) wred[wave] = me;
+  __syncthreads();
+  const float Mc = bc[0], Lc = bc[1];
+  float Me = wred[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) Me = fmaxf(Me, wred[w]);
+  const float M = fmaxf(Mc, Me);
+  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
+  float le = 0.0f;
+  for (int j = tid; j < E; j += NT) {
+    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
+    se[j] = wgt;
+    le += wgt;
+  }
+  le = wave_sum(le);
+  if (lane == 0) wred[NW + wave] = le;
+  __syncthreads();
+  float Le = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) Le += wred[NW + w];
+  const float denom = ec * Lc + Le;
+  // exact values: thread (d, part) takes tokens part, part + parts, ...
+  float ve = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kExactVB; ++i) {
+    const int j = part + i * parts;
+    if (j < E) ve += se[j] * vv[i];
+  }
+  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
+    float v8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = j0 + i * parts;
+      if (j < E) ve += se[j] * v8[i];
+    }
+  }
+  float cs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kChunkLoads; ++i) cs += part + i * parts < a.nchunks ? cv[i] : 0.0f;
+  for (int c = part + kChunkLoads * parts; c < a.nchunks; c += parts) cs += cp[(long)c * rows_all * D];
+  buf[tid] = ve;
+  cbuf[tid] = cs;
+  __syncthreads();
+  if (tid < D) {
+    float ves = 0.0f, csum = 0.0f;
+    for (int p = 0; p < parts; ++p) {
+      ves += buf[p * D + tid];
+      csum += cbuf[p * D + tid];
+    }
+    const float value = denom > 0.0f ? (ec * csum + ec * Lc * mv + ves) / denom : 0.0f;
+    store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * D + tid, a.out_dtype, value);
+  }
+}
+
+
 struct K3aArgs {
   const uint8_t* vcodes;  // decoded value codes, u8 [G][n_slots/16][64][16] (vcode_index)
   const float2* vaff;     // (scale, offset) per (group, token): value = code * scale + offset
@@ -1015,201 +1233,20 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// K3b: two kinds of workgroup in one launch.
-// - Row workgroups (the last batch * R_total, 4 waves each), one per
-//   (sequence, output row): merge the tiles' softmax statistics of the
-//   compressed part with the exact tokens (sinks, recent window, new tokens)
-//   in one softmax, and write the row's final affine form
-//     out = scale * (sum of its chunk partials) + base,
-//   scale = e_c / L, base = (e_c * L_c * mean_v + sum_e p_e * v_e) / L.
-//   This is all latency (dependent round trips to memory), so it runs beside
-//   the chunk workgroups instead of after them.
-// - Chunk workgroups, one per (sequence, KV head, 128-component chunk): sum
-//   the partials over the sequence's splits, multiply once by the value-basis
-//   chunk [128][D].
+// K3b: one workgroup per (sequence, KV head, 128-component chunk): sum the
+// value partials over the sequence's splits, multiply once by the value-basis
+// chunk [128][D].
 // ---------------------------------------------------------------------------
-constexpr int kMaxExact = 1024;
-
-struct RowMergeArgs {
-  const int32_t* cu_seqlens;
-  const int32_t* cu_exact;
-  const float* tile_max;
-  const float* tile_sum;
-  const float* mean_v;
-  const float* key_exact;
-  const float* value_exact;
-  const float* mask;
-  const void* query;
-  float* row_scale;  // [batch * R_total]
-  float* row_base;   // [batch * R_total][D]
-  float scaling;
-  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles;
-  int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
-};
-
 struct K3bArgs {
   const int32_t* cu_seqlens;
   const float* w_part;
   const uint16_t* value_basis;
   float* out_part;
   int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
-  RowMergeArgs m;
 };
 
-constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
-
-__device__ void row_merge(const RowMergeArgs& a, int wg) {
-  __shared__ float q[128];
-  __shared__ float se[kMaxExact];
-  __shared__ float wred[2][4];
-  __shared__ float buf[256];
-  __shared__ float bc[2];
-  const int row = wg % a.R_total;
-  const int b = wg / a.R_total;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int D = a.D;
-  const int gq = a.Hq / a.Hkv;
-  const int qh = row / a.q_len, qi = row % a.q_len;
-  const int h = qh / gq;
-  const int e0 = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
-  const int E = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
-  const int d = tid % D, part = tid / D, parts = 256 / D;
-  // Every global load of the first 64 exact tokens goes out in one round, before any wait: each
-  // dependent round trip to memory costs microseconds here, and this work is nothing but them.
-  // (1) the tiles' softmax statistics (wave 0; 4 tiles per lane at once), (2) the query, (3) a
-  // quarter key row (token tid / 4, 32 dimensions), (4) exact values.
-  float mm = -INFINITY, ll = 0.0f;
-  if (wave == 0) {
-    const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-    const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
-    const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
-    const float* tm = a.tile_max + (long)row * a.ntiles + tb0;
-    const float* ts = a.tile_sum + (long)row * a.ntiles + tb0;
-    float m4[4], s4[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int t = min(lane + 64 * k, max(ntb - 1, 0));
-      m4[k] = ntb > 0 ? tm[t] : -INFINITY;
-      s4[k] = ntb > 0 ? ts[t] : 0.0f;
-    }
-    auto merge = [&](float mt, float st) {  // online merge of this lane's tiles
-      if (mt == -INFINITY) return;
-      if (mt > mm) {
-        ll = ll * __expf(mm - mt) + st;
-        mm = mt;
-      } else {
-        ll += st * __expf(mt - mm);
-      }
-    };
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
-    for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
-  }
-  if (tid < D) q[tid] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + tid, a.query_dtype);
-  const int kj = tid >> 2, ks = tid & 3;
-  const bool kslice = ks * 32 < D;
-  float4 k4[8];
-  float mval = 0.0f;
-  if (E > 0) {
-    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
-                                       min(ks * 32, D - 32));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
-    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
-  }
-  float vv[kExactVB];
-#pragma unroll
-  for (int i = 0; i < kExactVB; ++i)
-    vv[i] = E > 0 ? a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d] : 0.0f;
-  if (wave == 0) {
-    const float m = wave_max(mm);
-    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
-    if (lane == 0) {
-      bc[0] = m;
-      bc[1] = l;
-    }
-  }
-  __syncthreads();
-  // exact scores: four lanes per token, 32 dimensions each, 64 tokens per pass
-  float me = -INFINITY;
-  const int E64 = (E + 63) & ~63;
-  for (int j = kj; j < E64; j += 64) {
-    if (j != kj && j < E) {
-      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
-#pragma unroll
-      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
-      if (a.mask) mval = a.mask[(long)qi * E + j];
-    }
-    float dot = 0.0f;
-    if (kslice) {
-      const float* qr = q + ks * 32;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
-    }
-    dot += lane_xor1(dot);
-    dot += lane_xor2(dot);
-    if (j < E) {
-      const float sc = dot * a.scaling + mval;
-      if (ks == 0) se[j] = sc;
-      me = fmaxf(me, sc);
-    }
-  }
-  me = wave_max(me);
-  if (lane == 0) wred[0][wave] = me;
-  __syncthreads();
-  const float Mc = bc[0], Lc = bc[1];
-  const float Me = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
-  const float M = fmaxf(Mc, Me);
-  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
-  float le = 0.0f;
-  for (int j = tid; j < E; j += 256) {
-    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
-    se[j] = wgt;
-    le += wgt;
-  }
-  le = wave_sum(le);
-  if (lane == 0) wred[1][wave] = le;
-  __syncthreads();
-  const float Le = wred[1][0] + wred[1][1] + wred[1][2] + wred[1][3];
-  const float denom = ec * Lc + Le;
-  // exact values: thread (d, part) takes tokens part, part + parts, ...
-  float ve = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kExactVB; ++i) {
-    const int j = part + i * parts;
-    if (j < E) ve += se[j] * vv[i];
-  }
-  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
-    float v8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = j0 + i * parts;
-      if (j < E) ve += se[j] * v8[i];
-    }
-  }
-  buf[tid] = ve;
-  __syncthreads();
-  if (tid < D) {
-    float ves = 0.0f;
-    for (int p = 0; p < parts; ++p) ves += buf[p * D + tid];
-    const float cm = ec * Lc * a.mean_v[((long)a.layer * a.Hkv + h) * D + tid];
-    a.row_base[(long)wg * D + tid] = denom > 0.0f ? (cm + ves) / denom : 0.0f;
-    if (tid == 0) a.row_scale[wg] = denom > 0.0f ? ec / denom : 0.0f;
-  }
-}
-
 __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
-  // the row workgroups come after the chunk workgroups (measured faster than before them)
-  const int chunk_wgs = (int)gridDim.x - a.batch * a.R_total;
-  if ((int)blockIdx.x >= chunk_wgs) {
-    row_merge(a.m, blockIdx.x - chunk_wgs);
-    return;
-  }
-  __shared__ float W[8][kChunk];
+  __shared__ __attribute__((aligned(16))) float W[8][kChunk];
   __shared__ float red[4][8][130];
   const int bid = blockIdx.x;
   const int c = bid % a.nchunks;
@@ -1227,32 +1264,40 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
   const int dp = tid % npair, part = tid / npair;
   const int ilen = kChunk / parts;
   const uint32_t* bv = (const uint32_t*)(a.value_basis + (((long)a.layer * a.Hkv + h) * a.rank + (long)c * kChunk) * D);
-  const long sp_stride = (long)a.R_total * a.rank;
+  // The basis chunk (shared by every row) and the first rows' split partials go out in one round:
+  // loads are unconditional (clamped indices), because a load under a per-element condition
+  // compiles to its own branch and wait.  Thread (dp, part) holds components part * ilen .. +ilen
+  // of dimension pair dp.
+  uint32_t bw[kChunk / 4];
+#pragma unroll
+  for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = bv[(long)(part * ilen + min(ii, ilen - 1)) * npair + dp];
+  const long sp_stride4 = (long)a.R_total * a.rank / 4;  // split stride in float4 units
+  const int rr = tid >> 5, k4 = tid & 31;                // the W element (row rr, components 4 k4 .. +4)
   for (int r0 = 0; r0 < RH; r0 += 8) {
     const int nr = min(8, RH - r0);
-    // partial sums over the splits, all loads of a thread issued together
-    for (int e = tid; e < nr * kChunk; e += 256) {
-      const int rr = e / kChunk, i = e % kChunk;
-      const float* src = a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + rr) * a.rank + c * kChunk + i;
-      // splits in batches of 8 whose loads go out together (indices clamped, extras masked)
-      float s = 0.0f;
-      for (int s0 = 0; s0 < nsp; s0 += 8) {
-        float v[8];
+    if (r0 > 0) __syncthreads();  // W and red are reused; no barrier (and wait) before the first loads
+    // W[rr][4 k4 ..] = sum over the sequence's splits, in split order (16 loads per batch in flight)
+    const float4* src = (const float4*)(a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + min(rr, nr - 1)) * a.rank +
+                                        (long)c * kChunk) + k4;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nsp; s0 += 16) {
+      float4 v[16];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, nsp - 1) * sp_stride];
+      for (int k = 0; k < 16; ++k) v[k] = src[(long)min(s0 + k, nsp - 1) * sp_stride4];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) s += s0 + k < nsp ? v[k] : 0.0f;
+      for (int k = 0; k < 16; ++k) {  // past the last split the (finite) repeat is added as exactly 0
+        const float keep = s0 + k < nsp ? 1.0f : 0.0f;
+        sum.x += v[k].x * keep;
+        sum.y += v[k].y * keep;
+        sum.z += v[k].z * keep;
+        sum.w += v[k].w * keep;
       }
-      W[rr][i] = s;
     }
+    if (rr < nr) *(float4*)&W[rr][4 * k4] = sum;
     __syncthreads();
     float acc0[8], acc1[8];
 #pragma unroll
     for (int rr = 0; rr < 8; ++rr) acc0[rr] = acc1[rr] = 0.0f;
-    // (issued after the partial sums: putting these loads first measured slower)
-    uint32_t bw[kChunk / 4];
-#pragma unroll
-    for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = bv[(long)(part * ilen + min(ii, ilen - 1)) * npair + dp];
 #pragma unroll
     for (int ii = 0; ii < kChunk / 4; ++ii) {
       if (ii >= ilen) break;
@@ -1290,44 +1335,14 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
       const float s = red[0][rr][dd] + red[1][rr][dd] + red[2][rr][dd] + red[3][rr][dd];
       a.out_part[(((long)c * a.batch + b) * a.R_total + (long)h * RH + r0 + rr) * D + dd] = s;
     }
-    __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------------------
-// K3c: one thread per (sequence, output row, dimension):
-// out = scale * (sum of the row's chunk partials, in chunk order) + base.
-// ---------------------------------------------------------------------------
-struct K3cArgs {
-  const float* out_part;   // [nchunks][batch * R_total][D]
-  const float* row_scale;  // [batch * R_total]
-  const float* row_base;   // [batch * R_total][D]
-  void* out;
-  int batch, Hq, q_len, D, R_total, nchunks, out_dtype;
-};
+constexpr int kFinishThreads = 256;
 
-constexpr int kFinishThreads = 64;
-
-__global__ __launch_bounds__(kFinishThreads) void finish_kernel(K3cArgs a) {
-  const long n = (long)a.batch * a.R_total * a.D;
-  const long i = (long)blockIdx.x * kFinishThreads + threadIdx.x;
-  if (i >= n) return;
-  const int d = (int)(i % a.D);
-  const long br = i / a.D;
-  const int row = (int)(br % a.R_total);
-  const int b = (int)(br / a.R_total);
-  const float scale = a.row_scale[br];
-  const float base = a.row_base[i];
-  float s = 0.0f;
-  for (int c0 = 0; c0 < a.nchunks; c0 += 16) {
-    float v[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) v[k] = a.out_part[(long)min(c0 + k, a.nchunks - 1) * n + i];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) s += c0 + k < a.nchunks ? v[k] : 0.0f;
-  }
-  const int qh = row / a.q_len, qi = row % a.q_len;
-  store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * a.D + d, a.out_dtype, scale * s + base);
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(RowMergeArgs a) {
+  __shared__ float smem[128 + kMaxExact + 2 * (kFinishThreads / 64) + 2 * kFinishThreads + 2];
+  row_finish<kFinishThreads>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1336,7 +1351,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(K3cArgs a) {
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
   int ksplit;
-  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, row_scale, row_base, split_scores,
+  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, split_scores,
       total;
 };
 
@@ -1356,7 +1371,7 @@ inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
 }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
-// [split partials][chunk partials][row scales][row bases][K2 rank-slice partial scores].
+// [split partials][chunk partials][K2 rank-slice partial scores].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
@@ -1390,10 +1405,6 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)L.nsplits * L.R_total * a->rank * 4);
   L.out_part = off;
   off += align256((size_t)L.nchunks * a->batch * L.R_total * a->head_dim * 4);
-  L.row_scale = off;
-  off += align256((size_t)a->batch * L.R_total * 4);
-  L.row_base = off;
-  off += align256((size_t)a->batch * L.R_total * a->head_dim * 4);
   L.ksplit = k2_split(a, L.ntiles);
   L.split_scores = off;
   if (L.ksplit > 1) off += align256((size_t)L.ksplit * L.R_total * L.ntiles * kTileTok * 4);
@@ -1592,7 +1603,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
   const int G = dkv::stream_groups(a->key);
-  if (L.nsplits > 0) {
+  if (L.nsplits > 0) {  // K3a: one workgroup per (split, group, row block)
     K3aArgs k{};
     k.vcodes = (const uint8_t*)(ws + L.vcodes);
     k.vaff = (const float2*)(ws + L.vaff);
@@ -1629,7 +1640,12 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.rank = a->rank;
   kb.R_total = L.R_total;
   kb.nchunks = L.nchunks;
-  RowMergeArgs& m = kb.m;
+  const long k3b_blocks = (long)a->batch * a->kv_heads * L.nchunks;
+  hipLaunchKernelGGL(basis_apply_kernel, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
+  rc = dkv::check_launch("basis_apply");
+  if (rc) return rc;
+  // K3c: one workgroup per (sequence, output row)
+  RowMergeArgs m{};
   m.cu_seqlens = a->cu_seqlens;
   m.cu_exact = a->cu_exact;
   m.tile_max = (const float*)(ws + L.tile_max);
@@ -1640,8 +1656,10 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   m.value_exact = a->value_exact;
   m.mask = a->mask;
   m.query = a->query;
-  m.row_scale = (float*)(ws + L.row_scale);
-  m.row_base = (float*)(ws + L.row_base);
+  m.out_part = (const float*)(ws + L.out_part);
+  m.out = a->out;
+  m.out_dtype = a->out_dtype;
+  m.nchunks = L.nchunks;
   m.scaling = a->scaling;
   m.batch = a->batch;
   m.n_total = L.n_total;
@@ -1655,25 +1673,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   m.R_total = L.R_total;
   m.E_total = E_total;
   m.query_dtype = a->query_dtype;
-  const long k3b_blocks = (long)a->batch * L.R_total + (long)a->batch * a->kv_heads * L.nchunks;
-  hipLaunchKernelGGL(basis_apply_kernel, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
-  rc = dkv::check_launch("basis_apply");
-  if (rc) return rc;
-  K3cArgs kc{};
-  kc.out_part = (const float*)(ws + L.out_part);
-  kc.row_scale = (const float*)(ws + L.row_scale);
-  kc.row_base = (const float*)(ws + L.row_base);
-  kc.out = a->out;
-  kc.batch = a->batch;
-  kc.Hq = a->q_heads;
-  kc.q_len = a->q_len;
-  kc.D = a->head_dim;
-  kc.R_total = L.R_total;
-  kc.nchunks = L.nchunks;
-  kc.out_dtype = a->out_dtype;
-  const long outs = (long)a->batch * L.R_total * a->head_dim;
-  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((outs + kFinishThreads - 1) / kFinishThreads)),
-                     dim3(kFinishThreads), 0, st, kc);
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kFinishThreads), 0, st, m);
   return dkv::check_launch("finish");
 }
 
