@@ -55,6 +55,9 @@ def parse():
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    p.add_argument("--gemm-reference", action="store_true",
+                   help="only time the bare fp16 GEMM of K2's key-rebuild shape at 3b-16k-3pct through "
+                        "torch.matmul (hipBLASLt): a library figure beside the fused kernel; one JSON line")
     return p.parse_args()
 
 
@@ -78,6 +81,31 @@ def copy_calibration(mib: int) -> None:
                       "copy_read_plus_write_GBps": round(2 * n / seconds / 1e9, 1)}), flush=True)
 
 
+def gemm_reference(steps: int = 50) -> None:
+    """[16,348 x 2,048] x [2,048 x 1,024] fp16: the decoded key coefficients of one layer times the key
+    basis of its 8 KV heads, which K2 computes fused with the decode epilogue (RoPE, QK, softmax
+    statistics).  The library GEMM does none of that work, so it bounds what an unfused K2 would cost."""
+    import torch
+
+    n, rank, width = 16348, 2048, 1024
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = torch.randn(n, rank, device="cuda", dtype=torch.float16, generator=g) * 0.01
+    b = torch.randn(rank, width, device="cuda", dtype=torch.float16, generator=g) * 0.01
+    c = torch.empty(n, width, device="cuda", dtype=torch.float16)
+    for _ in range(10):
+        torch.matmul(a, b, out=c)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        torch.matmul(a, b, out=c)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / steps * 1e3
+    print(json.dumps({"gemm": f"fp16 [{n} x {rank}] x [{rank} x {width}] (torch.matmul)", "launches": steps,
+                      "us_per_gemm": round(us, 2), "TFLOPs": round(2 * n * rank * width / us / 1e6, 1)}), flush=True)
+
+
 def read_traffic(path: str):
     """HBM bytes per K2 launch from a committed rocprofv3 --pmc summary (line 'traffic_bytes_per_launch: N')."""
     try:
@@ -89,8 +117,24 @@ def read_traffic(path: str):
     return None
 
 
+def host_cores() -> int:
+    """The cores this process may run on (its CPU affinity), capped by OMP_NUM_THREADS when that is set:
+    the host's share for this GPU."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
 def cpu_baseline(w, seconds: float):
-    """Oracle (numpy fp32) attention for a bounded number of layers of the same workload, scaled to a step."""
+    """Oracle (numpy fp32) attention of the same workload on every host core this process may use:
+    one warm-up layer, then three passes over the layers (all of them when a pass fits a third of
+    ``seconds``, else the first k), each pass's mean per-layer time scaled to a step; the reported
+    rate is the median of the three passes."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
@@ -98,7 +142,7 @@ def cpu_baseline(w, seconds: float):
     from oracle import attention_ref
 
     s = w.shape
-    cores = min(16, os.cpu_count() or 1)
+    cores = host_cores()
     coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
     kb = w.synthetic_basis_host
     positions = w.context.positions.long().cpu()
@@ -106,29 +150,32 @@ def cpu_baseline(w, seconds: float):
     sin = w.tables.rope_sin.cpu()[positions].numpy()
     cos, sin = np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
     wdt = s.kv_heads * s.head_dim
-    times = []
+    inputs = {}
+
+    def layer_inputs(layer):
+        if layer not in inputs:
+            inputs[layer] = (w.queries[layer].float().cpu().numpy(), kb["key"][layer * wdt:(layer + 1) * wdt].T,
+                             kb["value"][layer * wdt:(layer + 1) * wdt].T, w.tables.mean_k[layer].cpu().numpy(),
+                             w.tables.mean_v[layer].cpu().numpy(), w.key_exact[layer][None].cpu().numpy(),
+                             w.value_exact[layer][None].cpu().numpy())
+        return inputs[layer]
+
+    def run(layer):
+        q, bk, bv, mk, mv, ke, ve = layer_inputs(layer)
+        t0 = time.perf_counter()
+        attention_ref.attend(q, coef["key"], coef["value"], bk, bv, mk, mv, cos, sin, ke, ve)
+        return time.perf_counter() - t0
+
     with threadpool_limits(limits=cores):
-        t_start = time.perf_counter()
-        step = 0
-        # every layer once, then around again until the time bound
-        while step < s.layers or time.perf_counter() - t_start < seconds:
-            layer = step % s.layers
-            q = w.queries[layer].float().cpu().numpy()
-            ke = w.key_exact[layer][None].cpu().numpy()
-            ve = w.value_exact[layer][None].cpu().numpy()
-            bk = kb["key"][layer * wdt:(layer + 1) * wdt].T
-            bv = kb["value"][layer * wdt:(layer + 1) * wdt].T
-            mk = w.tables.mean_k[layer].cpu().numpy()
-            mv = w.tables.mean_v[layer].cpu().numpy()
-            t0 = time.perf_counter()
-            attention_ref.attend(q, coef["key"], coef["value"], bk, bv, mk, mv, cos, sin, ke, ve)
-            times.append(time.perf_counter() - t0)
-            step += 1
-    per_layer = sum(times) / len(times)
+        warm = run(0)
+        per_pass = max(1, min(s.layers, int(seconds / 3 / max(warm, 1e-6))))
+        passes = [float(np.mean([run(layer) for layer in range(per_pass)])) for _ in range(3)]
+    per_layer = float(np.median(passes))
     return {"value": 1.0 / (per_layer * s.layers), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} layer passes ({s.layers} layers, cycled for {sum(times):.1f} s) of the same "
-                      f"workload through the numpy fp32 oracle (oracle/attention_ref.attend over K1-decoded "
-                      f"coefficients), {per_layer * 1e3:.0f} ms/layer, scaled x{s.layers}"}
+            "sample": f"numpy fp32 oracle (oracle/attention_ref.attend over K1-decoded coefficients) of the same "
+                      f"workload on {cores} host cores: one warm-up layer, then 3 passes over {per_pass} of "
+                      f"{s.layers} layers; median pass {per_layer * 1e3:.0f} ms/layer (passes "
+                      f"{', '.join(f'{p * 1e3:.0f}' for p in passes)} ms), scaled x{s.layers}"}
 
 
 def question_stage(w):
@@ -276,6 +323,9 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.gemm_reference:
+        gemm_reference()
         return
     if args.storage:
         storage_bench()

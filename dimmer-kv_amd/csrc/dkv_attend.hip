@@ -58,6 +58,9 @@ struct K2Args {
   float scaling;
   int batch, layer, Hkv, Hq, q_len, G, n_total, n_slots, ntiles, total_wg, per_xcd, query_dtype;
   int rope_rows;  // rows of the RoPE tables: positions are clamped to 0 .. rope_rows - 1
+  // question scoring: (max, sum exp) of every row over each 64-token quarter of a tile, [R][ntiles * 4]
+  float* sub_max;
+  float* sub_sum;
   // rank split (decoding with few workgroups): each workgroup rebuilds its keys from g_per_split
   // of the 64-component groups and writes partial scores [ksplit][R_total][ntiles * 256]
   float* split_scores;
@@ -143,6 +146,19 @@ DKV_DEVICE long prob_index(long row, long slot, int R_total) {
   return ((slot >> 4) * R_total + row) * 16 + (slot & 15);
 }
 
+// Where K2 writes the probability of (row, slot) when decoding: the value side's blocked layout.
+// Question scoring uses qprob_index.
+DKV_DEVICE long k2_prob_index(long row, long slot, int R_total, int ntiles, int rowmajor) {
+  return rowmajor ? row * ((long)ntiles * 256) + slot : prob_index(row, slot, R_total);
+}
+
+// Question scoring: row-major [R][ntiles * 256] with the tokens of each 64-token quarter q of a
+// tile interleaved in pairs: token q * 64 + h * 32 + j sits at position q * 64 + 2 j + h, so one
+// lane stores the pair (j, j + 32) of the MFMA output in 4 bytes.
+DKV_DEVICE long qprob_index(long row, int tile, int quarter, int j, int ntiles) {
+  return row * ((long)ntiles * 256) + (long)tile * 256 + quarter * 64 + 2 * j;
+}
+
 // ---------------------------------------------------------------------------
 // K1 (fp16 operand form): decode the hot key codes of every token into the
 // exact register image of a 32x32x16 MFMA operand: for 64-component group g,
@@ -206,7 +222,7 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs 
 // ---------------------------------------------------------------------------
 constexpr int kSmallRows = 4;
 
-template <int D, bool SPLIT>
+template <int D, bool SPLIT, bool ROWMAJOR>
 DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
                                            float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
                                            int tile, int h0, int b, int RH, const int* pos_s, const float* qs,
@@ -321,10 +337,25 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
                            (long)tile * kTileTok + n] = x[tb];
           continue;
         }
-        // fp32 scores are for question scoring (no probabilities then); decoding reads only the probabilities
+        // fp32 scores only when no probability buffer is given; decoding reads only the probabilities
         if (!a.probs && tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
       if constexpr (SPLIT) continue;
+      if constexpr (ROWMAJOR) {  // question scoring: this wave's quarter, written at once (see qprob_index)
+        const float mq = max32(fmaxf(x[0], x[1]));
+        const float e0 = mq == -INFINITY ? 0.0f : __expf(x[0] - mq);
+        const float e1 = mq == -INFINITY ? 0.0f : __expf(x[1] - mq);
+        const float sq = sum32(e0 + e1);
+        const long r_all = (long)h * RH + r;
+        if (lhi == 0)
+          *(uint32_t*)(a.probs + qprob_index(r_all, tile, tq, l32, a.ntiles)) =
+              (uint32_t)f16_bits(e0) | ((uint32_t)f16_bits(e1) << 16);
+        if (lane == 0) {
+          a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mq;
+          a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sq;
+        }
+        continue;
+      }
       const float mx = max32(fmaxf(x[0], x[1]));
       float sm = 0.0f;
       if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
@@ -335,7 +366,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       }
     }
   }
-  if constexpr (SPLIT) return;  // the merge kernel writes statistics and probabilities
+  if constexpr (SPLIT || ROWMAJOR) return;  // the merge kernel, or the loop above, wrote everything
   __syncthreads();
   if (tid < HPW * kSmallRows) {
     const int hl = tid / kSmallRows, r = tid % kSmallRows;
@@ -371,7 +402,8 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       const float x = xs[hw][r][lhi];
       const float p = (x == -INFINITY) ? 0.0f : __expf(x - M);
       const int n = tq * 64 + lhi * 32 + l32;
-      a.probs[prob_index((long)(h0 + hl) * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len)] = f16_bits(p);
+      a.probs[k2_prob_index((long)(h0 + hl) * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len, a.ntiles,
+                            ROWMAJOR)] = f16_bits(p);
     }
   }
 }
@@ -384,7 +416,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 // [256][64] are fetched into registers one group ahead and stored into a
 // double-buffered, padded LDS tile; 32x32x16 fp16 MFMAs accumulate the keys.
 // ---------------------------------------------------------------------------
-template <int D, bool SMALL, bool SPLIT = false>
+template <int D, bool SMALL, bool SPLIT = false, bool ROWMAJOR = false>
 __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   constexpr int HPW = 256 / D;      // heads per workgroup
   constexpr int DB = D / 32;        // 32-row blocks per head
@@ -555,7 +587,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int gq = a.Hq / a.Hkv;
   const int half_d = D / 2;
   if constexpr (SMALL) {
-    keys_scores_small_epilogue<D, SPLIT>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s, split);
+    keys_scores_small_epilogue<D, SPLIT, ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s,
+                                                   q_s, split);
     return;
   } else {
 
@@ -598,10 +631,13 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   }
   __syncthreads();
 
-  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block.
+  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block; the block's scores stay
+  // in registers until the tile maxima are known, then become fp16 probabilities relative to
+  // them (and fp32 scores only when no probability buffer is given).
   const int mblocks = (RH + 31) / 32;
   constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in this phase
   for (int mb = 0; mb < mblocks; ++mb) {
+    float xs[HPWAVE][16][2];
 #pragma unroll
     for (int hh = 0; hh < HPWAVE; ++hh) {
       const int hl = hs * HPWAVE + hh;
@@ -633,20 +669,47 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         }
       }
       // sacc[tb][v]: token tq*64 + tb*32 + l32, row mb*32 + 8*(v/4) + 4*lhi + (v&3)
+      if constexpr (ROWMAJOR) {
+        // question scoring: probabilities relative to this wave's 64 tokens (a tile quarter) and the
+        // quarter's (max, sum), written at once: no exchange between waves
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = mb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+          float x[2];
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            const int n = tq * 64 + tb * 32 + l32;
+            x[tb] = (row < RH) && (n < count) ? sacc[tb][v] * a.scaling : -INFINITY;
+          }
+          const float mx = max32(fmaxf(x[0], x[1]));
+          const float e0 = mx == -INFINITY ? 0.0f : __expf(x[0] - mx);
+          const float e1 = mx == -INFINITY ? 0.0f : __expf(x[1] - mx);
+          const float sm = sum32(e0 + e1);
+          if (row < RH) {
+            const long r_all = (long)h * RH + row;
+            const uint32_t pair = (uint32_t)f16_bits(e0) | ((uint32_t)f16_bits(e1) << 16);
+            *(uint32_t*)(a.probs + qprob_index(r_all, tile, tq, l32, a.ntiles)) = pair;
+            if (l32 == 0) {
+              a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mx;
+              a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sm;
+            }
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = mb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-        float x[2];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
           const int n = tq * 64 + tb * 32 + l32;
           const bool ok = (row < RH) && (n < count);
-          x[tb] = ok ? sacc[tb][v] * a.scaling : -INFINITY;
-          if (ok) a.scores[(long)(h * RH + row) * a.n_total + tok0 + n] = x[tb];
+          xs[hh][v][tb] = ok ? sacc[tb][v] * a.scaling : -INFINITY;
+          if (ok && !a.probs) a.scores[(long)(h * RH + row) * a.n_total + tok0 + n] = xs[hh][v][tb];
         }
-        const float mx = max32(fmaxf(x[0], x[1]));
+        const float mx = max32(fmaxf(xs[hh][v][0], xs[hh][v][1]));
         float sm = 0.0f;
-        if (mx != -INFINITY) sm = __expf(x[0] - mx) + __expf(x[1] - mx);
+        if (mx != -INFINITY) sm = __expf(xs[hh][v][0] - mx) + __expf(xs[hh][v][1] - mx);
         sm = sum32(sm);
         if (l32 == 0) {
           const int rr = 8 * (v >> 2) + 4 * lhi + (v & 3);
@@ -655,6 +718,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         }
       }
     }
+    if constexpr (ROWMAJOR) continue;  // question scoring wrote everything above
     __syncthreads();
     if (tid < HPW * 32) {
       const int hl = tid >> 5, rr = tid & 31;
@@ -676,19 +740,29 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         a.tile_sum[o] = S;
       }
     }
-    // probabilities relative to the tile maximum (fp16) for this block of rows, from the
-    // scores this workgroup wrote above (visible to it after the barrier); 0 past the tokens
-    for (int e = a.probs ? tid : HPW * 32 * kTileTok; e < HPW * 32 * kTileTok; e += kK2Threads) {
-      const int hl = e / (32 * kTileTok), rr = (e / kTileTok) % 32, n = e % kTileTok;
-      const int row = mb * 32 + rr;
-      if (row >= RH) continue;
-      float M = -INFINITY;
+    // probabilities relative to the tile maximum (fp16), from the registers; 0 past the tokens
+    if (a.probs) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
-      const long r_all = (long)(h0 + hl) * RH + row;
-      const float x = n < count ? a.scores[r_all * a.n_total + tok0 + n] : -INFINITY;
-      a.probs[prob_index(r_all, (long)tile * kTileTok + n, a.Hq * a.q_len)] =
-          f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
+      for (int hh = 0; hh < HPWAVE; ++hh) {
+        const int hl = hs * HPWAVE + hh;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rr = 8 * (v >> 2) + 4 * lhi + (v & 3);
+          const int row = mb * 32 + rr;
+          if (row >= RH) continue;
+          float M = -INFINITY;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
+          const long r_all = (long)(h0 + hl) * RH + row;
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            const float x = xs[hh][v][tb];
+            const int n = tq * 64 + tb * 32 + l32;
+            a.probs[k2_prob_index(r_all, (long)tile * kTileTok + n, a.Hq * a.q_len, a.ntiles, ROWMAJOR)] =
+                f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
+          }
+        }
+      }
     }
     __syncthreads();
   }
@@ -1438,7 +1512,10 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
   return DKV_OK;
 }
 
-int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st, bool probs = true) {
+// Decoding writes probabilities in the value side's layout (and may split the rank); question
+// scoring writes them row-major for the importance kernel and never splits.
+int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st, bool scoring = false,
+                       float* sub_max = nullptr, float* sub_sum = nullptr) {
   if (L.ntiles == 0) return DKV_OK;
   K2Args k{};
   k.coef = (const uint16_t*)(ws + L.coef);
@@ -1452,7 +1529,9 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.rope_rows = a->rope_rows;
   k.query = a->query;
   k.scores = (float*)(ws + L.scores);
-  k.probs = probs ? (uint16_t*)(ws + L.probs) : nullptr;
+  k.probs = (uint16_t*)(ws + L.probs);
+  k.sub_max = sub_max;
+  k.sub_sum = sub_sum;
   k.tile_max = (float*)(ws + L.tile_max);
   k.tile_sum = (float*)(ws + L.tile_sum);
   k.scaling = a->scaling;
@@ -1472,7 +1551,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   // decoding (at most kSmallRows query rows per KV head) and question scoring are separate
   // instantiations, so neither epilogue's registers weigh on the other's main loop
   const bool small = (a->q_heads / a->kv_heads) * a->q_len <= kSmallRows;
-  if (probs && L.ksplit > 1) {  // decoding with few workgroups: rank slices, then the merge
+  if (!scoring && L.ksplit > 1) {  // decoding with few workgroups: rank slices, then the merge
     k.ksplit = L.ksplit;
     k.g_per_split = k.G / L.ksplit;
     k.split_scores = (float*)(ws + L.split_scores);
@@ -1499,16 +1578,26 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
     hipLaunchKernelGGL(split_merge_kernel, dim3((unsigned)((long)L.ntiles * L.R_total)), dim3(kTileTok), 0, st, mg);
     return dkv::check_launch("split_merge");
   }
+  // probabilities: the value side's blocked layout when decoding, row-major [R][ntiles * 256] for
+  // question scoring (read by the importance kernel)
   if (a->head_dim == 128) {
-    if (small)
+    if (small && !scoring)
       hipLaunchKernelGGL((keys_scores_kernel<128, true>), grid, dim3(kK2Threads), 0, st, k);
-    else
+    else if (small)
+      hipLaunchKernelGGL((keys_scores_kernel<128, true, false, true>), grid, dim3(kK2Threads), 0, st, k);
+    else if (!scoring)
       hipLaunchKernelGGL((keys_scores_kernel<128, false>), grid, dim3(kK2Threads), 0, st, k);
-  } else {
-    if (small)
-      hipLaunchKernelGGL((keys_scores_kernel<64, true>), grid, dim3(kK2Threads), 0, st, k);
     else
+      hipLaunchKernelGGL((keys_scores_kernel<128, false, false, true>), grid, dim3(kK2Threads), 0, st, k);
+  } else {
+    if (small && !scoring)
+      hipLaunchKernelGGL((keys_scores_kernel<64, true>), grid, dim3(kK2Threads), 0, st, k);
+    else if (small)
+      hipLaunchKernelGGL((keys_scores_kernel<64, true, false, true>), grid, dim3(kK2Threads), 0, st, k);
+    else if (!scoring)
       hipLaunchKernelGGL((keys_scores_kernel<64, false>), grid, dim3(kK2Threads), 0, st, k);
+    else
+      hipLaunchKernelGGL((keys_scores_kernel<64, false, false, true>), grid, dim3(kK2Threads), 0, st, k);
   }
   return dkv::check_launch("keys_scores");
 }
@@ -1691,27 +1780,26 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
 // ===========================================================================
 // K4a: question scoring of the hot tier (scripts/progressive.py:239-254 with
 // scripts/dimmer.py:52-66).  Per layer: K2 scores every (query head, query
-// position) row against the compressed keys; row_stats merges the tiles'
-// softmax statistics with those of the exact context tokens and of the
-// question's own keys (causal); importance_part accumulates sum over rows of
-// p = exp(s - M) / L per token;
-// importance_add folds the row-chunk partials into importance[n] in a fixed
-// order, so results do not depend on scheduling.
+// position) row against the compressed keys and writes fp16 probabilities
+// relative to each tile's maximum (row-major) with the tiles' softmax
+// statistics; row_stats merges those statistics with the exact context tokens
+// and the question's own keys (causal) into the row's maximum M and sum L, and
+// writes each tile's factor exp(tile max - M) / L; importance adds
+// sum over rows of probability * factor to every token, in a fixed order, so
+// results do not depend on scheduling.
 // ===========================================================================
 namespace {
-
-constexpr int kRowChunk = 64;  // rows per importance_part workgroup
-constexpr int kTokChunk = 256;
 
 struct RowStatsArgs {
   const void* query;
   const float* key_exact;     // [Hkv][E][D]
   const float* key_question;  // [Hkv][Lq][D]
-  const float* tile_max;      // [R_total][ntiles] (compressed part, from K2)
-  const float* tile_sum;
+  const float* sub_max;       // [R_total][nsub] (compressed part per 64-token tile quarter, from K2)
+  const float* sub_sum;
   float* stat;                // [R_total][2]: softmax maximum M and 1 / L over every key of the row
+  float* fac;                 // [R_total][nsub]: exp(quarter max - M) / L, the quarter's probability factor
   float scaling;
-  int Hkv, Hq, q_len, D, E, query_dtype, ntiles;
+  int Hkv, Hq, q_len, D, E, query_dtype, nsub;
 };
 
 constexpr int kStatKeysPerThread = 16;  // keys per thread kept in registers (more are recomputed)
@@ -1731,8 +1819,8 @@ __global__ __launch_bounds__(128) void row_stats_kernel(RowStatsArgs a) {
   if (tid < D) q[tid] = load_as_float(a.query, ((long)qh * a.q_len + qi) * D + tid, a.query_dtype);
   // compressed part: online merge of this thread's tiles
   float mc = -INFINITY, lc = 0.0f;
-  for (int t = tid; t < a.ntiles; t += 128) {
-    const float mt = a.tile_max[(long)row * a.ntiles + t], st = a.tile_sum[(long)row * a.ntiles + t];
+  for (int t = tid; t < a.nsub; t += 128) {
+    const float mt = a.sub_max[(long)row * a.nsub + t], st = a.sub_sum[(long)row * a.nsub + t];
     if (mt == -INFINITY) continue;
     if (mt > mc) {
       lc = lc * __expf(mc - mt) + st;
@@ -1785,48 +1873,84 @@ __global__ __launch_bounds__(128) void row_stats_kernel(RowStatsArgs a) {
   l = wave_sum(l);
   if (lane == 0) red[1][wave] = l;
   __syncthreads();
+  const float L = red[1][0] + red[1][1];
+  const float invL = L > 0.0f ? 1.0f / L : 0.0f;
   if (tid == 0) {
-    const float L = red[1][0] + red[1][1];
     a.stat[2 * row] = M;
-    a.stat[2 * row + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+    a.stat[2 * row + 1] = invL;
+  }
+  // p = exp(s - M) / L = exp(s - quarter max) * fac: K2 wrote the first factor, the importance
+  // kernel applies the second
+  for (int t = tid; t < a.nsub; t += 128) {
+    const float mt = a.sub_max[(long)row * a.nsub + t];
+    a.fac[(long)row * a.nsub + t] = (mt == -INFINITY || M == -INFINITY) ? 0.0f : __expf(mt - M) * invL;
   }
 }
 
+// importance[t] += sum over rows r of probs[r][t] * fac[r][quarter of t]: one workgroup per 64-token
+// tile quarter.  Lane (row lane rl = lane / 8, position chunk tc = lane % 8) of wave w reads 8
+// positions (16 B) of rows w * 8 + rl, + 32, + 64, ...; the row lanes, then the waves, are summed in
+// a fixed order, so the result does not depend on scheduling.  Position 2 j + h of the quarter holds
+// token h * 32 + j (qprob_index).
 struct ImportanceArgs {
-  const float* scores;  // [R_total][n]
-  const float* stat;    // [R_total][2] (M, 1 / L) of every row (row_stats_kernel)
-  float* part;          // [nrc][n]
-  int R_total, n;
+  const uint16_t* probs;  // fp16 [R_total][ntiles * 256], relative to each quarter's maximum (K2)
+  const float* fac;       // [R_total][ntiles * 4] (row_stats_kernel)
+  float* importance;      // [n]
+  int R_total, n, ntiles;
 };
 
-__global__ __launch_bounds__(kTokChunk) void importance_part_kernel(ImportanceArgs a) {
-  __shared__ float Mr[kRowChunk];
-  __shared__ float invL[kRowChunk];
-  const int ntc = (a.n + kTokChunk - 1) / kTokChunk;
-  const int tc = blockIdx.x % ntc, rc = blockIdx.x / ntc;
-  const int tid = threadIdx.x;
-  const int r0 = rc * kRowChunk;
-  const int nr = min(kRowChunk, a.R_total - r0);
-  if (tid < nr) {
-    Mr[tid] = a.stat[2 * (r0 + tid)];
-    invL[tid] = a.stat[2 * (r0 + tid) + 1];
+constexpr int kImpBatch = 8;  // row iterations whose loads go out together
+
+__global__ __launch_bounds__(256) void importance_kernel(ImportanceArgs a) {
+  __shared__ float part[4][64];
+  const int sub = blockIdx.x;  // tile quarter: tile sub / 4, quarter sub % 4
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int rl = lane >> 3, tc = lane & 7;
+  const long pos = (long)sub * 64 + tc * 8;
+  const long pstride = (long)a.ntiles * kTileTok;
+  const int nsub = a.ntiles * 4;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int r0 = wave * 8 + rl; r0 < a.R_total; r0 += 32 * kImpBatch) {
+    uint4 pv[kImpBatch];
+    float fv[kImpBatch];
+#pragma unroll
+    for (int k = 0; k < kImpBatch; ++k) {  // clamped rows: every load is unconditional
+      const int r = min(r0 + 32 * k, a.R_total - 1);
+      pv[k] = *(const uint4*)(a.probs + (long)r * pstride + pos);
+      fv[k] = a.fac[(long)r * nsub + sub];
+    }
+#pragma unroll
+    for (int k = 0; k < kImpBatch; ++k) {
+      const float f = r0 + 32 * k < a.R_total ? fv[k] : 0.0f;
+      const uint32_t w[4] = {pv[k].x, pv[k].y, pv[k].z, pv[k].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += half_bits_to_float((uint16_t)(w[i] & 0xffffu)) * f;
+        acc[2 * i + 1] += half_bits_to_float((uint16_t)(w[i] >> 16)) * f;
+      }
+    }
+  }
+  // sum the 8 row lanes (lane bits 3..5) of each position chunk, then the 4 waves
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float v = acc[i];
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    acc[i] = v;
+  }
+  if (rl == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[wave][tc * 8 + i] = acc[i];
   }
   __syncthreads();
-  const int tok = tc * kTokChunk + tid;
-  if (tok >= a.n) return;
-  float acc = 0.0f;
-#pragma unroll 16
-  for (int r = 0; r < nr; ++r) acc += __expf(a.scores[(long)(r0 + r) * a.n + tok] - Mr[r]) * invL[r];
-  a.part[(long)rc * a.n + tok] = acc;
-}
-
-__global__ __launch_bounds__(256) void importance_add_kernel(const float* __restrict__ part, int nrc, int n,
-                                                             float* __restrict__ importance) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  float s = 0.0f;
-  for (int r = 0; r < nrc; ++r) s += part[(long)r * n + i];
-  importance[i] += s;
+  if (tid < 64) {
+    // position tid of the quarter holds token (tid % 2) * 32 + tid / 2 of it (one sequence: tokens are slots)
+    const int t = sub * 64 + (tid & 1) * 32 + (tid >> 1);
+    if (t < a.n) a.importance[t] += part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+  }
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int n) {
@@ -1836,19 +1960,24 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, i
 
 struct ScoreLayout {
   Layout base;
-  size_t stat, part, total;
-  int nrc;
+  size_t sub_max, sub_sum, stat, fac, total;
 };
 
+// The attend layout up to the tile statistics (decoded keys, probabilities), then the per-quarter
+// statistics, the per-row statistics and the per-(row, quarter) probability factors.
 ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   ScoreLayout S{};
   S.base = make_layout(a);
-  size_t off = S.base.w_part;  // scores + tile stats are shared with the attend layout
+  const size_t per_quarter = align256((size_t)S.base.R_total * S.base.ntiles * 4 * 4);
+  size_t off = S.base.w_part;
+  S.sub_max = off;
+  off += per_quarter;
+  S.sub_sum = off;
+  off += per_quarter;
   S.stat = off;
   off += align256((size_t)S.base.R_total * 2 * 4);
-  S.nrc = (S.base.R_total + kRowChunk - 1) / kRowChunk;
-  S.part = off;
-  off += align256((size_t)S.nrc * S.base.n_total * 4);
+  S.fac = off;
+  off += per_quarter;
   S.total = off;
   return S;
 }
@@ -1968,14 +2097,14 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
               "dkv_score_layer: workspace %zu B < required %zu B", workspace_bytes, S.total);
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
-  rc = launch_keys_scores(a, S.base, ws, st, /*probs=*/false);
+  rc = launch_keys_scores(a, S.base, ws, st, /*scoring=*/true, (float*)(ws + S.sub_max), (float*)(ws + S.sub_sum));
   if (rc) return rc;
   RowStatsArgs e{};
   e.query = a->query;
   e.key_exact = a->key_exact;
   e.key_question = key_question;
-  e.tile_max = (const float*)(ws + S.base.tile_max);
-  e.tile_sum = (const float*)(ws + S.base.tile_sum);
+  e.sub_max = (const float*)(ws + S.sub_max);
+  e.sub_sum = (const float*)(ws + S.sub_sum);
   e.stat = (float*)(ws + S.stat);
   e.scaling = a->scaling;
   e.Hkv = a->kv_heads;
@@ -1984,25 +2113,21 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   e.D = a->head_dim;
   e.E = E;
   e.query_dtype = a->query_dtype;
-  e.ntiles = S.base.ntiles;
+  e.nsub = S.base.ntiles * 4;
+  e.fac = (float*)(ws + S.fac);
   hipLaunchKernelGGL(row_stats_kernel, dim3(S.base.R_total), dim3(128), 0, st, e);
   rc = dkv::check_launch("row_stats");
   if (rc) return rc;
-  const int n = S.base.n_total;
-  if (n == 0) return DKV_OK;
+  if (S.base.n_total == 0) return DKV_OK;
   ImportanceArgs im{};
-  im.scores = (const float*)(ws + S.base.scores);
-  im.stat = (const float*)(ws + S.stat);
-  im.part = (float*)(ws + S.part);
+  im.probs = (const uint16_t*)(ws + S.base.probs);
+  im.fac = (const float*)(ws + S.fac);
+  im.importance = importance;
   im.R_total = S.base.R_total;
-  im.n = n;
-  const int ntc = (n + kTokChunk - 1) / kTokChunk;
-  hipLaunchKernelGGL(importance_part_kernel, dim3(ntc * S.nrc), dim3(kTokChunk), 0, st, im);
-  rc = dkv::check_launch("importance_part");
-  if (rc) return rc;
-  hipLaunchKernelGGL(importance_add_kernel, dim3((n + 255) / 256), dim3(256), 0, st, (const float*)(ws + S.part),
-                     S.nrc, n, importance);
-  return dkv::check_launch("importance_add");
+  im.n = S.base.n_total;
+  im.ntiles = S.base.ntiles;
+  hipLaunchKernelGGL(importance_kernel, dim3((unsigned)S.base.ntiles * 4), dim3(256), 0, st, im);
+  return dkv::check_launch("importance");
 }
 
 extern "C" size_t dkv_topk_workspace_bytes(int32_t n) {

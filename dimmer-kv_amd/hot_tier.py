@@ -173,16 +173,19 @@ class PackedStream:
         the other's new offset.  Rows already at full precision cost nothing (their cold blob is
         empty) and are merged like the others, so no host-side filtering is needed; the fetched
         count is the only value read back."""
-        rows = rows.to(device=self.blob.device, dtype=torch.int32).contiguous()
         if rows.numel() == 0:
             return 0
         if self.cold is None:
             raise ValueError("this stream was packed without a cold tier")
-        lo, hi = int(rows.min()), int(rows.max())
-        if lo < 0 or hi >= self.n:
-            raise ValueError(f"refine rows must lie in 0..{self.n - 1} (got {lo}..{hi})")
+        device = self.blob.device
+        rows_h = rows.detach().to("cpu", torch.int64).numpy()  # a question selects a few hundred rows
+        if rows_h.min() < 0 or rows_h.max() >= self.n:
+            raise ValueError(f"refine rows must lie in 0..{self.n - 1} (got {rows_h.min()}..{rows_h.max()})")
+        rows = rows.to(device=device, dtype=torch.int32).contiguous()
         fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
-        rows = torch.unique(rows)
+        distinct = np.unique(rows_h)
+        if distinct.size != rows_h.size:
+            rows = torch.from_numpy(distinct.astype(np.int32)).to(device)
         k = rows.numel()
         if self.refined + k > self.refine_capacity:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")

@@ -112,6 +112,37 @@ def test_refine_then_attend():
     assert sum(streams[k].refine(torch.from_numpy(rows).to(DEV)) for k in ("key", "value")) == 0
 
 
+@pytest.mark.parametrize("tier", ["device", "host"])
+def test_refine_with_repeated_rows(tier):
+    """Rows given more than once: ``fetched`` counts each occurrence (the reference's formula over
+    the rows as given, scripts/progressive.py:232), the gather runs once per distinct row, and the
+    refined tier is byte for byte the tier refined with the distinct rows; rows outside the stream
+    raise before anything runs."""
+    from hot_tier import OrderTables, PackedStream
+
+    shape = synth.ModelShape(2, 8, 64, 32, 1024)
+    print(f"[case] refine with repeated rows ({tier} cold tier)", flush=True)
+    case = build_case(shape, 900, seed=79, query_scale=60.0)
+    otab = OrderTables(case.order.planes, case.order.prefix_bytes, DEV)
+
+    def packed():
+        return PackedStream.pack(torch.from_numpy(case.codes["key"]).to(DEV), torch.from_numpy(case.low["key"]).to(DEV),
+                                 torch.from_numpy(case.span["key"]).to(DEV),
+                                 torch.from_numpy(case.pieces["key"]).to(DEV), otab, refine_capacity=16, cold_tier=tier)
+
+    rows = np.array([7, 300, 7, 42, 300, 300, 5])
+    a, b = packed(), packed()
+    fetched = a.refine(torch.from_numpy(rows).to(DEV))
+    assert fetched == pr.fetched_bytes({"key": case.order}, {"key": case.pieces["key"]}, rows)
+    b.refine(torch.from_numpy(np.unique(rows)).to(DEV))
+    torch.cuda.synchronize()
+    assert a.refined == b.refined == len(np.unique(rows))
+    assert torch.equal(a.pieces, b.pieces) and torch.equal(a.tok_off, b.tok_off)
+    assert torch.equal(a.blob, b.blob)
+    with pytest.raises(ValueError, match="refine rows"):
+        a.refine(torch.tensor([0, case.ctx.middle], device=DEV))
+
+
 def test_refine_from_host_cold_tier_matches_device_tier():
     """A cold tier in pinned host memory (only the chosen tokens' planes copied over) refines to the
     same bytes as the device-resident one, including rows refined twice and rows already full."""
