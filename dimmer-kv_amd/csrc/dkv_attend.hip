@@ -51,8 +51,7 @@ struct K2Args {
   const float* rope_cos;
   const float* rope_sin;
   const void* query;
-  float* scores;         // f32 [R][n_total]: written when probs is NULL (question scoring) or RH > 4
-  uint16_t* probs;  // fp16 exp(score - tile max), [R][n_slots]; NULL when only scores are needed
+  uint16_t* probs;  // fp16 exp(score - tile max) (decoding) or exp(score - quarter max) (question scoring)
   float* tile_max;
   float* tile_sum;
   float scaling;
@@ -76,12 +75,20 @@ DKV_DEVICE uint16_t f16_bits(float v) {
 
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
 
-// 8 consecutive query elements (idx a multiple of 8) as fp16, with one or two vector loads.
-DKV_DEVICE half8 load_query8(const void* q, long idx, int dtype) {
+// The query type as a compile-time tag: a kernel section instantiated per type issues its query
+// loads back to back, where a type switch around each load would make every load wait for the last.
+template <int T>
+struct QueryType {
+  static constexpr int value = T;
+};
+
+// 8 consecutive query elements (idx a multiple of 8) of type T as fp16.
+template <int T>
+DKV_DEVICE half8 load_query8_t(const void* q, long idx) {
   half8 r;
-  if (dtype == DKV_F16) {
+  if constexpr (T == DKV_F16) {
     r = *(const half8*)((const half_t*)q + idx);
-  } else if (dtype == DKV_BF16) {
+  } else if constexpr (T == DKV_BF16) {
     const uint4 v = *(const uint4*)((const uint16_t*)q + idx);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -90,12 +97,64 @@ DKV_DEVICE half8 load_query8(const void* q, long idx, int dtype) {
       r[2 * i + 1] = (half_t)__uint_as_float(w[i] & 0xffff0000u);
     }
   } else {
-    const float4 a = *(const float4*)((const float*)q + idx);
-    const float4 b = *(const float4*)((const float*)q + idx + 4);
-    r[0] = (half_t)a.x; r[1] = (half_t)a.y; r[2] = (half_t)a.z; r[3] = (half_t)a.w;
-    r[4] = (half_t)b.x; r[5] = (half_t)b.y; r[6] = (half_t)b.z; r[7] = (half_t)b.w;
+    const float4 x = *(const float4*)((const float*)q + idx);
+    const float4 y = *(const float4*)((const float*)q + idx + 4);
+    r[0] = (half_t)x.x; r[1] = (half_t)x.y; r[2] = (half_t)x.z; r[3] = (half_t)x.w;
+    r[4] = (half_t)y.x; r[5] = (half_t)y.y; r[6] = (half_t)y.z; r[7] = (half_t)y.w;
   }
   return r;
+}
+
+// One query element as the aligned 32-bit word that holds it: one unconditional load whatever the
+// type (a 16-bit tensor has an even element count, so the word never passes its end), converted
+// once the value is needed.
+DKV_DEVICE uint32_t load_query_word(const void* q, long idx, int dtype) {
+  return *(const uint32_t*)((const char*)q + (dtype == DKV_F32 ? idx * 4 : ((idx * 2) & ~3L)));
+}
+
+DKV_DEVICE float query_word_value(uint32_t w, long idx, int dtype) {
+  const uint16_t h = (uint16_t)(w >> ((idx & 1) * 16));
+  return dtype == DKV_F32 ? __uint_as_float(w) : dtype == DKV_BF16 ? bf16_bits_to_float(h) : half_bits_to_float(h);
+}
+
+// A query fragment as it travels from memory to the MFMA: fp16 and bf16 fragments stay raw
+// 16-byte words until they are used, so their loads can be waited for late; fp32 fragments (two
+// 16-byte loads) are converted when loaded.
+template <int T>
+struct QueryFrag {
+  using type = uint4;
+};
+template <>
+struct QueryFrag<DKV_F32> {
+  using type = half8;
+};
+
+template <int T>
+DKV_DEVICE typename QueryFrag<T>::type load_query_frag(const void* q, long idx) {
+  if constexpr (T == DKV_F32)
+    return load_query8_t<DKV_F32>(q, idx);
+  else
+    return *(const uint4*)((const uint16_t*)q + idx);
+}
+
+template <int T>
+DKV_DEVICE half8 query_frag_half(const typename QueryFrag<T>::type& f) {
+  if constexpr (T == DKV_F32) {
+    return f;
+  } else if constexpr (T == DKV_F16) {
+    half8 r;
+    __builtin_memcpy(&r, &f, 16);
+    return r;
+  } else {
+    half8 r;
+    const uint32_t w[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[2 * i] = (half_t)__uint_as_float(w[i] << 16);
+      r[2 * i + 1] = (half_t)__uint_as_float(w[i] & 0xffff0000u);
+    }
+    return r;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -146,18 +205,6 @@ DKV_DEVICE long prob_index(long row, long slot, int R_total) {
   return ((slot >> 4) * R_total + row) * 16 + (slot & 15);
 }
 
-// Where K2 writes the probability of (row, slot) when decoding: the value side's blocked layout.
-// Question scoring uses qprob_index.
-DKV_DEVICE long k2_prob_index(long row, long slot, int R_total, int ntiles, int rowmajor) {
-  return rowmajor ? row * ((long)ntiles * 256) + slot : prob_index(row, slot, R_total);
-}
-
-// Question scoring: row-major [R][ntiles * 256] with the tokens of each 64-token quarter q of a
-// tile interleaved in pairs: token q * 64 + h * 32 + j sits at position q * 64 + 2 j + h, so one
-// lane stores the pair (j, j + 32) of the MFMA output in 4 bytes.
-DKV_DEVICE long qprob_index(long row, int tile, int quarter, int j, int ntiles) {
-  return row * ((long)ntiles * 256) + (long)tile * 256 + quarter * 64 + 2 * j;
-}
 
 // ---------------------------------------------------------------------------
 // K1 (fp16 operand form): decode the hot key codes of every token into the
@@ -337,19 +384,17 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
                            (long)tile * kTileTok + n] = x[tb];
           continue;
         }
-        // fp32 scores only when no probability buffer is given; decoding reads only the probabilities
-        if (!a.probs && tb == lhi && n < count) a.scores[(long)(h * RH + r) * a.n_total + tok0 + n] = x[tb];
       }
       if constexpr (SPLIT) continue;
-      if constexpr (ROWMAJOR) {  // question scoring: this wave's quarter, written at once (see qprob_index)
+      if constexpr (ROWMAJOR) {  // question scoring: this wave's quarter (64 tokens), written at once
         const float mq = max32(fmaxf(x[0], x[1]));
         const float e0 = mq == -INFINITY ? 0.0f : __expf(x[0] - mq);
         const float e1 = mq == -INFINITY ? 0.0f : __expf(x[1] - mq);
         const float sq = sum32(e0 + e1);
         const long r_all = (long)h * RH + r;
-        if (lhi == 0)
-          *(uint32_t*)(a.probs + qprob_index(r_all, tile, tq, l32, a.ntiles)) =
-              (uint32_t)f16_bits(e0) | ((uint32_t)f16_bits(e1) << 16);
+        // lanes l32 and l32 + 32 hold both token blocks: each writes its own
+        a.probs[r_all * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + lhi * 32 + l32] =
+            f16_bits(lhi ? e1 : e0);
         if (lane == 0) {
           a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mq;
           a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sq;
@@ -402,8 +447,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       const float x = xs[hw][r][lhi];
       const float p = (x == -INFINITY) ? 0.0f : __expf(x - M);
       const int n = tq * 64 + lhi * 32 + l32;
-      a.probs[k2_prob_index((long)(h0 + hl) * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len, a.ntiles,
-                            ROWMAJOR)] = f16_bits(p);
+      a.probs[prob_index((long)(h0 + hl) * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len)] = f16_bits(p);
     }
   }
 }
@@ -425,7 +469,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __shared__ __attribute__((aligned(16))) half_t lds[2 * 2 * kTileTok * kStride];
   __shared__ float stat_m[HPW][4][32];
   __shared__ float stat_s[HPW][4][32];
-  __shared__ int pos_s[kTileTok];                  // the tile's RoPE positions (decode epilogue)
+  __shared__ int pos_s[kTileTok];                  // the tile's RoPE positions
   __shared__ float q_s[HPW * kSmallRows * D];      // the workgroup's query rows (decode epilogue)
 
   const int bid = blockIdx.x;
@@ -451,9 +495,10 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const int RH = (a.Hq / a.Hkv) * a.q_len;
 
-  // the decode epilogue's positions and query rows are fetched now, behind the main loop
+  // the epilogue's positions (clamped into the RoPE tables; past the tile's end, its last token's)
+  // and the decode epilogue's query rows are fetched now, behind the main loop
+  if (tid < kTileTok) pos_s[tid] = min(max(a.positions[tok0 + min(tid, count - 1)], 0), a.rope_rows - 1);
   if constexpr (SMALL) {
-    if (tid < kTileTok) pos_s[tid] = min(max(a.positions[tok0 + min(tid, count - 1)], 0), a.rope_rows - 1);
     const int gq = a.Hq / a.Hkv;
     for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
       const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
@@ -592,30 +637,40 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     return;
   } else {
 
-  // ---- epilogue 1 (many query rows): RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8]
+  // ---- epilogue 1 (many query rows): RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8].
+  // Positions come from LDS (clamped to the tile's last token past its end), so every RoPE load
+  // is unconditional and the compiler can keep several in flight.
   half_t* Kl = lds;
 #pragma unroll
   for (int tb = 0; tb < 2; ++tb) {
     const int n = tq * 64 + tb * 32 + l32;
-    const bool valid = n < count;
-    const int pos = valid ? min(max(a.positions[tok0 + n], 0), a.rope_rows - 1) : 0;
-    const float* cosr = a.rope_cos + (long)pos * half_d;
-    const float* sinr = a.rope_sin + (long)pos * half_d;
+    const long pos = pos_s[n];
+    const float* cosr = a.rope_cos + pos * half_d;
+    const float* sinr = a.rope_sin + pos * half_d;
+    // the token's cos / sin values for both rotated row blocks, all loads issued before any use
+    float4 c[2][4], sv4[2][4];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0, i = 0; rb < 4; ++rb) {
+      if ((rb % DB) >= HALF_BLK) continue;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
+        c[i][v4] = *(const float4*)(cosr + d0);
+        sv4[i][v4] = *(const float4*)(sinr + d0);
+      }
+      ++i;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int rb = 0, i = 0; rb < 4; ++rb) {
       if ((rb % DB) >= HALF_BLK) continue;
       const int rb2 = rb + HALF_BLK;
       const int hl = hs * (128 / D) + rb / DB;
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
         const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
-        float4 c = make_float4(1.f, 1.f, 1.f, 1.f), s = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (valid) {
-          c = *(const float4*)(cosr + d0);
-          s = *(const float4*)(sinr + d0);
-        }
-        const float cv[4] = {c.x, c.y, c.z, c.w};
-        const float sv[4] = {s.x, s.y, s.z, s.w};
+        const float cv[4] = {c[i][v4].x, c[i][v4].y, c[i][v4].z, c[i][v4].w};
+        const float sv[4] = {sv4[i][v4].x, sv4[i][v4].y, sv4[i][v4].z, sv4[i][v4].w};
         half4 lo, hi;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -627,121 +682,182 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         *(half4*)(Kl + (hl * kTileTok + n) * KSTR + d0) = lo;
         *(half4*)(Kl + (hl * kTileTok + n) * KSTR + d0 + half_d) = hi;
       }
+      ++i;
     }
   }
   __syncthreads();
 
-  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block; the block's scores stay
-  // in registers until the tile maxima are known, then become fp16 probabilities relative to
-  // them (and fp32 scores only when no probability buffer is given).
+  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block.  The key fragments of a
+  // head and this wave's 64 tokens serve every row block, so they are read from LDS once per head;
+  // the query fragments of a row block are loaded together (rows past the end read the last row,
+  // whose scores are discarded), in the query's own type.
   const int mblocks = (RH + 31) / 32;
   constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in this phase
-  for (int mb = 0; mb < mblocks; ++mb) {
-    float xs[HPWAVE][16][2];
+  constexpr int KS = D / 16;       // MFMA k-steps over the head dimension
+  auto key_frags = [&](half8 (&kf)[KS][2], int hl) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+        kf[ks][tb] = lds_half8(Kl + (hl * kTileTok + tq * 64 + tb * 32 + l32) * KSTR + ks * 16 + lhi * 8);
+  };
+  // the query fragments of row block mb of head h (rows past the end read the last row)
+  auto load_queries = [&](auto qtype, auto (&qf)[KS], int h, int mb) {
+    constexpr int QT = decltype(qtype)::value;
+    const int r = min(mb * 32 + l32, RH - 1);
+    const int qh = h * gq + r / a.q_len, qi = r % a.q_len;
+    const long qbase = (((long)b * a.Hq + qh) * a.q_len + qi) * D + lhi * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = load_query_frag<QT>(a.query, qbase + ks * 16);
+  };
+  // sacc[tb][v] = q . k for token tq*64 + tb*32 + l32 and row mb*32 + 8*(v/4) + 4*lhi + (v&3), or,
+  // with the operands exchanged (TOKENS_IN_V), for token tq*64 + tb*32 + 8*(v/4) + 4*lhi + (v&3) and
+  // row mb*32 + l32
+  auto block_mfma = [&](auto qtype, auto tokens_in_v, floatx16 (&sacc)[2], const half8 (&kf)[KS][2],
+                        const auto (&qf)[KS]) {
+    constexpr int QT = decltype(qtype)::value;
+    constexpr bool TOKENS_IN_V = decltype(tokens_in_v)::value;
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sacc[tb][v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const half8 q8 = query_frag_half<QT>(qf[ks]);
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) {
+        if constexpr (TOKENS_IN_V)
+          sacc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks][tb], q8, sacc[tb], 0, 0, 0);
+        else
+          sacc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(q8, kf[ks][tb], sacc[tb], 0, 0, 0);
+      }
+    }
+  };
+
+  // question scoring: probabilities relative to this wave's 64 tokens (a tile quarter) and the
+  // quarter's (max, sum), written at once: no exchange between waves, so heads and row blocks run in
+  // any order (heads outer: one head's key fragments in registers at a time).  The scores come with
+  // the tokens in the accumulator registers and the rows across the lanes, so a row's quarter
+  // statistics are 32 values in the lane and one exchange with lane l32 + 32.
+  auto row_blocks_quarters = [&](auto qtype) {
+    using QF = typename QueryFrag<decltype(qtype)::value>::type;
 #pragma unroll
     for (int hh = 0; hh < HPWAVE; ++hh) {
       const int hl = hs * HPWAVE + hh;
       const int h = h0 + hl;
-      floatx16 sacc[2];
+      half8 kf[KS][2];
+      key_frags(kf, hl);
+      auto quarter = [&](const QF (&qf)[KS], int mb) {
+        floatx16 sacc[2];
+        block_mfma(qtype, QueryType<1>{}, sacc, kf, qf);
+        float mx = -INFINITY;
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[tb][v] = 0.0f;
-      const int r = mb * 32 + l32;
-      const bool rvalid = r < RH;
-      const int qh = h * gq + (rvalid ? r / a.q_len : 0);
-      const int qi = rvalid ? r % a.q_len : 0;
-      const long qbase = (((long)b * a.Hq + qh) * a.q_len + qi) * D;
+          for (int v = 0; v < 16; ++v) {
+            const int n = tq * 64 + tb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+            sacc[tb][v] = n < count ? sacc[tb][v] * a.scaling : -INFINITY;
+            mx = fmaxf(mx, sacc[tb][v]);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        float sm = 0.0f;
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-        const int kof = ks * 16 + lhi * 8;
-        half8 qa;
-        if (rvalid) {
-          qa = load_query8(a.query, qbase + kof, a.query_dtype);
-        } else {
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) qa[i] = (half_t)0.0f;
-        }
+          for (int v = 0; v < 16; ++v) {
+            sacc[tb][v] = mx == -INFINITY ? 0.0f : __expf(sacc[tb][v] - mx);
+            sm += sacc[tb][v];
+          }
+        sm += __shfl_xor(sm, 32);
+        // Every store is unconditional, so the compiler knows how many are in flight and the next
+        // block's query loads are waited for without waiting for these stores.  Lanes of rows past
+        // the end computed row RH - 1 from the same query and key bits, so they store the same
+        // bytes there; lanes l32 and l32 + 32 store the same statistics.
+        const long r_all = (long)h * RH + min(mb * 32 + l32, RH - 1);
+        // tokens 8 j + 4 lhi .. + 3 of each 32-token block: 8 bytes per store
+        uint16_t* dst = a.probs + r_all * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + 4 * lhi;
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-          const half8 kb = lds_half8(Kl + (hl * kTileTok + tq * 64 + tb * 32 + l32) * KSTR + kof);
-          sacc[tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(qa, kb, sacc[tb], 0, 0, 0);
-        }
+        for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            *(uint2*)(dst + tb * 32 + 8 * j) =
+                make_uint2((uint32_t)f16_bits(sacc[tb][4 * j]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 1]) << 16),
+                           (uint32_t)f16_bits(sacc[tb][4 * j + 2]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 3]) << 16));
+        a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mx;
+        a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sm;
+      };
+      // two query buffers: the next row block's fragments load while this block's MFMAs run
+      QF qa[KS], qb[KS];
+      load_queries(qtype, qa, h, 0);
+      for (int mb = 0; mb < mblocks; mb += 2) {
+        load_queries(qtype, qb, h, min(mb + 1, mblocks - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        quarter(qa, mb);
+        if (mb + 1 >= mblocks) break;
+        load_queries(qtype, qa, h, min(mb + 2, mblocks - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        quarter(qb, mb + 1);
       }
-      // sacc[tb][v]: token tq*64 + tb*32 + l32, row mb*32 + 8*(v/4) + 4*lhi + (v&3)
-      if constexpr (ROWMAJOR) {
-        // question scoring: probabilities relative to this wave's 64 tokens (a tile quarter) and the
-        // quarter's (max, sum), written at once: no exchange between waves
+    }
+  };
+
+  // decoding many rows: the four waves of a head exchange their quarters' statistics per row block,
+  // then write probabilities relative to the tile maximum in the value side's layout
+  auto row_blocks = [&](auto qtype) {
+    half8 kf[HPWAVE][KS][2];
+#pragma unroll
+    for (int hh = 0; hh < HPWAVE; ++hh) key_frags(kf[hh], hs * HPWAVE + hh);
+    for (int mb = 0; mb < mblocks; ++mb) {
+      float xs[HPWAVE][16][2];
+#pragma unroll
+      for (int hh = 0; hh < HPWAVE; ++hh) {
+        const int hl = hs * HPWAVE + hh;
+        typename QueryFrag<decltype(qtype)::value>::type qf[KS];
+        load_queries(qtype, qf, h0 + hl, mb);
+        __builtin_amdgcn_sched_barrier(0);
+        floatx16 sacc[2];
+        block_mfma(qtype, QueryType<0>{}, sacc, kf[hh], qf);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int row = mb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-          float x[2];
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb) {
             const int n = tq * 64 + tb * 32 + l32;
-            x[tb] = (row < RH) && (n < count) ? sacc[tb][v] * a.scaling : -INFINITY;
+            xs[hh][v][tb] = (row < RH) && (n < count) ? sacc[tb][v] * a.scaling : -INFINITY;
           }
-          const float mx = max32(fmaxf(x[0], x[1]));
-          const float e0 = mx == -INFINITY ? 0.0f : __expf(x[0] - mx);
-          const float e1 = mx == -INFINITY ? 0.0f : __expf(x[1] - mx);
-          const float sm = sum32(e0 + e1);
-          if (row < RH) {
-            const long r_all = (long)h * RH + row;
-            const uint32_t pair = (uint32_t)f16_bits(e0) | ((uint32_t)f16_bits(e1) << 16);
-            *(uint32_t*)(a.probs + qprob_index(r_all, tile, tq, l32, a.ntiles)) = pair;
-            if (l32 == 0) {
-              a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mx;
-              a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sm;
+          const float mx = max32(fmaxf(xs[hh][v][0], xs[hh][v][1]));
+          float sm = 0.0f;
+          if (mx != -INFINITY) sm = __expf(xs[hh][v][0] - mx) + __expf(xs[hh][v][1] - mx);
+          sm = sum32(sm);
+          if (l32 == 0) {
+            const int rr = 8 * (v >> 2) + 4 * lhi + (v & 3);
+            stat_m[hl][tq][rr] = mx;
+            stat_s[hl][tq][rr] = sm;
+          }
+        }
+      }
+      __syncthreads();
+      if (tid < HPW * 32) {
+        const int hl = tid >> 5, rr = tid & 31;
+        const int row = mb * 32 + rr;
+        if (row < RH) {
+          float M = -INFINITY;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
+          float S = 0.0f;
+          if (M != -INFINITY) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float mq = stat_m[hl][q][rr];
+              if (mq != -INFINITY) S += stat_s[hl][q][rr] * __expf(mq - M);
             }
           }
-        }
-        continue;
-      }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = mb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-          const int n = tq * 64 + tb * 32 + l32;
-          const bool ok = (row < RH) && (n < count);
-          xs[hh][v][tb] = ok ? sacc[tb][v] * a.scaling : -INFINITY;
-          if (ok && !a.probs) a.scores[(long)(h * RH + row) * a.n_total + tok0 + n] = xs[hh][v][tb];
-        }
-        const float mx = max32(fmaxf(xs[hh][v][0], xs[hh][v][1]));
-        float sm = 0.0f;
-        if (mx != -INFINITY) sm = __expf(xs[hh][v][0] - mx) + __expf(xs[hh][v][1] - mx);
-        sm = sum32(sm);
-        if (l32 == 0) {
-          const int rr = 8 * (v >> 2) + 4 * lhi + (v & 3);
-          stat_m[hl][tq][rr] = mx;
-          stat_s[hl][tq][rr] = sm;
+          const long o = (long)((h0 + hl) * RH + row) * a.ntiles + tile;
+          a.tile_max[o] = M;
+          a.tile_sum[o] = S;
         }
       }
-    }
-    if constexpr (ROWMAJOR) continue;  // question scoring wrote everything above
-    __syncthreads();
-    if (tid < HPW * 32) {
-      const int hl = tid >> 5, rr = tid & 31;
-      const int row = mb * 32 + rr;
-      if (row < RH) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) M = fmaxf(M, stat_m[hl][q][rr]);
-        float S = 0.0f;
-        if (M != -INFINITY) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float mq = stat_m[hl][q][rr];
-            if (mq != -INFINITY) S += stat_s[hl][q][rr] * __expf(mq - M);
-          }
-        }
-        const long o = (long)((h0 + hl) * RH + row) * a.ntiles + tile;
-        a.tile_max[o] = M;
-        a.tile_sum[o] = S;
-      }
-    }
-    // probabilities relative to the tile maximum (fp16), from the registers; 0 past the tokens
-    if (a.probs) {
+      // probabilities relative to the tile maximum (fp16), from the registers; 0 past the tokens
 #pragma unroll
       for (int hh = 0; hh < HPWAVE; ++hh) {
         const int hl = hs * HPWAVE + hh;
@@ -758,13 +874,28 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
           for (int tb = 0; tb < 2; ++tb) {
             const float x = xs[hh][v][tb];
             const int n = tq * 64 + tb * 32 + l32;
-            a.probs[k2_prob_index(r_all, (long)tile * kTileTok + n, a.Hq * a.q_len, a.ntiles, ROWMAJOR)] =
+            a.probs[prob_index(r_all, (long)tile * kTileTok + n, a.Hq * a.q_len)] =
                 f16_bits(x == -INFINITY ? 0.0f : __expf(x - M));
           }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
+  };
+  if constexpr (ROWMAJOR) {
+    if (a.query_dtype == DKV_F16)
+      row_blocks_quarters(QueryType<DKV_F16>{});
+    else if (a.query_dtype == DKV_BF16)
+      row_blocks_quarters(QueryType<DKV_BF16>{});
+    else
+      row_blocks_quarters(QueryType<DKV_F32>{});
+  } else {
+    if (a.query_dtype == DKV_F16)
+      row_blocks(QueryType<DKV_F16>{});
+    else if (a.query_dtype == DKV_BF16)
+      row_blocks(QueryType<DKV_BF16>{});
+    else
+      row_blocks(QueryType<DKV_F32>{});
   }
   }
 }
@@ -851,11 +982,9 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
       s4[k] = ts[t];
     }
   }
-  // the query element as the aligned 32-bit word that holds it (one load whatever the dtype; a
-  // 16-bit tensor has an even element count, so the word never passes its end), converted later
+  // the query element, converted later
   const long qidx = (((long)b * a.Hq + qh) * a.q_len + qi) * D + d;
-  const uint32_t qword = *(const uint32_t*)((const char*)a.query +
-                                            (a.query_dtype == DKV_F32 ? qidx * 4 : ((qidx * 2) & ~3L)));
+  const uint32_t qword = load_query_word(a.query, qidx, a.query_dtype);
   const int kj = tid >> 2, ks = tid & 3;
   const bool kslice = ks * 32 < D;
   float4 k4[8];
@@ -898,11 +1027,7 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
       if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
     for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
   }
-  if (tid < D) {
-    const uint16_t q16 = (uint16_t)(qword >> ((qidx & 1) * 16));
-    q[tid] = a.query_dtype == DKV_F32 ? __uint_as_float(qword)
-           : a.query_dtype == DKV_BF16 ? bf16_bits_to_float(q16) : half_bits_to_float(q16);
-  }
+  if (tid < D) q[tid] = query_word_value(qword, qidx, a.query_dtype);
   if (wave == 0) {
     const float m = wave_max(mm);
     const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
@@ -1005,21 +1130,6 @@ struct K3aArgs {
   float* w_part;
   int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
 };
-
-// Max over a sequence's tiles of one row, 8 lanes per row (all loads of a lane issued together).
-DKV_DEVICE float rows_max8(const float* tile_max, int ntiles, int tb0, int ntb, int row, bool ok, int sub) {
-  float m = -INFINITY;
-  if (ok) {
-    const float* tm = tile_max + (long)row * ntiles + tb0;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = tm[min(sub + 8 * i, ntb - 1)];  // unconditional: issued together
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, sub + 8 * i < ntb ? v[i] : -INFINITY);
-    for (int t = sub + 64; t < ntb; t += 8) m = fmaxf(m, tm[t]);
-  }
-  return max8(m);
-}
 
 // ---------------------------------------------------------------------------
 // K1 for the value side: every token's value codes (all hot planes) as 8-bit
@@ -1211,9 +1321,20 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   const int my_row = rbk * 32 + l32;
   const bool row_ok = my_row < a.R_total;
 
-  // every global load of the wave goes out first: the affine pairs of its 128 tokens (one
-  // 16-byte load per lane, staged in LDS for the broadcast reads), its probability rows and
-  // value codes for all 8 steps; the row maxima come from the tile statistics meanwhile.
+  // every global load of the wave goes out first, unconditionally (clamped indices): the tile
+  // maxima of the block's rows (small, so they return first and the row maxima are known while
+  // the bulk is in flight), this wave's tile maximum, then the affine pairs of its 128 tokens
+  // (one 16-byte load per lane, staged in LDS for the broadcast reads), its probability rows and
+  // value codes for all 8 steps.
+  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
+  const int mrow = rbk * 32 + ((tid >> 3) & 31), msub = tid & 7;  // 8 lanes per row (waves 4-7 repeat 0-3)
+  const float* tmrow = a.tile_max + (long)min(mrow, a.R_total - 1) * a.ntiles + tb0;
+  float tmv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) tmv[i] = tmrow[min(msub + 8 * i, ntb - 1)];
+  // this wave's 128 tokens lie in one tile; its maximum for this lane's row
+  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
+  const float mt_raw = a.tile_max[(long)min(my_row, a.R_total - 1) * a.ntiles + tile];
   const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
   const float4 aff2 = *(const float4*)(aff + wt0 + 2 * lane);
   // step st covers slots slot0 + wt0 + 16 st .. +16 (one 16-slot block): the wave's probability
@@ -1230,10 +1351,8 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     c0[st] = *(const uint2*)(col0 + st * 64 * 16);
     c1[st] = *(const uint2*)(col1 + st * 64 * 16);
   }
-  // this wave's 128 tokens lie in one tile; its maximum for this lane's row (read now, used once
-  // the row maxima are known)
-  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
-  const float mt = (row_ok && wt0 < count) ? a.tile_max[(long)my_row * a.ntiles + tile] : -INFINITY;
+  __builtin_amdgcn_sched_barrier(0);
+  const float mt = (row_ok && wt0 < count) ? mt_raw : -INFINITY;
   // Power-of-two operand scaling.  scale = span / 256 of a low-variance group (about 6e-5 at
   // rank 2048) puts p * scale among fp16's subnormals, which keep only a few significant bits.
   // p <= 1, so scaling the wave's scales by the 2^e that brings their maximum into [2^14, 2^15)
@@ -1249,11 +1368,13 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   }
   const float sup = ldexpf(1.0f, sexp), sdown = ldexpf(1.0f, -sexp);
   *(float4*)&saff[wave][2 * lane] = make_float4(aff2.x * sup, aff2.y, aff2.z * sup, aff2.w);
-  if (tid < 256) {
-    const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
-    const int r = rbk * 32 + (tid >> 3);
-    const float m = rows_max8(a.tile_max, a.ntiles, tb0, ntb, r, r < a.R_total, tid & 7);
-    if ((tid & 7) == 0) Mrow[tid >> 3] = m;
+  {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, msub + 8 * i < ntb ? tmv[i] : -INFINITY);
+    for (int t = msub + 64; t < ntb; t += 8) m = fmaxf(m, tmrow[t]);  // sequences of more than 64 tiles
+    m = max8(m);
+    if (tid < 256 && msub == 0) Mrow[tid >> 3] = mrow < a.R_total ? m : -INFINITY;
   }
   __syncthreads();
   const float my_M = Mrow[l32];
@@ -1425,7 +1546,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RowMergeArgs a) 
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
   int ksplit;
-  size_t coef, vcodes, vaff, scores, probs, tile_max, tile_sum, w_part, out_part, split_scores,
+  size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, split_scores,
       total;
 };
 
@@ -1444,7 +1565,7 @@ inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
   return k;
 }
 
-// Workspace: [decoded key coefficients][decoded value codes][value affine][scores][tile statistics]
+// Workspace: [decoded key coefficients][decoded value codes][value affine][probabilities][tile statistics]
 // [split partials][chunk partials][K2 rank-slice partial scores].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
@@ -1467,8 +1588,6 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)L.n_slots * a->rank);
   L.vaff = off;
   off += align256((size_t)L.n_slots * (a->rank / 64) * 8);
-  L.scores = off;
-  off += align256((size_t)L.R_total * L.n_total * 4);
   L.probs = off;
   off += align256((size_t)L.R_total * L.n_slots * 2);
   L.tile_max = off;
@@ -1528,7 +1647,6 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.rope_sin = a->rope_sin;
   k.rope_rows = a->rope_rows;
   k.query = a->query;
-  k.scores = (float*)(ws + L.scores);
   k.probs = (uint16_t*)(ws + L.probs);
   k.sub_max = sub_max;
   k.sub_sum = sub_sum;
@@ -1620,8 +1738,8 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   const Layout L = make_layout(a);
   // only the decoded areas at the head of the workspace are written, so an attend or a score
   // workspace (both start with them) will do
-  DKV_REQUIRE(workspace && workspace_bytes >= L.scores, DKV_EWORKSPACE,
-              "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.scores);
+  DKV_REQUIRE(workspace && workspace_bytes >= L.probs, DKV_EWORKSPACE,
+              "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.probs);
   DecodeArgs d{};
   d.s = a->key;
   d.cu_seqlens = a->cu_seqlens;
@@ -1781,12 +1899,12 @@ extern "C" int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, siz
 // K4a: question scoring of the hot tier (scripts/progressive.py:239-254 with
 // scripts/dimmer.py:52-66).  Per layer: K2 scores every (query head, query
 // position) row against the compressed keys and writes fp16 probabilities
-// relative to each tile's maximum (row-major) with the tiles' softmax
-// statistics; row_stats merges those statistics with the exact context tokens
-// and the question's own keys (causal) into the row's maximum M and sum L, and
-// writes each tile's factor exp(tile max - M) / L; importance adds
-// sum over rows of probability * factor to every token, in a fixed order, so
-// results do not depend on scheduling.
+// relative to the maximum of each 64-token tile quarter (row-major) with the
+// quarters' softmax statistics; row_stats merges those statistics with the
+// exact context tokens and the question's own keys (causal) into the row's
+// maximum M and sum L; importance adds, to every token, the sum over rows of
+// probability * exp(quarter max - M) / L, in a fixed order, so results do not
+// depend on scheduling.
 // ===========================================================================
 namespace {
 
@@ -1797,133 +1915,182 @@ struct RowStatsArgs {
   const float* sub_max;       // [R_total][nsub] (compressed part per 64-token tile quarter, from K2)
   const float* sub_sum;
   float* stat;                // [R_total][2]: softmax maximum M and 1 / L over every key of the row
-  float* fac;                 // [R_total][nsub]: exp(quarter max - M) / L, the quarter's probability factor
   float scaling;
-  int Hkv, Hq, q_len, D, E, query_dtype, nsub;
+  int Hkv, Hq, q_len, E, query_dtype, nsub;
 };
 
-constexpr int kStatKeysPerThread = 16;  // keys per thread kept in registers (more are recomputed)
+constexpr int kStatThreads = 256;
+constexpr int kStatWaves = kStatThreads / 64;
+constexpr int kStatKeys = kStatThreads / 2;  // exact keys scored per pass: two lanes per key
+constexpr int kStatBatch = 4;                // quarter statistics per thread whose loads go out together
 
-// One workgroup per (query head, query position) row: the softmax statistics over the
-// compressed tokens (merged from K2's per-tile maxima and sums), the exact context tokens and
-// the question's own keys up to this position (causal).
-__global__ __launch_bounds__(128) void row_stats_kernel(RowStatsArgs a) {
-  __shared__ float q[128];
-  __shared__ float red[2][2];
+// The (max, sum exp) of a batch of quarter statistics (-inf maxima and entries past nsub skipped),
+// merged into (mc, lc).
+DKV_DEVICE void merge_quarters(const float (&mt)[kStatBatch], const float (&st)[kStatBatch], int first, int stride,
+                               int nsub, float& mc, float& lc) {
+  float bm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kStatBatch; ++i) bm = first + i * stride < nsub ? fmaxf(bm, mt[i]) : bm;
+  if (bm == -INFINITY) return;
+  float bs = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kStatBatch; ++i) {
+    const bool live = first + i * stride < nsub && mt[i] != -INFINITY;
+    bs += live ? st[i] * __expf(mt[i] - bm) : 0.0f;
+  }
+  if (bm > mc) {
+    lc = (mc == -INFINITY ? 0.0f : lc * __expf(mc - bm)) + bs;
+    mc = bm;
+  } else {
+    lc += bs * __expf(bm - mc);
+  }
+}
+
+// One workgroup per (query head, query position) row: the softmax statistics over the compressed
+// tokens (merged from K2's per-quarter maxima and sums), the exact context tokens and the
+// question's own keys up to this position (causal).  Every global load of the first round (the
+// thread's quarter statistics, the query element, the first pass of exact keys) is unconditional
+// and goes out before any is used.  Lanes 2 k and 2 k + 1 score key k of a pass, each over half of
+// the head dimension.
+template <int D>
+__global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a) {
+  constexpr int U = D / 8;  // float4 per lane: half a key row
+  __shared__ __attribute__((aligned(16))) float q[D];
+  __shared__ float red[2][kStatWaves];
   const int row = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kj = tid >> 1, kh = tid & 1;
   const int gq = a.Hq / a.Hkv;
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
-  const int D = a.D;
-  if (tid < D) q[tid] = load_as_float(a.query, ((long)qh * a.q_len + qi) * D + tid, a.query_dtype);
-  // compressed part: online merge of this thread's tiles
-  float mc = -INFINITY, lc = 0.0f;
-  for (int t = tid; t < a.nsub; t += 128) {
-    const float mt = a.sub_max[(long)row * a.nsub + t], st = a.sub_sum[(long)row * a.nsub + t];
-    if (mt == -INFINITY) continue;
-    if (mt > mc) {
-      lc = lc * __expf(mc - mt) + st;
-      mc = mt;
-    } else {
-      lc += st * __expf(mt - mc);
-    }
-  }
-  __syncthreads();
   const int nkeys = a.E + qi + 1;  // exact context tokens + question keys 0..qi
-  float dots[kStatKeysPerThread];
-  float me = -INFINITY;
-  for (int k = 0, j = tid; j < nkeys; ++k, j += 128) {
-    const float4* kr = (const float4*)(j < a.E ? a.key_exact + ((long)h * a.E + j) * D
-                                               : a.key_question + ((long)h * a.q_len + (j - a.E)) * D);
-    float dot = 0.0f;
-    for (int i = 0; i < D / 4; i += 8) {
-      float4 k4[8];
+  const float* smax = a.sub_max + (long)row * a.nsub;
+  const float* ssum = a.sub_sum + (long)row * a.nsub;
+  auto key_half = [&](int j) {
+    return (const float4*)(j < a.E ? a.key_exact + ((long)h * a.E + j) * D
+                                   : a.key_question + ((long)h * a.q_len + (j - a.E)) * D) + kh * U;
+  };
+  float mt[kStatBatch], st[kStatBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) k4[u] = kr[i + u];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        dot += q[4 * (i + u)] * k4[u].x + q[4 * (i + u) + 1] * k4[u].y + q[4 * (i + u) + 2] * k4[u].z +
-               q[4 * (i + u) + 3] * k4[u].w;
-    }
-    dot *= a.scaling;
-    if (k < kStatKeysPerThread) dots[k] = dot;
-    me = fmaxf(me, dot);
+  for (int i = 0; i < kStatBatch; ++i) {
+    const int t = min(tid + i * kStatThreads, a.nsub - 1);
+    mt[i] = smax[t];
+    st[i] = ssum[t];
   }
-  // joint maximum over both parts, then the sum of exponentials
+  const long qidx = ((long)qh * a.q_len + qi) * D + min(tid, D - 1);
+  const uint32_t qword = load_query_word(a.query, qidx, a.query_dtype);
+  float4 k4[U];
+  {
+    const float4* kr = key_half(min(kj, nkeys - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // compressed part
+  float mc = -INFINITY, lc = 0.0f;
+  merge_quarters(mt, st, tid, kStatThreads, a.nsub, mc, lc);
+  for (int t0 = kStatThreads * kStatBatch; t0 < a.nsub; t0 += kStatThreads * kStatBatch) {  // long contexts
+#pragma unroll
+    for (int i = 0; i < kStatBatch; ++i) {
+      const int t = min(t0 + tid + i * kStatThreads, a.nsub - 1);
+      mt[i] = smax[t];
+      st[i] = ssum[t];
+    }
+    merge_quarters(mt, st, t0 + tid, kStatThreads, a.nsub, mc, lc);
+  }
+  if (tid < D) q[tid] = query_word_value(qword, qidx, a.query_dtype);
+  __syncthreads();
+  auto score = [&]() {  // both lanes of the pair return the key's scaled score
+    float dot = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float4 q4 = *(const float4*)&q[kh * (D / 2) + 4 * u];
+      dot += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+    }
+    return (dot + __shfl_xor(dot, 1)) * a.scaling;
+  };
+  const float first = score();
+  float me = kj < nkeys ? first : -INFINITY;
+  for (int j0 = kStatKeys; j0 < nkeys; j0 += kStatKeys) {  // more exact keys than one pass holds
+    const float4* kr = key_half(min(j0 + kj, nkeys - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+    const float sc = score();
+    me = j0 + kj < nkeys ? fmaxf(me, sc) : me;
+  }
+  // joint maximum over both parts, then the sum of exponentials (each key counted by its even lane)
   float m = fmaxf(me, mc);
   m = wave_max(m);
   if (lane == 0) red[0][wave] = m;
   __syncthreads();
-  const float M = fmaxf(red[0][0], red[0][1]);
+  float M = red[0][0];
+#pragma unroll
+  for (int w = 1; w < kStatWaves; ++w) M = fmaxf(M, red[0][w]);
   float l = (mc == -INFINITY || M == -INFINITY) ? 0.0f : lc * __expf(mc - M);
-  for (int k = 0, j = tid; j < nkeys; ++k, j += 128) {
-    float dot;
-    if (k < kStatKeysPerThread) {
-      dot = dots[k];
-    } else {
-      const float* kr = j < a.E ? a.key_exact + ((long)h * a.E + j) * D
-                                : a.key_question + ((long)h * a.q_len + (j - a.E)) * D;
-      dot = 0.0f;
-      for (int d = 0; d < D; ++d) dot += q[d] * kr[d];
-      dot *= a.scaling;
-    }
-    l += __expf(dot - M);
+  l += kh == 0 && kj < nkeys ? __expf(first - M) : 0.0f;
+  for (int j0 = kStatKeys; j0 < nkeys; j0 += kStatKeys) {
+    const float4* kr = key_half(min(j0 + kj, nkeys - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+    const float sc = score();
+    l += kh == 0 && j0 + kj < nkeys ? __expf(sc - M) : 0.0f;
   }
   l = wave_sum(l);
   if (lane == 0) red[1][wave] = l;
   __syncthreads();
-  const float L = red[1][0] + red[1][1];
-  const float invL = L > 0.0f ? 1.0f / L : 0.0f;
   if (tid == 0) {
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kStatWaves; ++w) L += red[1][w];
     a.stat[2 * row] = M;
-    a.stat[2 * row + 1] = invL;
-  }
-  // p = exp(s - M) / L = exp(s - quarter max) * fac: K2 wrote the first factor, the importance
-  // kernel applies the second
-  for (int t = tid; t < a.nsub; t += 128) {
-    const float mt = a.sub_max[(long)row * a.nsub + t];
-    a.fac[(long)row * a.nsub + t] = (mt == -INFINITY || M == -INFINITY) ? 0.0f : __expf(mt - M) * invL;
+    a.stat[2 * row + 1] = L > 0.0f ? 1.0f / L : 0.0f;
   }
 }
 
-// importance[t] += sum over rows r of probs[r][t] * fac[r][quarter of t]: one workgroup per 64-token
-// tile quarter.  Lane (row lane rl = lane / 8, position chunk tc = lane % 8) of wave w reads 8
-// positions (16 B) of rows w * 8 + rl, + 32, + 64, ...; the row lanes, then the waves, are summed in
-// a fixed order, so the result does not depend on scheduling.  Position 2 j + h of the quarter holds
-// token h * 32 + j (qprob_index).
+// importance[t] += sum over rows r of p = exp(s - M_r) / L_r = probs[r][t] * exp(quarter max - M_r)
+// / L_r: one workgroup per 64-token tile quarter.  Lane (row lane rl = lane / 8, token chunk
+// tc = lane % 8) of wave w reads 8 tokens (16 B) of rows w * 8 + rl, + 64, + 128, ...; the row
+// lanes, then the waves, are summed in a fixed order, so the result does not depend on scheduling.
 struct ImportanceArgs {
   const uint16_t* probs;  // fp16 [R_total][ntiles * 256], relative to each quarter's maximum (K2)
-  const float* fac;       // [R_total][ntiles * 4] (row_stats_kernel)
+  const float* sub_max;   // [R_total][ntiles * 4] quarter maxima (K2)
+  const float* stat;      // [R_total][2]: M and 1 / L (row_stats_kernel)
   float* importance;      // [n]
   int R_total, n, ntiles;
 };
 
-constexpr int kImpBatch = 8;  // row iterations whose loads go out together
+constexpr int kImpThreads = 512;
+constexpr int kImpWaves = kImpThreads / 64;
+constexpr int kImpBatch = 12;  // row iterations whose loads go out together
 
-__global__ __launch_bounds__(256) void importance_kernel(ImportanceArgs a) {
-  __shared__ float part[4][64];
+__global__ __launch_bounds__(kImpThreads) void importance_kernel(ImportanceArgs a) {
+  __shared__ float part[kImpWaves][64];
   const int sub = blockIdx.x;  // tile quarter: tile sub / 4, quarter sub % 4
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rl = lane >> 3, tc = lane & 7;
   const long pos = (long)sub * 64 + tc * 8;
   const long pstride = (long)a.ntiles * kTileTok;
   const int nsub = a.ntiles * 4;
+  constexpr int kRowStep = kImpWaves * 8;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int r0 = wave * 8 + rl; r0 < a.R_total; r0 += 32 * kImpBatch) {
+  for (int r0 = wave * 8 + rl; r0 < a.R_total; r0 += kRowStep * kImpBatch) {
     uint4 pv[kImpBatch];
-    float fv[kImpBatch];
+    float mq[kImpBatch];
+    float2 ml[kImpBatch];
 #pragma unroll
     for (int k = 0; k < kImpBatch; ++k) {  // clamped rows: every load is unconditional
-      const int r = min(r0 + 32 * k, a.R_total - 1);
+      const int r = min(r0 + kRowStep * k, a.R_total - 1);
       pv[k] = *(const uint4*)(a.probs + (long)r * pstride + pos);
-      fv[k] = a.fac[(long)r * nsub + sub];
+      mq[k] = a.sub_max[(long)r * nsub + sub];
+      ml[k] = *(const float2*)(a.stat + 2 * r);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch goes out before the first is used
 #pragma unroll
     for (int k = 0; k < kImpBatch; ++k) {
-      const float f = r0 + 32 * k < a.R_total ? fv[k] : 0.0f;
+      const bool live = r0 + kRowStep * k < a.R_total && mq[k] != -INFINITY && ml[k].x != -INFINITY;
+      const float f = live ? __expf(mq[k] - ml[k].x) * ml[k].y : 0.0f;
       const uint32_t w[4] = {pv[k].x, pv[k].y, pv[k].z, pv[k].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1932,7 +2099,7 @@ __global__ __launch_bounds__(256) void importance_kernel(ImportanceArgs a) {
       }
     }
   }
-  // sum the 8 row lanes (lane bits 3..5) of each position chunk, then the 4 waves
+  // sum the 8 row lanes (lane bits 3..5) of each token chunk, then the waves
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float v = acc[i];
@@ -1947,9 +2114,11 @@ __global__ __launch_bounds__(256) void importance_kernel(ImportanceArgs a) {
   }
   __syncthreads();
   if (tid < 64) {
-    // position tid of the quarter holds token (tid % 2) * 32 + tid / 2 of it (one sequence: tokens are slots)
-    const int t = sub * 64 + (tid & 1) * 32 + (tid >> 1);
-    if (t < a.n) a.importance[t] += part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kImpWaves; ++w) sum += part[w][tid];
+    const int t = sub * 64 + tid;  // one sequence: token slots are tokens
+    if (t < a.n) a.importance[t] += sum;
   }
 }
 
@@ -1960,11 +2129,11 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, i
 
 struct ScoreLayout {
   Layout base;
-  size_t sub_max, sub_sum, stat, fac, total;
+  size_t sub_max, sub_sum, stat, total;
 };
 
 // The attend layout up to the tile statistics (decoded keys, probabilities), then the per-quarter
-// statistics, the per-row statistics and the per-(row, quarter) probability factors.
+// statistics and the per-row statistics.
 ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   ScoreLayout S{};
   S.base = make_layout(a);
@@ -1976,8 +2145,6 @@ ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   off += per_quarter;
   S.stat = off;
   off += align256((size_t)S.base.R_total * 2 * 4);
-  S.fac = off;
-  off += per_quarter;
   S.total = off;
   return S;
 }
@@ -2110,23 +2277,25 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   e.Hkv = a->kv_heads;
   e.Hq = a->q_heads;
   e.q_len = a->q_len;
-  e.D = a->head_dim;
   e.E = E;
   e.query_dtype = a->query_dtype;
   e.nsub = S.base.ntiles * 4;
-  e.fac = (float*)(ws + S.fac);
-  hipLaunchKernelGGL(row_stats_kernel, dim3(S.base.R_total), dim3(128), 0, st, e);
+  if (a->head_dim == 128)
+    hipLaunchKernelGGL(row_stats_kernel<128>, dim3(S.base.R_total), dim3(kStatThreads), 0, st, e);
+  else
+    hipLaunchKernelGGL(row_stats_kernel<64>, dim3(S.base.R_total), dim3(kStatThreads), 0, st, e);
   rc = dkv::check_launch("row_stats");
   if (rc) return rc;
   if (S.base.n_total == 0) return DKV_OK;
   ImportanceArgs im{};
   im.probs = (const uint16_t*)(ws + S.base.probs);
-  im.fac = (const float*)(ws + S.fac);
+  im.sub_max = (const float*)(ws + S.sub_max);
+  im.stat = (const float*)(ws + S.stat);
   im.importance = importance;
   im.R_total = S.base.R_total;
   im.n = S.base.n_total;
   im.ntiles = S.base.ntiles;
-  hipLaunchKernelGGL(importance_kernel, dim3((unsigned)S.base.ntiles * 4), dim3(256), 0, st, im);
+  hipLaunchKernelGGL(importance_kernel, dim3((unsigned)S.base.ntiles * 4), dim3(kImpThreads), 0, st, im);
   return dkv::check_launch("importance");
 }
 

@@ -82,16 +82,19 @@ def test_dequantize_codes_exhaustive():
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape_name,tokens,layers,query_scale,q_len", [
-    ("1b", 1500, (0, 7, 15), 1.0, 1),       # config-0 shape, N(0,1) query
-    ("1b", 1500, (3,), 150.0, 1),           # peaked attention
-    ("3b2", 900, (0, 1), 120.0, 1),         # head_dim 128 path
-    ("3b2", 700, (1,), 120.0, 5),           # q_len > 1 with a causal exact part
+@pytest.mark.parametrize("shape_name,tokens,layers,query_scale,q_len,qdtype", [
+    ("1b", 1500, (0, 7, 15), 1.0, 1, "float32"),    # 1500-token 1B shape, N(0,1) query
+    ("1b", 1500, (3,), 150.0, 1, "float32"),        # peaked attention
+    ("3b2", 900, (0, 1), 120.0, 1, "float32"),      # head_dim 128 path
+    ("3b2", 700, (1,), 120.0, 5, "float32"),        # q_len > 1 with a causal exact part
+    ("3b2", 700, (0,), 120.0, 5, "bfloat16"),       # many-row epilogue, per query type
+    ("1b", 900, (2,), 150.0, 3, "float16"),
 ])
-def test_attend_matches_oracle(shape_name, tokens, layers, query_scale, q_len):
+def test_attend_matches_oracle(shape_name, tokens, layers, query_scale, q_len, qdtype):
     shape = synth.SHAPE_1B if shape_name == "1b" else synth.ModelShape(2, 8, 128, 24, 2048)
-    print(f"[case] attend {shape_name} T={tokens} scale={query_scale} q_len={q_len}", flush=True)
-    case = build_case(shape, tokens, seed=1234, query_scale=query_scale, q_len=q_len)
+    print(f"[case] attend {shape_name} T={tokens} scale={query_scale} q_len={q_len} {qdtype}", flush=True)
+    case = build_case(shape, tokens, seed=1234, query_scale=query_scale, q_len=q_len,
+                      query_dtype=getattr(torch, qdtype))
     ctx, _, _ = gpu_context(case)
     for layer in layers:
         ref = oracle_attend(case, layer)

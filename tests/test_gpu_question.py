@@ -52,17 +52,19 @@ def _gpu_importance(case, ctx, plane_cap):
     return imp
 
 
-@pytest.mark.parametrize("shape_name,tokens,q_len,plane_cap", [
-    ("1b2", 1100, 16, 2),
-    ("3b2", 900, 8, 2),
-    ("1b2", 600, 4, 8),
+@pytest.mark.parametrize("shape_name,tokens,q_len,plane_cap,qdtype", [
+    ("1b2", 1100, 16, 2, "float32"),
+    ("3b2", 900, 8, 2, "float32"),
+    ("1b2", 600, 4, 8, "float32"),
+    ("3b2", 1300, 16, 2, "bfloat16"),  # the scoring epilogue is instantiated per query type
+    ("1b2", 800, 8, 2, "float16"),
 ])
-def test_question_scoring_and_topk(shape_name, tokens, q_len, plane_cap):
+def test_question_scoring_and_topk(shape_name, tokens, q_len, plane_cap, qdtype):
     import dkv_hip
 
     shape = synth.ModelShape(2, 8, 64, 32, 1024) if shape_name == "1b2" else synth.ModelShape(2, 8, 128, 24, 2048)
-    print(f"[case] scoring {shape_name} T={tokens} q_len={q_len} cap={plane_cap}", flush=True)
-    case = build_case(shape, tokens, seed=321, query_scale=40.0, q_len=q_len)
+    print(f"[case] scoring {shape_name} T={tokens} q_len={q_len} cap={plane_cap} {qdtype}", flush=True)
+    case = build_case(shape, tokens, seed=321, query_scale=40.0, q_len=q_len, query_dtype=getattr(torch, qdtype))
     ctx, _, _ = gpu_context(case)
     got = _gpu_importance(case, ctx, plane_cap).cpu().numpy()
     ref = _oracle_importance(case, plane_cap)
