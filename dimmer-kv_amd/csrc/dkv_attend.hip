@@ -741,15 +741,20 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // statistics are 32 values in the lane and one exchange with lane l32 + 32.
   auto row_blocks_quarters = [&](auto qtype) {
     using QF = typename QueryFrag<decltype(qtype)::value>::type;
+    // every head's key fragments into registers; then the key tile's LDS is free, and each wave
+    // stages its probabilities there so that every global store writes whole 128-byte lines
+    half8 kf[HPWAVE][KS][2];
+#pragma unroll
+    for (int hh = 0; hh < HPWAVE; ++hh) key_frags(kf[hh], hs * HPWAVE + hh);
+    __syncthreads();
+    constexpr int SROW = 72;  // staging row: 64 tokens + 8 halves of padding
+    half_t* stage = lds + wave * 32 * SROW;
 #pragma unroll
     for (int hh = 0; hh < HPWAVE; ++hh) {
-      const int hl = hs * HPWAVE + hh;
-      const int h = h0 + hl;
-      half8 kf[KS][2];
-      key_frags(kf, hl);
+      const int h = h0 + hs * HPWAVE + hh;
       auto quarter = [&](const QF (&qf)[KS], int mb) {
         floatx16 sacc[2];
-        block_mfma(qtype, QueryType<1>{}, sacc, kf, qf);
+        block_mfma(qtype, QueryType<1>{}, sacc, kf[hh], qf);
         float mx = -INFINITY;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -769,20 +774,28 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
             sm += sacc[tb][v];
           }
         sm += __shfl_xor(sm, 32);
-        // Every store is unconditional, so the compiler knows how many are in flight and the next
-        // block's query loads are waited for without waiting for these stores.  Lanes of rows past
-        // the end computed row RH - 1 from the same query and key bits, so they store the same
-        // bytes there; lanes l32 and l32 + 32 store the same statistics.
-        const long r_all = (long)h * RH + min(mb * 32 + l32, RH - 1);
-        // tokens 8 j + 4 lhi .. + 3 of each 32-token block: 8 bytes per store
-        uint16_t* dst = a.probs + r_all * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + 4 * lhi;
+        // row l32 of the block, tokens tb*32 + 8j + 4lhi .. + 3 into the staging rows
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            *(uint2*)(dst + tb * 32 + 8 * j) =
+            *(uint2*)(stage + l32 * SROW + tb * 32 + 8 * j + 4 * lhi) =
                 make_uint2((uint32_t)f16_bits(sacc[tb][4 * j]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 1]) << 16),
                            (uint32_t)f16_bits(sacc[tb][4 * j + 2]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 3]) << 16));
+        __builtin_amdgcn_wave_barrier();  // LDS runs a wave's accesses in order: the reads see the writes
+        // lane L then holds 8 tokens of rows L/8 + 8k: eight lanes write one row's 128 bytes.  Every
+        // store is unconditional, so the compiler knows how many are in flight and the next block's
+        // query loads are waited for without waiting for these stores.  Rows past the end were
+        // computed from row RH - 1's query and key bits, so they store the same bytes there.
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint4 pv = *(const uint4*)(stage + ((lane >> 3) + 8 * k) * SROW + (lane & 7) * 8);
+          const long r = (long)h * RH + min(mb * 32 + (lane >> 3) + 8 * k, RH - 1);
+          *(uint4*)(a.probs + r * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + (lane & 7) * 8) = pv;
+        }
+        __builtin_amdgcn_wave_barrier();  // the next block's staging writes stay behind these reads
+        // lanes l32 and l32 + 32 hold the same statistics
+        const long r_all = (long)h * RH + min(mb * 32 + l32, RH - 1);
         a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mx;
         a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sm;
       };
@@ -1922,128 +1935,159 @@ struct RowStatsArgs {
 constexpr int kStatThreads = 256;
 constexpr int kStatWaves = kStatThreads / 64;
 constexpr int kStatKeys = kStatThreads / 2;  // exact keys scored per pass: two lanes per key
-constexpr int kStatBatch = 4;                // quarter statistics per thread whose loads go out together
 
-// The (max, sum exp) of a batch of quarter statistics (-inf maxima and entries past nsub skipped),
-// merged into (mc, lc).
-DKV_DEVICE void merge_quarters(const float (&mt)[kStatBatch], const float (&st)[kStatBatch], int first, int stride,
-                               int nsub, float& mc, float& lc) {
-  float bm = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kStatBatch; ++i) bm = first + i * stride < nsub ? fmaxf(bm, mt[i]) : bm;
-  if (bm == -INFINITY) return;
-  float bs = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kStatBatch; ++i) {
-    const bool live = first + i * stride < nsub && mt[i] != -INFINITY;
-    bs += live ? st[i] * __expf(mt[i] - bm) : 0.0f;
-  }
-  if (bm > mc) {
-    lc = (mc == -INFINITY ? 0.0f : lc * __expf(mc - bm)) + bs;
-    mc = bm;
-  } else {
-    lc += bs * __expf(bm - mc);
-  }
-}
-
-// One workgroup per (query head, query position) row: the softmax statistics over the compressed
-// tokens (merged from K2's per-quarter maxima and sums), the exact context tokens and the
-// question's own keys up to this position (causal).  Every global load of the first round (the
-// thread's quarter statistics, the query element, the first pass of exact keys) is unconditional
-// and goes out before any is used.  Lanes 2 k and 2 k + 1 score key k of a pass, each over half of
-// the head dimension.
-template <int D>
+// One workgroup per RPW consecutive rows of one query head (RPW divides q_len): the softmax
+// statistics of each row over the compressed tokens (merged from K2's per-quarter maxima and sums),
+// the exact context tokens and the question's own keys up to the row's position (causal).  The
+// rows share their KV head, so each exact key is loaded once for all of them.  Every global load
+// of the first round (the rows' quarter statistics, their query rows, the first pass of exact keys)
+// is unconditional and goes out before any is used.  Lanes 2 k and 2 k + 1 score key k of a pass,
+// each over half of the head dimension.
+template <int D, int RPW>
 __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a) {
-  constexpr int U = D / 8;  // float4 per lane: half a key row
-  __shared__ __attribute__((aligned(16))) float q[D];
-  __shared__ float red[2][kStatWaves];
-  const int row = blockIdx.x;
+  constexpr int U = D / 8;                             // float4 per lane: half a key row
+  constexpr int QW = (RPW * D + kStatThreads - 1) / kStatThreads;  // query elements per thread
+  __shared__ __attribute__((aligned(16))) float q[RPW][D];
+  __shared__ float red[2][kStatWaves][RPW];
+  const int row0 = blockIdx.x * RPW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kj = tid >> 1, kh = tid & 1;
   const int gq = a.Hq / a.Hkv;
-  const int qh = row / a.q_len, qi = row % a.q_len;
+  const int qh = row0 / a.q_len, qi0 = row0 % a.q_len;
   const int h = qh / gq;
-  const int nkeys = a.E + qi + 1;  // exact context tokens + question keys 0..qi
-  const float* smax = a.sub_max + (long)row * a.nsub;
-  const float* ssum = a.sub_sum + (long)row * a.nsub;
+  const int nkeys_max = a.E + qi0 + RPW;  // row i sees exact context tokens + question keys 0..qi0 + i
   auto key_half = [&](int j) {
     return (const float4*)(j < a.E ? a.key_exact + ((long)h * a.E + j) * D
                                    : a.key_question + ((long)h * a.q_len + (j - a.E)) * D) + kh * U;
   };
-  float mt[kStatBatch], st[kStatBatch];
+  // first round: quarter statistics (one per row and thread), query words, the first pass of keys
+  float mt[RPW], st[RPW];
+  {
+    const int t = max(min(tid, a.nsub - 1), 0);  // nsub = 0 (no compressed tokens): a value nobody uses
 #pragma unroll
-  for (int i = 0; i < kStatBatch; ++i) {
-    const int t = min(tid + i * kStatThreads, a.nsub - 1);
-    mt[i] = smax[t];
-    st[i] = ssum[t];
+    for (int i = 0; i < RPW; ++i) {
+      mt[i] = a.sub_max[(long)(row0 + i) * a.nsub + t];
+      st[i] = a.sub_sum[(long)(row0 + i) * a.nsub + t];
+    }
   }
-  const long qidx = ((long)qh * a.q_len + qi) * D + min(tid, D - 1);
-  const uint32_t qword = load_query_word(a.query, qidx, a.query_dtype);
+  uint32_t qword[QW];
+  const long qbase = ((long)qh * a.q_len + qi0) * D;  // the RPW rows' queries are contiguous
+#pragma unroll
+  for (int w = 0; w < QW; ++w) qword[w] = load_query_word(a.query, qbase + min(tid + w * kStatThreads, RPW * D - 1),
+                                                          a.query_dtype);
   float4 k4[U];
   {
-    const float4* kr = key_half(min(kj, nkeys - 1));
+    const float4* kr = key_half(min(kj, nkeys_max - 1));
 #pragma unroll
     for (int u = 0; u < U; ++u) k4[u] = kr[u];
   }
   __builtin_amdgcn_sched_barrier(0);
-  // compressed part
-  float mc = -INFINITY, lc = 0.0f;
-  merge_quarters(mt, st, tid, kStatThreads, a.nsub, mc, lc);
-  for (int t0 = kStatThreads * kStatBatch; t0 < a.nsub; t0 += kStatThreads * kStatBatch) {  // long contexts
+  // compressed part: the thread's quarters of each row
+  float mc[RPW], lc[RPW];
 #pragma unroll
-    for (int i = 0; i < kStatBatch; ++i) {
-      const int t = min(t0 + tid + i * kStatThreads, a.nsub - 1);
-      mt[i] = smax[t];
-      st[i] = ssum[t];
-    }
-    merge_quarters(mt, st, t0 + tid, kStatThreads, a.nsub, mc, lc);
+  for (int i = 0; i < RPW; ++i) {
+    const bool live = tid < a.nsub && mt[i] != -INFINITY;
+    mc[i] = live ? mt[i] : -INFINITY;
+    lc[i] = live ? st[i] : 0.0f;
   }
-  if (tid < D) q[tid] = query_word_value(qword, qidx, a.query_dtype);
-  __syncthreads();
-  auto score = [&]() {  // both lanes of the pair return the key's scaled score
-    float dot = 0.0f;
+  for (int t0 = kStatThreads; t0 < a.nsub; t0 += kStatThreads) {  // more quarters than threads
+    const int t = min(t0 + tid, a.nsub - 1);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float4 q4 = *(const float4*)&q[kh * (D / 2) + 4 * u];
-      dot += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+    for (int i = 0; i < RPW; ++i) {
+      mt[i] = a.sub_max[(long)(row0 + i) * a.nsub + t];
+      st[i] = a.sub_sum[(long)(row0 + i) * a.nsub + t];
     }
-    return (dot + __shfl_xor(dot, 1)) * a.scaling;
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      if (t0 + tid >= a.nsub || mt[i] == -INFINITY) continue;
+      if (mt[i] > mc[i]) {
+        lc[i] = (mc[i] == -INFINITY ? 0.0f : lc[i] * __expf(mc[i] - mt[i])) + st[i];
+        mc[i] = mt[i];
+      } else {
+        lc[i] += st[i] * __expf(mt[i] - mc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < QW; ++w) {
+    const int e = tid + w * kStatThreads;
+    if (e < RPW * D) (&q[0][0])[e] = query_word_value(qword[w], qbase + e, a.query_dtype);
+  }
+  __syncthreads();
+  // scores of the thread's key (both lanes of the pair get the full dot) for every row, RG rows at a
+  // time (the scheduling barrier keeps the compiler from holding every row's query in registers)
+  constexpr int RG = 256 / D;
+  auto scores = [&](float (&sc)[RPW]) {
+#pragma unroll
+    for (int i0 = 0; i0 < RPW; i0 += RG) {
+#pragma unroll
+      for (int i = i0; i < i0 + RG && i < RPW; ++i) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float4 q4 = *(const float4*)&q[i][kh * (D / 2) + 4 * u];
+          dot += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
+        }
+        sc[i] = (dot + __shfl_xor(dot, 1)) * a.scaling;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
-  const float first = score();
-  float me = kj < nkeys ? first : -INFINITY;
-  for (int j0 = kStatKeys; j0 < nkeys; j0 += kStatKeys) {  // more exact keys than one pass holds
-    const float4* kr = key_half(min(j0 + kj, nkeys - 1));
+  float first[RPW], m[RPW];
+  scores(first);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) m[i] = fmaxf(mc[i], kj < a.E + qi0 + i + 1 ? first[i] : -INFINITY);
+  for (int j0 = kStatKeys; j0 < nkeys_max; j0 += kStatKeys) {  // more exact keys than one pass holds
+    const float4* kr = key_half(min(j0 + kj, nkeys_max - 1));
 #pragma unroll
     for (int u = 0; u < U; ++u) k4[u] = kr[u];
-    const float sc = score();
-    me = j0 + kj < nkeys ? fmaxf(me, sc) : me;
-  }
-  // joint maximum over both parts, then the sum of exponentials (each key counted by its even lane)
-  float m = fmaxf(me, mc);
-  m = wave_max(m);
-  if (lane == 0) red[0][wave] = m;
-  __syncthreads();
-  float M = red[0][0];
+    float sc[RPW];
+    scores(sc);
 #pragma unroll
-  for (int w = 1; w < kStatWaves; ++w) M = fmaxf(M, red[0][w]);
-  float l = (mc == -INFINITY || M == -INFINITY) ? 0.0f : lc * __expf(mc - M);
-  l += kh == 0 && kj < nkeys ? __expf(first - M) : 0.0f;
-  for (int j0 = kStatKeys; j0 < nkeys; j0 += kStatKeys) {
-    const float4* kr = key_half(min(j0 + kj, nkeys - 1));
+    for (int i = 0; i < RPW; ++i) m[i] = j0 + kj < a.E + qi0 + i + 1 ? fmaxf(m[i], sc[i]) : m[i];
+  }
+  // joint maxima, then the sums of exponentials (each key counted by its even lane)
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) m[i] = wave_max(m[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) red[0][wave][i] = m[i];
+  }
+  __syncthreads();
+  float M[RPW], l[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    M[i] = red[0][0][i];
+#pragma unroll
+    for (int w = 1; w < kStatWaves; ++w) M[i] = fmaxf(M[i], red[0][w][i]);
+    l[i] = (mc[i] == -INFINITY || M[i] == -INFINITY) ? 0.0f : lc[i] * __expf(mc[i] - M[i]);
+    l[i] += kh == 0 && kj < a.E + qi0 + i + 1 ? __expf(first[i] - M[i]) : 0.0f;
+  }
+  for (int j0 = kStatKeys; j0 < nkeys_max; j0 += kStatKeys) {
+    const float4* kr = key_half(min(j0 + kj, nkeys_max - 1));
 #pragma unroll
     for (int u = 0; u < U; ++u) k4[u] = kr[u];
-    const float sc = score();
-    l += kh == 0 && j0 + kj < nkeys ? __expf(sc - M) : 0.0f;
-  }
-  l = wave_sum(l);
-  if (lane == 0) red[1][wave] = l;
-  __syncthreads();
-  if (tid == 0) {
-    float L = 0.0f;
+    float sc[RPW];
+    scores(sc);
 #pragma unroll
-    for (int w = 0; w < kStatWaves; ++w) L += red[1][w];
-    a.stat[2 * row] = M;
-    a.stat[2 * row + 1] = L > 0.0f ? 1.0f / L : 0.0f;
+    for (int i = 0; i < RPW; ++i) l[i] += kh == 0 && j0 + kj < a.E + qi0 + i + 1 ? __expf(sc[i] - M[i]) : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) l[i] = wave_sum(l[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) red[1][wave][i] = l[i];
+  }
+  __syncthreads();
+  if (tid < RPW) {  // thread i writes row i: its maximum from the first exchange, its sum from the second
+    float Mi = red[0][0][tid], L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kStatWaves; ++w) {
+      Mi = fmaxf(Mi, red[0][w][tid]);
+      L += red[1][w][tid];
+    }
+    a.stat[2 * (row0 + tid)] = Mi;
+    a.stat[2 * (row0 + tid) + 1] = L > 0.0f ? 1.0f / L : 0.0f;
   }
 }
 
@@ -2280,10 +2324,20 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   e.E = E;
   e.query_dtype = a->query_dtype;
   e.nsub = S.base.ntiles * 4;
-  if (a->head_dim == 128)
-    hipLaunchKernelGGL(row_stats_kernel<128>, dim3(S.base.R_total), dim3(kStatThreads), 0, st, e);
-  else
-    hipLaunchKernelGGL(row_stats_kernel<64>, dim3(S.base.R_total), dim3(kStatThreads), 0, st, e);
+  // eight rows of one query head per workgroup when the question length allows it
+  const bool rows8 = a->q_len % 8 == 0;
+  const dim3 sgrid((unsigned)(rows8 ? S.base.R_total / 8 : S.base.R_total));
+  if (a->head_dim == 128) {
+    if (rows8)
+      hipLaunchKernelGGL((row_stats_kernel<128, 8>), sgrid, dim3(kStatThreads), 0, st, e);
+    else
+      hipLaunchKernelGGL((row_stats_kernel<128, 1>), sgrid, dim3(kStatThreads), 0, st, e);
+  } else {
+    if (rows8)
+      hipLaunchKernelGGL((row_stats_kernel<64, 8>), sgrid, dim3(kStatThreads), 0, st, e);
+    else
+      hipLaunchKernelGGL((row_stats_kernel<64, 1>), sgrid, dim3(kStatThreads), 0, st, e);
+  }
   rc = dkv::check_launch("row_stats");
   if (rc) return rc;
   if (S.base.n_total == 0) return DKV_OK;
