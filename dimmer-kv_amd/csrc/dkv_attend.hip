@@ -269,28 +269,17 @@ __global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs 
 // ---------------------------------------------------------------------------
 constexpr int kSmallRows = 4;
 
-template <int D, bool SPLIT, bool ROWMAJOR>
-DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
-                                           float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
-                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs,
-                                           int split) {
-  constexpr int HPW = 256 / D;
-  constexpr int DB = D / 32;
-  constexpr int HALF_BLK = DB / 2;
+// Stage the RoPE rows (cos and sin, [256][D/2 + 4] floats each) of the tile's tokens in LDS, with
+// coalesced loads: positions from pos_s, the loads of a batch issued together, rows past the tile's
+// tokens replaced by (1, 0) afterwards.  Ends with a barrier.
+template <int D>
+DKV_DEVICE void stage_rope_rows(const K2Args& a, float* cs, float* sn, const int* pos_s, int count) {
   constexpr int HALF_D = D / 2;
-  constexpr int CSTR = HALF_D + 4;  // floats per staged RoPE row (keeps b128 reads conflict-free)
-  float* cs = (float*)lds_h;                 // [256][CSTR] cos
-  float* sn = cs + kTileTok * CSTR;          // [256][CSTR] sin
-  // pos_s (the tile's positions) and qs ([HPW][kSmallRows][D] query rows) were staged at kernel start
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tq = wave & 3, hs = wave >> 2;
-  const int l32 = lane & 31, lhi = lane >> 5;
-
-  // stage RoPE rows of the tile's tokens (positions from LDS; the loads of a batch go out together,
-  // padding rows replaced afterwards)
+  constexpr int CSTR = HALF_D + 4;
   constexpr int V4_PER_ROW = HALF_D / 4;
   constexpr int STAGE_ITERS = kTileTok * V4_PER_ROW / kK2Threads;  // 8 (D = 128) or 4 (D = 64)
   constexpr int STAGE_BATCH = 4;  // (one round of 8 measured slower: the main loop's registers)
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int i0 = 0; i0 < STAGE_ITERS; i0 += STAGE_BATCH) {
     long pos[STAGE_BATCH];
@@ -313,6 +302,26 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
     }
   }
   __syncthreads();
+}
+
+template <int D, bool SPLIT, bool ROWMAJOR>
+DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
+                                           float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
+                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs,
+                                           int split) {
+  constexpr int HPW = 256 / D;
+  constexpr int DB = D / 32;
+  constexpr int HALF_BLK = DB / 2;
+  constexpr int HALF_D = D / 2;
+  constexpr int CSTR = HALF_D + 4;  // floats per staged RoPE row (keeps b128 reads conflict-free)
+  float* cs = (float*)lds_h;                 // [256][CSTR] cos
+  float* sn = cs + kTileTok * CSTR;          // [256][CSTR] sin
+  // pos_s (the tile's positions) and qs ([HPW][kSmallRows][D] query rows) were staged at kernel start
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tq = wave & 3, hs = wave >> 2;
+  const int l32 = lane & 31, lhi = lane >> 5;
+
+  stage_rope_rows<D>(a, cs, sn, pos_s, count);
 
   // part[hw][r][tb]: partial q . k over this lane's dimensions, head hw of the wave
   constexpr int HPWAVE = HPW / 2;
@@ -465,7 +474,6 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   constexpr int HPW = 256 / D;      // heads per workgroup
   constexpr int DB = D / 32;        // 32-row blocks per head
   constexpr int HALF_BLK = DB / 2;  // RoPE partner offset in blocks
-  constexpr int KSTR = D + 8;       // LDS stride of the rebuilt-key tile
   __shared__ __attribute__((aligned(16))) half_t lds[2 * 2 * kTileTok * kStride];
   __shared__ float stat_m[HPW][4][32];
   __shared__ float stat_s[HPW][4][32];
@@ -630,77 +638,78 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __syncthreads();
 
   const int gq = a.Hq / a.Hkv;
-  const int half_d = D / 2;
   if constexpr (SMALL) {
     keys_scores_small_epilogue<D, SPLIT, ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s,
                                                    q_s, split);
     return;
   } else {
 
-  // ---- epilogue 1 (many query rows): RoPE, rebuilt keys -> LDS as fp16 [head][token][D+8].
-  // Positions come from LDS (clamped to the tile's last token past its end), so every RoPE load
-  // is unconditional and the compiler can keep several in flight.
-  half_t* Kl = lds;
+  // ---- epilogue 1 (many query rows): RoPE in registers, straight into MFMA key fragments.  The
+  // tile's cos / sin rows are staged in LDS with coalesced loads; each lane rotates the
+  // (d, d + D/2) pairs it holds in fp32 and rounds them to fp16.  Lane (l32, lhi) then holds, for
+  // its token, 4 of the 8 dimensions of every 8-dimension chunk c (offset 4 lhi); the key fragment
+  // of k-step ks needs chunk 2 ks + lhi whole, which one permlane32 swap per dword of the chunk pair
+  // (2 ks, 2 ks + 1) provides: lanes 0-31 keep their chunk 2 ks half and get lanes 32-63's, lanes
+  // 32-63 keep their chunk 2 ks + 1 half and get lanes 0-31's.
+  constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in the epilogue
+  constexpr int KS = D / 16;       // MFMA k-steps over the head dimension
+  constexpr int CSTR = D / 2 + 4;  // staged RoPE row stride (floats), as stage_rope_rows lays it out
+  half8 kf[HPWAVE][KS][2];
+  {
+    float* cs = (float*)lds;
+    float* sn = cs + kTileTok * CSTR;
+    stage_rope_rows<D>(a, cs, sn, pos_s, count);
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int n = tq * 64 + tb * 32 + l32;
-    const long pos = pos_s[n];
-    const float* cosr = a.rope_cos + pos * half_d;
-    const float* sinr = a.rope_sin + pos * half_d;
-    // the token's cos / sin values for both rotated row blocks, all loads issued before any use
-    float4 c[2][4], sv4[2][4];
+    for (int tb = 0; tb < 2; ++tb) {
+      const int n = tq * 64 + tb * 32 + l32;
+      uint32_t own[HPWAVE][D / 8][2];  // chunk c of head hh: this lane's 4 halves as 2 dwords
 #pragma unroll
-    for (int rb = 0, i = 0; rb < 4; ++rb) {
-      if ((rb % DB) >= HALF_BLK) continue;
+      for (int rb = 0; rb < 4; ++rb) {
+        if ((rb % DB) >= HALF_BLK) continue;
+        const int rb2 = rb + HALF_BLK;
+        const int hh = rb / DB;
 #pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
-        c[i][v4] = *(const float4*)(cosr + d0);
-        sv4[i][v4] = *(const float4*)(sinr + d0);
-      }
-      ++i;
-    }
-    __builtin_amdgcn_sched_barrier(0);
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
+          const float4 c4 = *(const float4*)(cs + n * CSTR + d0);
+          const float4 s4 = *(const float4*)(sn + n * CSTR + d0);
+          const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+          const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+          uint32_t lo[2], hi[2];
 #pragma unroll
-    for (int rb = 0, i = 0; rb < 4; ++rb) {
-      if ((rb % DB) >= HALF_BLK) continue;
-      const int rb2 = rb + HALF_BLK;
-      const int hl = hs * (128 / D) + rb / DB;
-#pragma unroll
-      for (int v4 = 0; v4 < 4; ++v4) {
-        const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
-        const float cv[4] = {c[i][v4].x, c[i][v4].y, c[i][v4].z, c[i][v4].w};
-        const float sv[4] = {sv4[i][v4].x, sv4[i][v4].y, sv4[i][v4].z, sv4[i][v4].w};
-        half4 lo, hi;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float klo = acc[tb][rb][v4 * 4 + e];
-          const float khi = acc[tb][rb2][v4 * 4 + e];
-          lo[e] = (half_t)(klo * cv[e] - khi * sv[e]);
-          hi[e] = (half_t)(khi * cv[e] + klo * sv[e]);
+          for (int e = 0; e < 4; e += 2) {
+            const float klo0 = acc[tb][rb][v4 * 4 + e], khi0 = acc[tb][rb2][v4 * 4 + e];
+            const float klo1 = acc[tb][rb][v4 * 4 + e + 1], khi1 = acc[tb][rb2][v4 * 4 + e + 1];
+            lo[e / 2] = (uint32_t)f16_bits(klo0 * cv[e] - khi0 * sv[e]) |
+                        ((uint32_t)f16_bits(klo1 * cv[e + 1] - khi1 * sv[e + 1]) << 16);
+            hi[e / 2] = (uint32_t)f16_bits(khi0 * cv[e] + klo0 * sv[e]) |
+                        ((uint32_t)f16_bits(khi1 * cv[e + 1] + klo1 * sv[e + 1]) << 16);
+          }
+          const int clo = (rb % DB) * 4 + v4, chi = (rb2 % DB) * 4 + v4;
+          own[hh][clo][0] = lo[0];
+          own[hh][clo][1] = lo[1];
+          own[hh][chi][0] = hi[0];
+          own[hh][chi][1] = hi[1];
         }
-        *(half4*)(Kl + (hl * kTileTok + n) * KSTR + d0) = lo;
-        *(half4*)(Kl + (hl * kTileTok + n) * KSTR + d0 + half_d) = hi;
       }
-      ++i;
+#pragma unroll
+      for (int hh = 0; hh < HPWAVE; ++hh)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const auto w0 = __builtin_amdgcn_permlane32_swap(own[hh][2 * ks][0], own[hh][2 * ks + 1][0], false, false);
+          const auto w1 = __builtin_amdgcn_permlane32_swap(own[hh][2 * ks][1], own[hh][2 * ks + 1][1], false, false);
+          const uint32_t f[4] = {w0[0], w1[0], w0[1], w1[1]};
+          __builtin_memcpy(&kf[hh][ks][tb], f, 16);
+        }
     }
   }
+  // the staged RoPE rows are read by every wave before any reuses their LDS
   __syncthreads();
 
-  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block.  The key fragments of a
-  // head and this wave's 64 tokens serve every row block, so they are read from LDS once per head;
-  // the query fragments of a row block are loaded together (rows past the end read the last row,
-  // whose scores are discarded), in the query's own type.
+  // ---- epilogue 2: scores = q . k * scaling on MFMA, per 32-row block, with the key fragments in
+  // registers; the query fragments of a row block are loaded together (rows past the end read the
+  // last row, whose scores are discarded), in the query's own type.
   const int mblocks = (RH + 31) / 32;
-  constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in this phase
-  constexpr int KS = D / 16;       // MFMA k-steps over the head dimension
-  auto key_frags = [&](half8 (&kf)[KS][2], int hl) {
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-        kf[ks][tb] = lds_half8(Kl + (hl * kTileTok + tq * 64 + tb * 32 + l32) * KSTR + ks * 16 + lhi * 8);
-  };
   // the query fragments of row block mb of head h (rows past the end read the last row)
   auto load_queries = [&](auto qtype, auto (&qf)[KS], int h, int mb) {
     constexpr int QT = decltype(qtype)::value;
@@ -741,12 +750,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // statistics are 32 values in the lane and one exchange with lane l32 + 32.
   auto row_blocks_quarters = [&](auto qtype) {
     using QF = typename QueryFrag<decltype(qtype)::value>::type;
-    // every head's key fragments into registers; then the key tile's LDS is free, and each wave
-    // stages its probabilities there so that every global store writes whole 128-byte lines
-    half8 kf[HPWAVE][KS][2];
-#pragma unroll
-    for (int hh = 0; hh < HPWAVE; ++hh) key_frags(kf[hh], hs * HPWAVE + hh);
-    __syncthreads();
+    // each wave stages its probabilities in LDS so that every global store writes whole 128-byte lines
     constexpr int SROW = 72;  // staging row: 64 tokens + 8 halves of padding
     half_t* stage = lds + wave * 32 * SROW;
 #pragma unroll
@@ -817,9 +821,6 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // decoding many rows: the four waves of a head exchange their quarters' statistics per row block,
   // then write probabilities relative to the tile maximum in the value side's layout
   auto row_blocks = [&](auto qtype) {
-    half8 kf[HPWAVE][KS][2];
-#pragma unroll
-    for (int hh = 0; hh < HPWAVE; ++hh) key_frags(kf[hh], hs * HPWAVE + hh);
     for (int mb = 0; mb < mblocks; ++mb) {
       float xs[HPWAVE][16][2];
 #pragma unroll
