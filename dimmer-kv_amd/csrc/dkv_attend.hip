@@ -205,6 +205,11 @@ DKV_DEVICE long prob_index(long row, long slot, int R_total) {
   return ((slot >> 4) * R_total + row) * 16 + (slot & 15);
 }
 
+// Question scoring's per-quarter statistics, [R/8][nsub][8]: eight consecutive rows sit together for
+// each 64-token quarter t, so a wave's 32 rows store four 32-byte pieces and the row-statistics
+// kernel reads its eight rows' quarters as one contiguous run.
+DKV_DEVICE long sub_index(long row, int t, int nsub) { return ((row >> 3) * nsub + t) * 8 + (row & 7); }
+
 
 // ---------------------------------------------------------------------------
 // K1 (fp16 operand form): decode the hot key codes of every token into the
@@ -405,8 +410,8 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
         a.probs[r_all * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + lhi * 32 + l32] =
             f16_bits(lhi ? e1 : e0);
         if (lane == 0) {
-          a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mq;
-          a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sq;
+          a.sub_max[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = mq;
+          a.sub_sum[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = sq;
         }
         continue;
       }
@@ -759,25 +764,36 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
       auto quarter = [&](const QF (&qf)[KS], int mb) {
         floatx16 sacc[2];
         block_mfma(qtype, QueryType<1>{}, sacc, kf[hh], qf);
-        float mx = -INFINITY;
+        // The maximum is taken over the raw dot products (the scale is positive) and the scale folds
+        // into the exponent: p = 2^(q.k * scale * log2(e) - max * scale * log2(e)), one fma and one
+        // exp2 per score.  Tokens past the tile's end (last tile only) score -inf.
+        if (count < kTileTok) {
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int n = tq * 64 + tb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+              sacc[tb][v] = n < count ? sacc[tb][v] : -INFINITY;
+            }
+        }
+        float mraw = -INFINITY;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int n = tq * 64 + tb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-            sacc[tb][v] = n < count ? sacc[tb][v] * a.scaling : -INFINITY;
-            mx = fmaxf(mx, sacc[tb][v]);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+          for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sacc[tb][v]);
+        mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
+        const float c2 = a.scaling * 1.44269504088896341f;
+        const float off2 = mraw == -INFINITY ? 0.0f : mraw * c2;
         float sm = 0.0f;
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
-            sacc[tb][v] = mx == -INFINITY ? 0.0f : __expf(sacc[tb][v] - mx);
+            sacc[tb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[tb][v], c2, -off2));  // -inf -> 0
             sm += sacc[tb][v];
           }
         sm += __shfl_xor(sm, 32);
+        const float mx = mraw * a.scaling;  // the quarter maximum of the scaled scores (-inf if empty)
         // row l32 of the block, tokens tb*32 + 8j + 4lhi .. + 3 into the staging rows
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -800,8 +816,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
         __builtin_amdgcn_wave_barrier();  // the next block's staging writes stay behind these reads
         // lanes l32 and l32 + 32 hold the same statistics
         const long r_all = (long)h * RH + min(mb * 32 + l32, RH - 1);
-        a.sub_max[r_all * a.ntiles * 4 + tile * 4 + tq] = mx;
-        a.sub_sum[r_all * a.ntiles * 4 + tile * 4 + tq] = sm;
+        a.sub_max[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = mx;
+        a.sub_sum[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = sm;
       };
       // two query buffers: the next row block's fragments load while this block's MFMAs run
       QF qa[KS], qb[KS];
@@ -1963,14 +1979,23 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a)
   };
   // first round: quarter statistics (one per row and thread), query words, the first pass of keys
   float mt[RPW], st[RPW];
-  {
-    const int t = max(min(tid, a.nsub - 1), 0);  // nsub = 0 (no compressed tokens): a value nobody uses
+  // the RPW rows' statistics of quarter t (eight rows of one block: 32 contiguous bytes per array)
+  auto load_quarter = [&](int t) {
+    if constexpr (RPW == 8) {
+      const float4* pm = (const float4*)(a.sub_max + sub_index(row0, t, a.nsub));
+      const float4* ps = (const float4*)(a.sub_sum + sub_index(row0, t, a.nsub));
+      const float4 m0 = pm[0], m1 = pm[1], s0 = ps[0], s1 = ps[1];
+      mt[0] = m0.x; mt[1] = m0.y; mt[2] = m0.z; mt[3] = m0.w; mt[4] = m1.x; mt[5] = m1.y; mt[6] = m1.z; mt[7] = m1.w;
+      st[0] = s0.x; st[1] = s0.y; st[2] = s0.z; st[3] = s0.w; st[4] = s1.x; st[5] = s1.y; st[6] = s1.z; st[7] = s1.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      mt[i] = a.sub_max[(long)(row0 + i) * a.nsub + t];
-      st[i] = a.sub_sum[(long)(row0 + i) * a.nsub + t];
+      for (int i = 0; i < RPW; ++i) {
+        mt[i] = a.sub_max[sub_index(row0 + i, t, a.nsub)];
+        st[i] = a.sub_sum[sub_index(row0 + i, t, a.nsub)];
+      }
     }
-  }
+  };
+  load_quarter(max(min(tid, a.nsub - 1), 0));  // nsub = 0 (no compressed tokens): values nobody uses
   uint32_t qword[QW];
   const long qbase = ((long)qh * a.q_len + qi0) * D;  // the RPW rows' queries are contiguous
 #pragma unroll
@@ -1992,12 +2017,7 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a)
     lc[i] = live ? st[i] : 0.0f;
   }
   for (int t0 = kStatThreads; t0 < a.nsub; t0 += kStatThreads) {  // more quarters than threads
-    const int t = min(t0 + tid, a.nsub - 1);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      mt[i] = a.sub_max[(long)(row0 + i) * a.nsub + t];
-      st[i] = a.sub_sum[(long)(row0 + i) * a.nsub + t];
-    }
+    load_quarter(min(t0 + tid, a.nsub - 1));
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       if (t0 + tid >= a.nsub || mt[i] == -INFINITY) continue;
@@ -2128,7 +2148,7 @@ __global__ __launch_bounds__(kImpThreads) void importance_kernel(ImportanceArgs 
     for (int k = 0; k < kImpBatch; ++k) {  // clamped rows: every load is unconditional
       const int r = min(r0 + kRowStep * k, a.R_total - 1);
       pv[k] = *(const uint4*)(a.probs + (long)r * pstride + pos);
-      mq[k] = a.sub_max[(long)r * nsub + sub];
+      mq[k] = a.sub_max[sub_index(r, sub, nsub)];
       ml[k] = *(const float2*)(a.stat + 2 * r);
     }
     __builtin_amdgcn_sched_barrier(0);  // every load of the batch goes out before the first is used
@@ -2182,7 +2202,7 @@ struct ScoreLayout {
 ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   ScoreLayout S{};
   S.base = make_layout(a);
-  const size_t per_quarter = align256((size_t)S.base.R_total * S.base.ntiles * 4 * 4);
+  const size_t per_quarter = align256((size_t)((S.base.R_total + 7) / 8 * 8) * S.base.ntiles * 4 * 4);
   size_t off = S.base.w_part;
   S.sub_max = off;
   off += per_quarter;
