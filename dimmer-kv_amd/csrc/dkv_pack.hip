@@ -543,6 +543,10 @@ __global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const u
   const int64_t off = tok_off[t];
   const int full_bytes = s.order.prefix_bytes[K];
   uint8_t* dst_tok = refined + (long)r * full_bytes;
+  // One group per thread.  The full segment is the header and m_full plane words (at most 17
+  // 32-bit words); word i comes from the hot segment (header and planes below m_hot) or the cold
+  // one (the header when m_hot = 0, then planes m_hot..).  Every word's source is selected first
+  // and all loads go out together (words past the segment re-read the header and are not stored).
   for (int g = threadIdx.x; g < G; g += blockDim.x) {
     const int m_hot = s.order.planes[(long)k * G + g];
     const int m_full = s.order.planes[(long)K * G + g];
@@ -550,17 +554,20 @@ __global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const u
     uint32_t* dst = (uint32_t*)(dst_tok + s.order.seg_off[(long)K * G + g]);
     const uint32_t* hseg = (const uint32_t*)(s.blob + off + s.order.seg_off[(long)k * G + g]);
     const uint32_t* cseg = (const uint32_t*)(cold + cold_tok_off[t] + s.order.cold_off[(long)k * G + g]);
-    if (m_hot > 0) {
-      dst[0] = hseg[0];
-    } else {
-      dst[0] = cseg[0];
-      cseg += 1;
+    const uint32_t* head = m_hot > 0 ? hseg : cseg;
+    const uint32_t* cplanes = m_hot > 0 ? cseg : cseg + 1;  // the cold part's plane words
+    const int words = 1 + 2 * m_full;
+    uint32_t v[17];
+    v[0] = head[0];
+#pragma unroll
+    for (int i = 1; i < 17; ++i) {
+      const int p = (i - 1) >> 1, j = (i - 1) & 1;
+      const uint32_t* src = i >= words ? head : p < m_hot ? hseg + 1 + 2 * p + j : cplanes + 2 * (p - m_hot) + j;
+      v[i] = *src;
     }
-    for (int p = 0; p < m_full; ++p) {
-      const uint32_t* src = (p < m_hot) ? (hseg + 1 + 2 * p) : (cseg + 2 * (p - m_hot));
-      dst[1 + 2 * p] = src[0];
-      dst[2 + 2 * p] = src[1];
-    }
+#pragma unroll
+    for (int i = 0; i < 17; ++i)
+      if (i < words) dst[i] = v[i];
   }
   __syncthreads();
   if (threadIdx.x == 0) {

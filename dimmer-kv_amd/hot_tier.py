@@ -92,8 +92,14 @@ class PackedStream:
         self.refined = 0
         self.version = 0  # bumped whenever tokens change (refine), so decoded copies know to refresh
         self.initial_pieces = pieces.clone()
+        # host mirrors of each token's piece count and of the prefix sizes: refine's byte count needs
+        # no device read; only the gather kernel changes the device pieces, and refine updates both
+        self._pieces_h = pieces.cpu().numpy().astype(np.int64)
+        self._prefix_h = tables.prefix64.cpu().numpy()
         self._stage_off = None  # host cold tier: device offsets of the staged cold blobs, by token
-        self._staged = None     # host cold tier: the last staging buffer (pinned) and its device copy
+        self._stage_host = None  # host cold tier: pinned staging buffer, reused by every refine
+        self._stage_dev = None   # ... its device copy
+        self._stage_done = None  # ... an event after the last copy out of it
 
     @property
     def cold_on_host(self) -> bool:
@@ -110,6 +116,10 @@ class PackedStream:
         self.cold_off = self.cold_off.cpu()
         self._cold_size0 = (self.tables.full_bytes - self.tables.prefix64[self.initial_pieces.long()]).cpu()
         self._stage_off = torch.zeros(self.n, dtype=torch.int64, device=self.blob.device)
+        # staging for refine, sized for the refine capacity now so that a question allocates nothing
+        room = max(self.refine_capacity * self.tables.full_bytes, 16)
+        self._stage_host = torch.empty(room, dtype=torch.uint8, pin_memory=True)
+        self._stage_dev = torch.empty(room, dtype=torch.uint8, device=self.blob.device)
 
     @property
     def n(self) -> int:
@@ -178,44 +188,59 @@ class PackedStream:
         if self.cold is None:
             raise ValueError("this stream was packed without a cold tier")
         device = self.blob.device
-        rows_h = rows.detach().to("cpu", torch.int64).numpy()  # a question selects a few hundred rows
+        # one device read: the rows themselves (a question selects a few hundred); the byte count
+        # comes from the host mirror of the pieces
+        rows_h = rows.detach().to("cpu", torch.int64).numpy()
         if rows_h.min() < 0 or rows_h.max() >= self.n:
             raise ValueError(f"refine rows must lie in 0..{self.n - 1} (got {rows_h.min()}..{rows_h.max()})")
-        rows = rows.to(device=device, dtype=torch.int32).contiguous()
-        fetched = (self.tables.full_bytes - self.tables.prefix64[self.pieces[rows.long()].long()]).sum()
-        distinct = np.unique(rows_h)
-        if distinct.size != rows_h.size:
-            rows = torch.from_numpy(distinct.astype(np.int32)).to(device)
+        fetched = int((self.tables.full_bytes - self._prefix_h[self._pieces_h[rows_h]]).sum())
+        rows_np = np.unique(rows_h)  # rows_np and rows list the same tokens in the same order
+        if rows_np.size != rows_h.size:
+            rows = torch.from_numpy(rows_np.astype(np.int32)).to(device)
+        else:
+            rows_np = rows_h
+            rows = rows.to(device=device, dtype=torch.int32).contiguous()
         k = rows.numel()
         if self.refined + k > self.refine_capacity:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
         base = self.hot_used + self.refined * self.tables.full_bytes
         cold, cold_off = self.cold, self.cold_off
         if self.cold_on_host:
-            cold, cold_off = self._stage_cold(rows)
+            cold, cold_off = self._stage_cold(rows_np, rows)
         dkv_hip.gather_cold(self.c_stream(), cold, cold_off, rows, base, self.blob, self.tok_off, self.pieces)
+        self._pieces_h[rows_np] = self.tables.pieces
         self.refined += k
         self.version += 1
-        return int(fetched)
+        return fetched
 
-    def _stage_cold(self, rows: torch.Tensor):
-        """Host cold tier: gather the cold blobs of ``rows`` into one pinned buffer, copy it to the
-        device (one host-to-device transfer), and point each row's cold offset into the copy."""
-        rows_h = rows.cpu().long()
+    def _stage_cold(self, rows_np: np.ndarray, rows: torch.Tensor):
+        """Host cold tier: gather the cold blobs of the distinct ``rows`` (host copy ``rows_np``, in
+        the same order) into the pinned staging buffer, copy it to the device (one host-to-device
+        transfer), and point each row's cold offset into the copy.  The buffers are kept and grow
+        only when a refine needs more; before the host writes the pinned buffer again it waits for
+        the previous copy out of it."""
+        rows_h = torch.from_numpy(np.ascontiguousarray(rows_np, dtype=np.int64))
         start = self.cold_off[rows_h].numpy()
         size = self._cold_size0[rows_h].numpy()
-        dst = np.zeros(size.size, np.int64)
-        np.cumsum(size[:-1], out=dst[1:])
-        staged = torch.empty(max(int(size.sum()), 16), dtype=torch.uint8, pin_memory=True)
-        cold_np, staged_np = self.cold.numpy(), staged.numpy()
-        for a, d, n in zip(start.tolist(), dst.tolist(), size.tolist()):  # one slice copy per token
-            staged_np[d:d + n] = cold_np[a:a + n]
-        dst = torch.from_numpy(dst)
+        dst = np.zeros(size.size + 1, np.int64)
+        np.cumsum(size, out=dst[1:])
+        used = int(dst[-1])
         device = self.blob.device
-        staged_dev = staged.to(device, non_blocking=True)
-        self._stage_off[rows.long()] = dst.to(device, non_blocking=True)
-        self._staged = (staged, staged_dev)  # both stay alive until the next refine
-        return staged_dev, self._stage_off
+        if self._stage_host is None or self._stage_host.numel() < max(used, 16):
+            self._stage_host = torch.empty(max(used, 16), dtype=torch.uint8, pin_memory=True)
+            self._stage_dev = torch.empty(max(used, 16), dtype=torch.uint8, device=device)
+        elif self._stage_done is not None:
+            self._stage_done.synchronize()
+        if used:
+            # one block copy per row (the pinned cold tier is best read in whole runs, not byte by byte)
+            cold_np, staged_np = self.cold.numpy(), self._stage_host.numpy()
+            for a, d, n in zip(start.tolist(), dst[:-1].tolist(), size.tolist()):
+                staged_np[d:d + n] = cold_np[a:a + n]
+            self._stage_dev[:used].copy_(self._stage_host[:used], non_blocking=True)
+        self._stage_done = torch.cuda.Event()
+        self._stage_done.record()
+        self._stage_off[rows.long()] = torch.from_numpy(dst[:-1]).to(device, non_blocking=True)
+        return self._stage_dev, self._stage_off
 
 
 LADDER_GROUP = 64
