@@ -2224,37 +2224,72 @@ DKV_DEVICE uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+constexpr int kTopkCache = 32;  // elements per thread kept in registers (n <= 32,768); larger n reloads
+
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restrict__ s, int n, int k,
                                                             int32_t* __restrict__ out) {
-  __shared__ uint32_t hist[256];
+  constexpr int kWaves = kTopkThreads / 64;
+  __shared__ uint32_t hist[kWaves][256];  // one histogram per wave: fewer LDS atomic collisions
   __shared__ uint32_t sh_prefix, sh_k;
   __shared__ int scan_g[kTopkThreads];
   __shared__ int scan_e[kTopkThreads];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (n + kTopkThreads - 1) / kTopkThreads;
   const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+  const bool cached = per <= kTopkCache;
+  uint32_t key[kTopkCache];
+#pragma unroll
+  for (int j = 0; j < kTopkCache; ++j) key[j] = cached ? order_key(s[min(i0 + j, n - 1)]) : 0u;  // n >= 1
+  auto key_at = [&](int j) { return cached ? key[j] : order_key(s[i0 + j]); };
   uint32_t prefix = 0, pmask = 0;
   uint32_t kk = (uint32_t)k;
   for (int shift = 24; shift >= 0; shift -= 8) {
-    if (tid < 256) hist[tid] = 0;
+    for (int e = tid; e < kWaves * 256; e += kTopkThreads) (&hist[0][0])[e] = 0;
     __syncthreads();
-    for (int i = i0; i < i1; ++i) {
-      const uint32_t u = order_key(s[i]);
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+    if (cached) {
+#pragma unroll
+      for (int j = 0; j < kTopkCache; ++j)
+        if (i0 + j < i1 && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1u);
+    } else {
+      for (int i = i0; i < i1; ++i) {
+        const uint32_t u = order_key(s[i]);
+        if ((u & pmask) == prefix) atomicAdd(&hist[wave][(u >> shift) & 255u], 1u);
+      }
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t cum = 0;
-      int bsel = 0;
-      for (int bb = 255; bb >= 0; --bb) {
-        if (cum + hist[bb] >= kk) {
-          bsel = bb;
-          break;
-        }
-        cum += hist[bb];
+    if (wave == 0) {
+      // lane l owns buckets 255 - 4l .. 252 - 4l (descending); suffix counts by a wave scan
+      uint32_t c[4], tot = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += hist[w][255 - 4 * lane - j];
+        c[j] = v;
+        tot += v;
       }
-      sh_k = kk - cum;
-      sh_prefix = prefix | ((uint32_t)bsel << shift);
+      uint32_t incl = tot;  // inclusive scan over lanes (higher buckets first)
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      const uint32_t before = incl - tot;
+      // the lane whose buckets take the count past kk holds the k-th key
+      if (before < kk && incl >= kk) {
+        uint32_t cum = before;
+        int bsel = 255 - 4 * lane - 3;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (cum + c[j] >= kk) {
+            bsel = 255 - 4 * lane - j;
+            break;
+          }
+          cum += c[j];
+        }
+        sh_k = kk - cum;
+        sh_prefix = prefix | ((uint32_t)bsel << shift);
+      }
     }
     __syncthreads();
     kk = sh_k;
@@ -2265,7 +2300,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   const uint32_t T = prefix;  // key of the k-th largest value
   int cg = 0, ce = 0;
   for (int i = i0; i < i1; ++i) {
-    const uint32_t u = order_key(s[i]);
+    const uint32_t u = key_at(i - i0);
     cg += u > T;
     ce += u == T;
   }
@@ -2288,7 +2323,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   // selected before this thread's range = greater elements + min(equal, need)
   int pos = g_before + min(eq_before, need_e);
   for (int i = i0; i < i1; ++i) {
-    const uint32_t u = order_key(s[i]);
+    const uint32_t u = key_at(i - i0);
     if (u > T) {
       out[pos++] = i;
     } else if (u == T) {

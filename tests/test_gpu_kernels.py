@@ -152,9 +152,12 @@ def test_topk_exact():
 
     print("[case] topk", flush=True)
     rng = np.random.default_rng(5)
-    for n, k in [(16348, 163), (1000, 1), (777, 777), (5000, 64)]:
+    # 40,000 > 32 x 1,024 elements: the kernel reloads them from memory instead of its register cache
+    for n, k in [(16348, 163), (1000, 1), (777, 777), (5000, 64), (40000, 400), (2048, 100)]:
         s = rng.standard_normal(n).astype(np.float32)
         s[rng.integers(0, n, 50)] = s[0]  # ties resolve by lower index
+        if n == 2048:
+            s[:] = 0.25  # every key equal: the lowest k indices
         out = torch.empty(k, dtype=torch.int32, device=DEV)
         dkv_hip.topk(torch.from_numpy(s).to(DEV), k, out)
         torch.cuda.synchronize()
