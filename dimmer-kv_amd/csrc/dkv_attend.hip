@@ -1159,6 +1159,7 @@ struct K3aArgs {
   const float* tile_max;
   float* w_part;
   int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
+  int total_wg, per_xcd;  // workgroups, and consecutive workgroup indices per XCD
 };
 
 // ---------------------------------------------------------------------------
@@ -1333,7 +1334,10 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   __shared__ float Mrow[32];
   __shared__ __attribute__((aligned(16))) float2 saff[kK3Waves][kK3WaveTok];  // (scale, offset) of each wave's tokens
 
-  const int bid = blockIdx.x;
+  // consecutive workgroup indices on one XCD: the group workgroups of a split share its
+  // probability rows, which that XCD's L2 then fetches once
+  const int bid = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (bid >= a.total_wg) return;
   const int rbk = bid % a.row_blocks;
   const int g = (bid / a.row_blocks) % a.G;
   const int sp = bid / (a.row_blocks * a.G);
@@ -1857,8 +1861,9 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.rank = a->rank;
     k.nsplits = L.nsplits;
     k.row_blocks = (L.R_total + 31) / 32;
-    const long blocks = (long)L.nsplits * k.row_blocks * G;
-    hipLaunchKernelGGL(value_weights_kernel, dim3((unsigned)blocks), dim3(kK3Waves * 64), 0, st, k);
+    k.total_wg = L.nsplits * k.row_blocks * G;
+    k.per_xcd = (k.total_wg + 7) / 8;
+    hipLaunchKernelGGL(value_weights_kernel, dim3(8u * (unsigned)k.per_xcd), dim3(kK3Waves * 64), 0, st, k);
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
   }
