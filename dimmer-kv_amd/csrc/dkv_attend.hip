@@ -1462,9 +1462,12 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// K3b: one workgroup per (sequence, KV head, 128-component chunk): sum the
-// value partials over the sequence's splits, multiply once by the value-basis
-// chunk [128][D].
+// K3b: one workgroup per (sequence, KV head, 128-component chunk, 64-dimension
+// slice): sum the head's value partials over the sequence's splits, multiply
+// once by the value-basis block [128 components][64 dimensions].  Thread
+// (dp, part) holds dimension pair dp of the slice for components part * 16
+// .. +16; the head's rows go in passes of NR (4 covers a decoding step's rows:
+// GQA group x q_len <= 4).
 // ---------------------------------------------------------------------------
 struct K3bArgs {
   const int32_t* cu_seqlens;
@@ -1474,96 +1477,102 @@ struct K3bArgs {
   int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
 };
 
+constexpr int kK3bParts = 8;                  // component parts of a chunk
+constexpr int kK3bComp = kChunk / kK3bParts;  // 16 components per thread
+constexpr int kK3bDims = 64;                  // dimensions per workgroup
+
+template <int NR>
 __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
-  __shared__ __attribute__((aligned(16))) float W[8][kChunk];
-  __shared__ float red[4][8][130];
+  __shared__ __attribute__((aligned(16))) float W[NR][kChunk];  // the pass's summed weights
+  __shared__ float red[kK3bParts][NR][kK3bDims + 2];             // per-part outputs
+  const int nds = a.D / kK3bDims;
   const int bid = blockIdx.x;
-  const int c = bid % a.nchunks;
-  const int h = (bid / a.nchunks) % a.Hkv;
-  const int b = bid / (a.nchunks * a.Hkv);
+  const int ds = bid % nds;
+  const int c = (bid / nds) % a.nchunks;
+  const int h = (bid / (nds * a.nchunks)) % a.Hkv;
+  const int b = bid / (nds * a.nchunks * a.Hkv);
   const int tid = threadIdx.x;
-  const int gq = a.Hq / a.Hkv;
-  const int RH = gq * a.q_len;
+  const int RH = (a.Hq / a.Hkv) * a.q_len;
   const int sp0 = tiles_before(a.cu_seqlens, b, kSplitTok);
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
   const int nsp = (sr.y - sr.x + kSplitTok - 1) / kSplitTok;
   const int D = a.D;
   const int npair = D / 2;
-  const int parts = 256 / npair;  // 4 (D=128) or 8 (D=64)
-  const int dp = tid % npair, part = tid / npair;
-  const int ilen = kChunk / parts;
-  const uint32_t* bv = (const uint32_t*)(a.value_basis + (((long)a.layer * a.Hkv + h) * a.rank + (long)c * kChunk) * D);
-  // The basis chunk (shared by every row) and the first rows' split partials go out in one round:
-  // loads are unconditional (clamped indices), because a load under a per-element condition
-  // compiles to its own branch and wait.  Thread (dp, part) holds components part * ilen .. +ilen
-  // of dimension pair dp.
-  uint32_t bw[kChunk / 4];
+  const int dp = tid & 31, part = tid >> 5;
+  // the basis block and the first pass's split partials go out in one round; thread (dp, part)
+  // holds components part * 16 + ii of dimension pair ds * 32 + dp, one dword each
+  const uint32_t* bv = (const uint32_t*)(a.value_basis + (((long)a.layer * a.Hkv + h) * a.rank + (long)c * kChunk +
+                                                         part * kK3bComp) * D) + ds * (kK3bDims / 2) + dp;
+  uint32_t bw[kK3bComp];
 #pragma unroll
-  for (int ii = 0; ii < kChunk / 4; ++ii) bw[ii] = bv[(long)(part * ilen + min(ii, ilen - 1)) * npair + dp];
+  for (int ii = 0; ii < kK3bComp; ++ii) bw[ii] = bv[(long)ii * npair];
   const long sp_stride4 = (long)a.R_total * a.rank / 4;  // split stride in float4 units
-  const int rr = tid >> 5, k4 = tid & 31;                // the W element (row rr, components 4 k4 .. +4)
-  for (int r0 = 0; r0 < RH; r0 += 8) {
-    const int nr = min(8, RH - r0);
-    if (r0 > 0) __syncthreads();  // W and red are reused; no barrier (and wait) before the first loads
+  const int rr = tid >> 5, k4 = tid & 31;                // the W element of this thread: row rr, components 4 k4 ..
+  // one pass over rows r0 .. r0 + NR - 1 (the first pass is not inside the loop: hoisted out of a
+  // loop, the basis conversions below would wait for the basis loads before the split loads go out)
+  auto pass = [&](int r0) {
+    const int nr = min(NR, RH - r0);
     // W[rr][4 k4 ..] = sum over the sequence's splits, in split order (16 loads per batch in flight)
-    const float4* src = (const float4*)(a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + min(rr, nr - 1)) * a.rank +
-                                        (long)c * kChunk) + k4;
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < nsp; s0 += 16) {
-      float4 v[16];
+    if (rr < nr) {
+      const float4* src = (const float4*)(a.w_part + ((long)sp0 * a.R_total + (long)h * RH + r0 + rr) * a.rank +
+                                          (long)c * kChunk) + k4;
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int s0 = 0; s0 < nsp; s0 += 16) {
+        float4 v[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = src[(long)min(s0 + k, nsp - 1) * sp_stride4];
+        for (int k = 0; k < 16; ++k) v[k] = src[(long)min(s0 + k, nsp - 1) * sp_stride4];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {  // past the last split the (finite) repeat is added as exactly 0
-        const float keep = s0 + k < nsp ? 1.0f : 0.0f;
-        sum.x += v[k].x * keep;
-        sum.y += v[k].y * keep;
-        sum.z += v[k].z * keep;
-        sum.w += v[k].w * keep;
-      }
-    }
-    if (rr < nr) *(float4*)&W[rr][4 * k4] = sum;
-    __syncthreads();
-    float acc0[8], acc1[8];
-#pragma unroll
-    for (int rr = 0; rr < 8; ++rr) acc0[rr] = acc1[rr] = 0.0f;
-#pragma unroll
-    for (int ii = 0; ii < kChunk / 4; ++ii) {
-      if (ii >= ilen) break;
-      const int i = part * ilen + ii;
-      const float b0 = half_bits_to_float((uint16_t)(bw[ii] & 0xffffu));
-      const float b1 = half_bits_to_float((uint16_t)(bw[ii] >> 16));
-#pragma unroll
-      for (int rr = 0; rr < 8; ++rr) {
-        acc0[rr] += W[rr][i] * b0;
-        acc1[rr] += W[rr][i] * b1;
-      }
-    }
-    if (parts > 4) {
-      if (part >= 4)
-        for (int rr = 0; rr < 8; ++rr) {
-          red[part - 4][rr][2 * dp] = acc0[rr];
-          red[part - 4][rr][2 * dp + 1] = acc1[rr];
+        for (int k = 0; k < 16; ++k) {  // past the last split the (finite) repeat is added as exactly 0
+          const float keep = s0 + k < nsp ? 1.0f : 0.0f;
+          sum.x += v[k].x * keep;
+          sum.y += v[k].y * keep;
+          sum.z += v[k].z * keep;
+          sum.w += v[k].w * keep;
         }
-      __syncthreads();
-      if (part < 4)
-        for (int rr = 0; rr < 8; ++rr) {
-          acc0[rr] += red[part][rr][2 * dp];
-          acc1[rr] += red[part][rr][2 * dp + 1];
-        }
-      __syncthreads();
-    }
-    if (part < 4)
-      for (int rr = 0; rr < 8; ++rr) {
-        red[part][rr][2 * dp] = acc0[rr];
-        red[part][rr][2 * dp + 1] = acc1[rr];
       }
-    __syncthreads();
-    for (int e = tid; e < nr * D; e += 256) {
-      const int rr = e / D, dd = e % D;
-      const float s = red[0][rr][dd] + red[1][rr][dd] + red[2][rr][dd] + red[3][rr][dd];
-      a.out_part[(((long)c * a.batch + b) * a.R_total + (long)h * RH + r0 + rr) * D + dd] = s;
+      *(float4*)&W[rr][4 * k4] = sum;
     }
+    __syncthreads();
+    // rows nr .. NR - 1 of W hold stale values; their sums are computed and never stored
+    float acc0[NR], acc1[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc0[r] = acc1[r] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kK3bComp / 4; ++q) {
+      float4 w4[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) w4[r] = *(const float4*)&W[r][part * kK3bComp + 4 * q];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t bb = bw[4 * q + e];
+        const float b0 = half_bits_to_float((uint16_t)(bb & 0xffffu));
+        const float b1 = half_bits_to_float((uint16_t)(bb >> 16));
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const float wv = e == 0 ? w4[r].x : e == 1 ? w4[r].y : e == 2 ? w4[r].z : w4[r].w;
+          acc0[r] += wv * b0;
+          acc1[r] += wv * b1;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      red[part][r][2 * dp] = acc0[r];
+      red[part][r][2 * dp + 1] = acc1[r];
+    }
+    __syncthreads();
+    for (int e = tid; e < nr * kK3bDims; e += 256) {
+      const int r = e / kK3bDims, dd = e % kK3bDims;
+      float s = 0.0f;
+#pragma unroll
+      for (int p = 0; p < kK3bParts; ++p) s += red[p][r][dd];
+      a.out_part[(((long)c * a.batch + b) * a.R_total + (long)h * RH + r0 + r) * D + ds * kK3bDims + dd] = s;
+    }
+  };
+  pass(0);
+  for (int r0 = NR; r0 < RH; r0 += NR) {
+    __syncthreads();  // W and red are reused
+    pass(r0);
   }
 }
 
@@ -1882,8 +1891,11 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.rank = a->rank;
   kb.R_total = L.R_total;
   kb.nchunks = L.nchunks;
-  const long k3b_blocks = (long)a->batch * a->kv_heads * L.nchunks;
-  hipLaunchKernelGGL(basis_apply_kernel, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
+  const long k3b_blocks = (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
+  if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
+    hipLaunchKernelGGL(basis_apply_kernel<4>, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
+  else
+    hipLaunchKernelGGL(basis_apply_kernel<8>, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
   rc = dkv::check_launch("basis_apply");
   if (rc) return rc;
   // K3c: one workgroup per (sequence, output row)
