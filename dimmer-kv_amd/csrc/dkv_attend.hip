@@ -1116,11 +1116,14 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
   for (int w = 0; w < NW; ++w) Le += wred[NW + w];
   const float denom = ec * Lc + Le;
   // exact values: thread (d, part) takes tokens part, part + parts, ...
+  // every weight read is unconditional (a read under a per-element condition is a branch and a wait
+  // each); the select drops the products of slots past the exact tokens, whatever they hold
   float ve = 0.0f;
 #pragma unroll
   for (int i = 0; i < kExactVB; ++i) {
     const int j = part + i * parts;
-    if (j < E) ve += se[j] * vv[i];
+    const float prod = se[min(j, kMaxExact - 1)] * vv[i];
+    ve += j < E ? prod : 0.0f;
   }
   for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
     float v8[8];
