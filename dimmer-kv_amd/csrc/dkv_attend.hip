@@ -594,8 +594,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     }                                                                                  \
   } while (0)
 
-  // Branch-free loop (group indices past the end are clamped; the surplus
-  // basis block lands in a buffer nobody reads).  Ping-pong: the two row
+  // Main loop, two groups per iteration.  Ping-pong: the two row
   // halves (waves 0-3 and 4-7, one of each on every SIMD) each load and read
   // only their own 128 basis rows, and alternate MFMA segments with memory
   // segments (LDS writes of the next block, next loads), one barrier apart:
@@ -611,8 +610,11 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   DKV_K2_ISSUE_A(gb + 1, af1);
   __syncthreads();
   if (hs == 1) __builtin_amdgcn_s_barrier();
-  for (int g = gb; g < ge; g += 2) {  // ge - gb is even (the rank is a multiple of 256; a slice an even count)
-    const int g2 = min(g + 2, ge - 1), g3 = min(g + 3, ge - 1);
+  // ge - gb is even (the rank is a multiple of 256; a slice an even count).  The last two groups run
+  // after the loop, which loads nothing more: loads past the end would only repeat the last group and
+  // hold up the epilogue's loads behind them (a branch around them in the loop costs more: the
+  // compiler then waits for every load at the join).
+  for (int g = gb; g < ge - 2; g += 2) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(0, af0);
@@ -620,8 +622,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     DKV_K2_FINISH(1);
-    DKV_K2_ISSUE_B(g2);
-    DKV_K2_ISSUE_A(g2, af0);
+    DKV_K2_ISSUE_B(g + 2);
+    DKV_K2_ISSUE_A(g + 2, af0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
@@ -630,10 +632,25 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     DKV_K2_FINISH(0);
-    DKV_K2_ISSUE_B(g3);
-    DKV_K2_ISSUE_A(g3, af1);
+    DKV_K2_ISSUE_B(g + 3);
+    DKV_K2_ISSUE_A(g + 3, af1);
     __syncthreads();
   }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(1);
+  DKV_K2_MFMA(0, af0);
+  __builtin_amdgcn_s_setprio(0);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  DKV_K2_FINISH(1);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(1);
+  DKV_K2_MFMA(1, af1);
+  __builtin_amdgcn_s_setprio(0);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __syncthreads();
   if (hs == 0) __builtin_amdgcn_s_barrier();
 #undef DKV_K2_ISSUE_A
 #undef DKV_K2_ISSUE_B
