@@ -958,16 +958,12 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 
 // ---------------------------------------------------------------------------
 // K3c: one workgroup per (sequence, output row).  It merges the tiles'
-// softmax statistics of the compressed part with the exact tokens (sinks,
-// recent window, new tokens) in one softmax and writes the row's output
-//   out = (e_c * (sum of the chunk partials) + e_c * L_c * mean_v
-//          + sum_e p_e * v_e) / (e_c * L_c + L_e),  e_c = exp(M_c - M).
-// This is a chain of dependent steps, so every global load it needs (tile
-// statistics, query, exact keys and values, mean, chunk partials) is issued
-// in one round at the start, when the memory system is quiet: after the
-// bulk value streaming of K3a has drained.
+// softmax statistics of the compressed part with the exact tokens' (sinks,
+// recent window, new tokens; computed beside K3b, row_exact) in one softmax
+// and writes the row's output.
 // ---------------------------------------------------------------------------
 constexpr int kMaxExact = 1024;
+constexpr int kRowThreads = 256;  // threads of a row workgroup (the exact tail in K3b, the merge in K3c)
 
 struct RowMergeArgs {
   const int32_t* cu_seqlens;
@@ -980,6 +976,7 @@ struct RowMergeArgs {
   const float* mask;
   const void* query;
   const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
+  float* ex;              // [batch * R_total][D + 2] per row: Me, Le, then ve[D] (the exact tail, K3b)
   void* out;              // [batch][q_len][Hq][D], out_dtype
   float scaling;
   int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
@@ -990,15 +987,18 @@ constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded
 
 constexpr int kChunkLoads = 8;  // chunk partials per thread issued in the first round
 
+// The exact tail of one output row (workgroup wg = b * R_total + row), in extra workgroups of K3b:
+// the row's scores against its sequence's exact tokens (mask added), their maximum Me,
+// Le = sum_e exp(s_e - Me) and ve[d] = sum_e exp(s_e - Me) v_e[d], written to ex[wg] as (Me, Le, ve).
+// It needs only the query and the exact tokens, so it runs beside K3b's chunk workgroups (their
+// registers and LDS leave room on every CU) instead of on the finish kernel's critical path.
 template <int NT>
-__device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
+__device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
   constexpr int NW = NT / 64;
   float* q = smem;               // [128] the query row
   float* se = q + 128;           // [kMaxExact] exact scores, then weights
   float* wred = se + kMaxExact;  // [2][NW] per-wave maxima and sums
   float* buf = wred + 2 * NW;    // [NT] per-thread exact value sums
-  float* bc = buf + NT;          // [2] the compressed part's (max, sum)
-  float* cbuf = bc + 2;          // [NT] per-thread chunk-partial sums
   const int row = wg % a.R_total;
   const int b = wg / a.R_total;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1012,24 +1012,8 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
   // Every global load goes out in one round before any value is used: each dependent round trip
   // to memory costs microseconds here, and this work is nothing but them.  Loads under a
   // per-element condition compile to one branch and one wait per load, so they are
-  // unconditional (clamped indices, valid dummy addresses) or under one uniform branch.
-  // (1) the tiles' softmax statistics (wave 0, 4 tiles per lane), (2) the query, (3) a quarter key
-  // row (token tid / 4, 32 dimensions), (4) exact values, (5) chunk partials and the mean.
-  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
-  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
-  const float* tm = ntb > 0 ? a.tile_max + (long)row * a.ntiles + tb0 : a.mean_v;
-  const float* ts = ntb > 0 ? a.tile_sum + (long)row * a.ntiles + tb0 : a.mean_v;
-  float m4[4], s4[4];
-  if (wave == 0) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int t = min(lane + 64 * k, max(ntb - 1, 0));
-      m4[k] = tm[t];
-      s4[k] = ts[t];
-    }
-  }
-  // the query element, converted later
+  // unconditional (clamped indices) or under one uniform branch: the query element, a quarter key
+  // row (token tid / 4, 32 dimensions), the exact values.
   const long qidx = (((long)b * a.Hq + qh) * a.q_len + qi) * D + d;
   const uint32_t qword = load_query_word(a.query, qidx, a.query_dtype);
   const int kj = tid >> 2, ks = tid & 3;
@@ -1050,41 +1034,9 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
 #pragma unroll
     for (int i = 0; i < kExactVB; ++i) vv[i] = 0.0f;
   }
-  // thread (d, part) sums the chunk partials part, part + parts, ... of output d
-  const long rows_all = (long)a.batch * a.R_total;
-  const float* cp = a.out_part + (long)wg * D + d;
-  float cv[kChunkLoads];
-#pragma unroll
-  for (int i = 0; i < kChunkLoads; ++i) cv[i] = cp[(long)min(part + i * parts, a.nchunks - 1) * rows_all * D];
-  const float mv = a.mean_v[((long)a.layer * a.Hkv + h) * D + d];
-  // now the values: the compressed part's online (max, sum) over this lane's tiles
-  float mm = -INFINITY, ll = 0.0f;
-  if (wave == 0) {
-    auto merge = [&](float mt, float st) {
-      if (mt == -INFINITY) return;
-      if (mt > mm) {
-        ll = ll * __expf(mm - mt) + st;
-        mm = mt;
-      } else {
-        ll += st * __expf(mt - mm);
-      }
-    };
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
-    for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
-  }
   if (tid < D) q[tid] = query_word_value(qword, qidx, a.query_dtype);
-  if (wave == 0) {
-    const float m = wave_max(mm);
-    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
-    if (lane == 0) {
-      bc[0] = m;
-      bc[1] = l;
-    }
-  }
   __syncthreads();
-  // exact scores: four lanes per token, 32 dimensions each, NT / 4 tokens per pass
+  // scores: four lanes per token, 32 dimensions each, NT / 4 tokens per pass
   float me = -INFINITY;
   constexpr int TPP = NT / 4;
   const int Epad = (E + TPP - 1) / TPP * TPP;
@@ -1113,28 +1065,21 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
   me = wave_max(me);
   if (lane == 0) wred[wave] = me;
   __syncthreads();
-  const float Mc = bc[0], Lc = bc[1];
   float Me = wred[0];
 #pragma unroll
   for (int w = 1; w < NW; ++w) Me = fmaxf(Me, wred[w]);
-  const float M = fmaxf(Mc, Me);
-  const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
   float le = 0.0f;
   for (int j = tid; j < E; j += NT) {
-    const float wgt = (M == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - M);
+    const float wgt = (Me == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - Me);
     se[j] = wgt;
     le += wgt;
   }
   le = wave_sum(le);
   if (lane == 0) wred[NW + wave] = le;
   __syncthreads();
-  float Le = 0.0f;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) Le += wred[NW + w];
-  const float denom = ec * Lc + Le;
-  // exact values: thread (d, part) takes tokens part, part + parts, ...
-  // every weight read is unconditional (a read under a per-element condition is a branch and a wait
-  // each); the select drops the products of slots past the exact tokens, whatever they hold
+  // exact values: thread (d, part) takes tokens part, part + parts, ...; every weight read is
+  // unconditional (a read under a per-element condition is a branch and a wait each), the select
+  // drops the products of slots past the exact tokens, whatever they hold
   float ve = 0.0f;
 #pragma unroll
   for (int i = 0; i < kExactVB; ++i) {
@@ -1152,20 +1097,101 @@ __device__ void row_finish(const RowMergeArgs& a, int wg, float* smem) {
       if (j < E) ve += se[j] * v8[i];
     }
   }
+  buf[tid] = ve;
+  __syncthreads();
+  float* ex = a.ex + (long)wg * (D + 2);
+  if (tid < D) {
+    float ves = 0.0f;
+    for (int p = 0; p < parts; ++p) ves += buf[p * D + tid];
+    ex[2 + tid] = ves;
+  }
+  if (tid == 0) {
+    float Le = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) Le += wred[NW + w];
+    ex[0] = Me;
+    ex[1] = Le;
+  }
+}
+
+// The finish kernel's work for one output row: merge the compressed part's tile statistics with the
+// exact tail's (Me, Le) in one softmax and write the row's output
+//   out = (e_c * (sum of the chunk partials) + e_c * L_c * mean_v + e_e * ve) / (e_c * L_c + e_e * L_e),
+//   e_c = exp(M_c - M), e_e = exp(M_e - M), M = max(M_c, M_e).
+// All its loads (tile statistics, the exact results, the chunk partials, the mean) go out in one round.
+template <int NT>
+__device__ void row_merge(const RowMergeArgs& a, int wg, float* smem) {
+  float* bc = smem;      // [2] the compressed part's (max, sum)
+  float* cbuf = bc + 2;  // [NT] per-thread chunk-partial sums
+  const int row = wg % a.R_total;
+  const int b = wg / a.R_total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int D = a.D;
+  const int gq = a.Hq / a.Hkv;
+  const int qh = row / a.q_len, qi = row % a.q_len;
+  const int h = qh / gq;
+  const int d = tid % D, part = tid / D, parts = NT / D;
+  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
+  const float* tm = ntb > 0 ? a.tile_max + (long)row * a.ntiles + tb0 : a.mean_v;
+  const float* ts = ntb > 0 ? a.tile_sum + (long)row * a.ntiles + tb0 : a.mean_v;
+  float m4[4], s4[4];
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int t = min(lane + 64 * k, max(ntb - 1, 0));
+      m4[k] = tm[t];
+      s4[k] = ts[t];
+    }
+  }
+  const float* ex = a.ex + (long)wg * (D + 2);
+  const float2 mle = *(const float2*)ex;  // (Me, Le)
+  const float ve = ex[2 + d];
+  // thread (d, part) sums the chunk partials part, part + parts, ... of output d
+  const long rows_all = (long)a.batch * a.R_total;
+  const float* cp = a.out_part + (long)wg * D + d;
+  float cv[kChunkLoads];
+#pragma unroll
+  for (int i = 0; i < kChunkLoads; ++i) cv[i] = cp[(long)min(part + i * parts, a.nchunks - 1) * rows_all * D];
+  const float mv = a.mean_v[((long)a.layer * a.Hkv + h) * D + d];
+  if (wave == 0) {  // the compressed part's online (max, sum) over this lane's tiles
+    float mm = -INFINITY, ll = 0.0f;
+    auto merge = [&](float mt, float st) {
+      if (mt == -INFINITY) return;
+      if (mt > mm) {
+        ll = ll * __expf(mm - mt) + st;
+        mm = mt;
+      } else {
+        ll += st * __expf(mt - mm);
+      }
+    };
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (lane + 64 * k < ntb) merge(m4[k], s4[k]);
+    for (int t = lane + 256; t < ntb; t += 64) merge(tm[t], ts[t]);
+    const float m = wave_max(mm);
+    const float l = wave_sum(mm == -INFINITY ? 0.0f : ll * __expf(mm - m));
+    if (lane == 0) {
+      bc[0] = m;
+      bc[1] = l;
+    }
+  }
   float cs = 0.0f;
 #pragma unroll
   for (int i = 0; i < kChunkLoads; ++i) cs += part + i * parts < a.nchunks ? cv[i] : 0.0f;
   for (int c = part + kChunkLoads * parts; c < a.nchunks; c += parts) cs += cp[(long)c * rows_all * D];
-  buf[tid] = ve;
   cbuf[tid] = cs;
   __syncthreads();
   if (tid < D) {
-    float ves = 0.0f, csum = 0.0f;
-    for (int p = 0; p < parts; ++p) {
-      ves += buf[p * D + tid];
-      csum += cbuf[p * D + tid];
-    }
-    const float value = denom > 0.0f ? (ec * csum + ec * Lc * mv + ves) / denom : 0.0f;
+    float csum = 0.0f;
+    for (int p = 0; p < parts; ++p) csum += cbuf[p * D + tid];
+    const float Mc = bc[0], Lc = bc[1], Me = mle.x, Le = mle.y;
+    const float M = fmaxf(Mc, Me);
+    const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
+    const float ee = (M == -INFINITY || Me == -INFINITY) ? 0.0f : __expf(Me - M);
+    const float denom = ec * Lc + ee * Le;
+    const float value = denom > 0.0f ? (ec * csum + ec * Lc * mv + ee * ve) / denom : 0.0f;
     store_from_float(a.out, (((long)b * a.q_len + qi) * a.Hq + qh) * D + tid, a.out_dtype, value);
   }
 }
@@ -1495,18 +1521,26 @@ struct K3bArgs {
   const uint16_t* value_basis;
   float* out_part;
   int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
+  int n_exact_wg;  // leading workgroups that compute the exact tail of one output row each (row_exact)
 };
 
 constexpr int kK3bParts = 8;                  // component parts of a chunk
 constexpr int kK3bComp = kChunk / kK3bParts;  // 16 components per thread
 constexpr int kK3bDims = 64;                  // dimensions per workgroup
 
+// (at most two waves per SIMD: the exact-tail role's registers are not capped for occupancy)
 template <int NR>
-__global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
+__global__ __launch_bounds__(kRowThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
+  if ((int)blockIdx.x < a.n_exact_wg) {  // the exact tail of output row blockIdx.x
+    __shared__ float xsm[128 + kMaxExact + 2 * (kRowThreads / 64) + kRowThreads];
+    row_exact<kRowThreads>(ex, blockIdx.x, xsm);
+    return;
+  }
   __shared__ __attribute__((aligned(16))) float W[NR][kChunk];  // the pass's summed weights
   __shared__ float red[kK3bParts][NR][kK3bDims + 2];             // per-part outputs
   const int nds = a.D / kK3bDims;
-  const int bid = blockIdx.x;
+  const int bid = blockIdx.x - a.n_exact_wg;
   const int ds = bid % nds;
   const int c = (bid / nds) % a.nchunks;
   const int h = (bid / (nds * a.nchunks)) % a.Hkv;
@@ -1596,11 +1630,9 @@ __global__ __launch_bounds__(256) void basis_apply_kernel(K3bArgs a) {
   }
 }
 
-constexpr int kFinishThreads = 256;
-
-__global__ __launch_bounds__(kFinishThreads) void finish_kernel(RowMergeArgs a) {
-  __shared__ float smem[128 + kMaxExact + 2 * (kFinishThreads / 64) + 2 * kFinishThreads + 2];
-  row_finish<kFinishThreads>(a, blockIdx.x, smem);
+__global__ __launch_bounds__(kRowThreads) void finish_kernel(RowMergeArgs a) {
+  __shared__ float smem[2 + kRowThreads];
+  row_merge<kRowThreads>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1609,7 +1641,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RowMergeArgs a) 
 struct Layout {
   int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
   int ksplit;
-  size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, split_scores,
+  size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, exact, split_scores,
       total;
 };
 
@@ -1629,7 +1661,7 @@ inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
 }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][probabilities][tile statistics]
-// [split partials][chunk partials][K2 rank-slice partial scores].
+// [split partials][chunk partials][exact-tail results][K2 rank-slice partial scores].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 Layout make_layout(const dkv_attend_args_t* a) {
   Layout L{};
@@ -1661,6 +1693,8 @@ Layout make_layout(const dkv_attend_args_t* a) {
   off += align256((size_t)L.nsplits * L.R_total * a->rank * 4);
   L.out_part = off;
   off += align256((size_t)L.nchunks * a->batch * L.R_total * a->head_dim * 4);
+  L.exact = off;
+  off += align256((size_t)a->batch * L.R_total * (a->head_dim + 2) * 4);
   L.ksplit = k2_split(a, L.ntiles);
   L.split_scores = off;
   if (L.ksplit > 1) off += align256((size_t)L.ksplit * L.R_total * L.ntiles * kTileTok * 4);
@@ -1896,29 +1930,8 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
   }
-  K3bArgs kb{};
-  kb.cu_seqlens = a->cu_seqlens;
-  kb.w_part = (const float*)(ws + L.w_part);
-  kb.value_basis = a->value_basis;
-  kb.out_part = (float*)(ws + L.out_part);
-  kb.batch = a->batch;
-  kb.n_total = L.n_total;
-  kb.layer = a->layer;
-  kb.Hkv = a->kv_heads;
-  kb.Hq = a->q_heads;
-  kb.q_len = a->q_len;
-  kb.D = a->head_dim;
-  kb.rank = a->rank;
-  kb.R_total = L.R_total;
-  kb.nchunks = L.nchunks;
-  const long k3b_blocks = (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
-  if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
-    hipLaunchKernelGGL(basis_apply_kernel<4>, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
-  else
-    hipLaunchKernelGGL(basis_apply_kernel<8>, dim3((unsigned)k3b_blocks), dim3(256), 0, st, kb);
-  rc = dkv::check_launch("basis_apply");
-  if (rc) return rc;
-  // K3c: one workgroup per (sequence, output row)
+  // row arguments: the exact tail (extra K3b workgroups) and the merge (K3c), one workgroup per
+  // (sequence, output row)
   RowMergeArgs m{};
   m.cu_seqlens = a->cu_seqlens;
   m.cu_exact = a->cu_exact;
@@ -1931,6 +1944,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   m.mask = a->mask;
   m.query = a->query;
   m.out_part = (const float*)(ws + L.out_part);
+  m.ex = (float*)(ws + L.exact);
   m.out = a->out;
   m.out_dtype = a->out_dtype;
   m.nchunks = L.nchunks;
@@ -1947,7 +1961,31 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   m.R_total = L.R_total;
   m.E_total = E_total;
   m.query_dtype = a->query_dtype;
-  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kFinishThreads), 0, st, m);
+  K3bArgs kb{};
+  kb.cu_seqlens = a->cu_seqlens;
+  kb.w_part = (const float*)(ws + L.w_part);
+  kb.value_basis = a->value_basis;
+  kb.out_part = (float*)(ws + L.out_part);
+  kb.batch = a->batch;
+  kb.n_total = L.n_total;
+  kb.layer = a->layer;
+  kb.Hkv = a->kv_heads;
+  kb.Hq = a->q_heads;
+  kb.q_len = a->q_len;
+  kb.D = a->head_dim;
+  kb.rank = a->rank;
+  kb.R_total = L.R_total;
+  kb.nchunks = L.nchunks;
+  kb.n_exact_wg = a->batch * L.R_total;
+  const long k3b_blocks = kb.n_exact_wg + (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
+  if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
+    hipLaunchKernelGGL(basis_apply_kernel<4>, dim3((unsigned)k3b_blocks), dim3(kRowThreads), 0, st, kb, m);
+  else
+    hipLaunchKernelGGL(basis_apply_kernel<8>, dim3((unsigned)k3b_blocks), dim3(kRowThreads), 0, st, kb, m);
+  rc = dkv::check_launch("basis_apply");
+  if (rc) return rc;
+  // K3c
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kRowThreads), 0, st, m);
   return dkv::check_launch("finish");
 }
 
