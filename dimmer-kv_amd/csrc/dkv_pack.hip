@@ -531,14 +531,12 @@ extern "C" int dkv_quantize8(const float* coef, int32_t n, int32_t groups, uint8
 // K4c: merge hot + cold segments of selected tokens into full blobs.
 // One workgroup per selected token; one thread per group.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const uint8_t* __restrict__ cold,
-                                                         const int64_t* __restrict__ cold_tok_off,
-                                                         const int32_t* __restrict__ idx, uint8_t* __restrict__ refined,
-                                                         int64_t refined_base_off, int64_t* tok_off,
-                                                         int16_t* pieces) {
+// Merges token t's hot and cold segments into the full blob at refined + r * full_bytes and points the
+// stream at it (one workgroup; one thread per group).
+DKV_DEVICE void gather_token(const dkv_stream_t& s, const uint8_t* __restrict__ cold,
+                             const int64_t* __restrict__ cold_tok_off, int t, int r, uint8_t* __restrict__ refined,
+                             int64_t refined_base_off, int64_t* tok_off, int16_t* pieces) {
   const int G = s.order.groups, K = s.order.pieces;
-  const int r = blockIdx.x;
-  const int t = idx[r];
   const int k = pieces[t];
   const int64_t off = tok_off[t];
   const int full_bytes = s.order.prefix_bytes[K];
@@ -576,6 +574,58 @@ __global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const u
   }
 }
 
+
+__global__ __launch_bounds__(64) void gather_cold_kernel(dkv_stream_t s, const uint8_t* __restrict__ cold,
+                                                         const int64_t* __restrict__ cold_tok_off,
+                                                         const int32_t* __restrict__ idx, uint8_t* __restrict__ refined,
+                                                         int64_t refined_base_off, int64_t* tok_off,
+                                                         int16_t* pieces) {
+  gather_token(s, cold, cold_tok_off, idx[blockIdx.x], blockIdx.x, refined, refined_base_off, tok_off, pieces);
+}
+
+// ---------------------------------------------------------------------------
+// K4c over any token list, without a host round trip.  refine_prepare_kernel:
+// one thread per entry r of rows; in-range entries add the reference's cold
+// bytes (full size - hot prefix of the token's current pieces,
+// progressive.py:232) to fetched[0] and claim the token in owner[t] with the
+// key (version << 32) | (2^31 - 1 - r): the largest key of this version is the
+// token's first entry, and older versions' keys are smaller, so owner never
+// needs clearing.  An entry outside 0..n-1 sets fetched[1].  The gather then
+// runs one workgroup per entry and merges a token only from its first entry,
+// and none at all if fetched[1] is set.  Integer sums: the result does not
+// depend on the order in which entries are added.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void refine_prepare_kernel(const int32_t* __restrict__ rows, int k, int n,
+                                                             const int16_t* __restrict__ pieces,
+                                                             const int32_t* __restrict__ prefix_bytes, int K,
+                                                             int64_t* owner, int64_t version, int64_t* fetched) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= k) return;
+  const int t = rows[r];
+  if (t < 0 || t >= n) {
+    atomicOr((unsigned long long*)&fetched[1], 1ull);
+    return;
+  }
+  const int64_t bytes = (int64_t)prefix_bytes[K] - prefix_bytes[pieces[t]];
+  atomicAdd((unsigned long long*)&fetched[0], (unsigned long long)bytes);
+  atomicMax((unsigned long long*)&owner[t], (unsigned long long)((version << 32) | (int64_t)(0x7fffffff - r)));
+}
+
+__global__ __launch_bounds__(64) void gather_owned_kernel(dkv_stream_t s, const uint8_t* __restrict__ cold,
+                                                          const int64_t* __restrict__ cold_tok_off,
+                                                          const int32_t* __restrict__ rows, int n,
+                                                          uint8_t* __restrict__ refined, int64_t refined_base_off,
+                                                          int64_t* tok_off, int16_t* pieces,
+                                                          const int64_t* __restrict__ owner, int64_t version,
+                                                          const int64_t* __restrict__ fetched) {
+  const int r = blockIdx.x;
+  const int t = rows[r];
+  // uniform per workgroup: a bad list changes nothing; a repeated token is merged from its first entry
+  if (fetched[1] != 0 || t < 0 || t >= n) return;
+  if (owner[t] != ((version << 32) | (int64_t)(0x7fffffff - r))) return;
+  gather_token(s, cold, cold_tok_off, t, r, refined, refined_base_off, tok_off, pieces);
+}
+
 extern "C" int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const int64_t* cold_tok_off,
                                const int32_t* idx, int32_t k, uint8_t* refined, int64_t refined_base_off,
                                int64_t* tok_off, int16_t* pieces, void* stream) {
@@ -590,6 +640,29 @@ extern "C" int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const
   hipLaunchKernelGGL(gather_cold_kernel, dim3(k), dim3(64), 0, dkv::as_stream(stream), view, cold, cold_tok_off, idx,
                      refined, refined_base_off, tok_off, pieces);
   return dkv::check_launch("dkv_gather_cold");
+}
+
+extern "C" int dkv_refine_rows(const dkv_stream_t* s, int32_t n, const uint8_t* cold, const int64_t* cold_tok_off,
+                               const int32_t* rows, int32_t k, uint8_t* refined, int64_t refined_base_off,
+                               int64_t* tok_off, int16_t* pieces, int64_t* owner, int32_t version, int64_t* fetched,
+                               void* stream) {
+  int rc = dkv::check_stream(s, "dkv_refine_rows");
+  if (rc) return rc;
+  DKV_REQUIRE(s->format == DKV_FMT_PLANES, DKV_EINVAL, "dkv_refine_rows: only bit-plane streams have a cold tier");
+  DKV_REQUIRE(cold && cold_tok_off && rows && refined && tok_off && pieces && owner && fetched && s->order.cold_off,
+              DKV_EINVAL, "dkv_refine_rows: null pointer");
+  DKV_REQUIRE(n >= 0 && k >= 0 && refined_base_off >= 0 && version > 0, DKV_ESHAPE,
+              "dkv_refine_rows: bad n / k / offset / version");
+  if (k == 0) return DKV_OK;
+  const hipStream_t st = dkv::as_stream(stream);
+  hipLaunchKernelGGL(refine_prepare_kernel, dim3((unsigned)((k + 255) / 256)), dim3(256), 0, st, rows, k, n,
+                     (const int16_t*)pieces, s->order.prefix_bytes, s->order.pieces, owner, (int64_t)version, fetched);
+  rc = dkv::check_launch("dkv_refine_rows");
+  if (rc) return rc;
+  dkv_stream_t view = *s;
+  hipLaunchKernelGGL(gather_owned_kernel, dim3(k), dim3(64), 0, st, view, cold, cold_tok_off, rows, n, refined,
+                     refined_base_off, tok_off, pieces, (const int64_t*)owner, (int64_t)version, (const int64_t*)fetched);
+  return dkv::check_launch("dkv_refine_rows");
 }
 
 // ---------------------------------------------------------------------------

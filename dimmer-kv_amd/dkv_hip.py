@@ -28,7 +28,7 @@ EXPORTS = [
     "dkv_attend_layer",
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
-    "dkv_gather_cold", "dkv_wire_pack", "dkv_wire_unpack", "dkv_attend_layer_noalloc",
+    "dkv_gather_cold", "dkv_refine_rows", "dkv_wire_pack", "dkv_wire_unpack", "dkv_attend_layer_noalloc",
     "dkv_quantize8",
 ]
 NOALLOC_MAX_BYTES = 64 << 20  # DKV_NOALLOC_MAX_BYTES: the static workspace of dkv_attend_layer_noalloc
@@ -255,6 +255,18 @@ def score_layer(args: AttendArgs, key_question: torch.Tensor, importance: torch.
 def topk(scores: torch.Tensor, k: int, out: torch.Tensor) -> None:
     _check(lib().dkv_topk(c_vp(ptr(scores)), c_i32(scores.numel()), c_i32(k), c_vp(ptr(out)), c_vp(None), c_sz(0),
                           c_vp(stream_handle())), "dkv_topk")
+
+
+def refine_rows(stream: Stream, n: int, cold, cold_tok_off, rows, refined_base_off: int, blob, tok_off, pieces,
+                owner, version: int, fetched) -> None:
+    """K4c over any token list on the device (dkv_refine_rows): ``fetched`` [2] int64, zero on entry,
+    gets the reference's byte count and the out-of-range flag."""
+    k = rows.numel()
+    refined_ptr = ptr(blob) + refined_base_off
+    _check(lib().dkv_refine_rows(ctypes.byref(stream), c_i32(n), c_vp(ptr(cold)), c_vp(ptr(cold_tok_off)),
+                                 c_vp(ptr(rows)), c_i32(k), c_vp(refined_ptr), c_i64(refined_base_off),
+                                 c_vp(ptr(tok_off)), c_vp(ptr(pieces)), c_vp(ptr(owner)), c_i32(version),
+                                 c_vp(ptr(fetched)), c_vp(stream_handle())), "dkv_refine_rows")
 
 
 def gather_cold(stream: Stream, cold, cold_tok_off, idx, refined_base_off: int, blob, tok_off, pieces) -> None:

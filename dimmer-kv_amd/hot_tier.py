@@ -92,10 +92,12 @@ class PackedStream:
         self.refined = 0
         self.version = 0  # bumped whenever tokens change (refine), so decoded copies know to refresh
         self.initial_pieces = pieces.clone()
-        # host mirrors of each token's piece count and of the prefix sizes: refine's byte count needs
-        # no device read; only the gather kernel changes the device pieces, and refine updates both
+        # host mirrors of each token's piece count and of the prefix sizes, for the host cold tier's
+        # refine (it needs the rows on the host anyway); the device tier counts bytes on the device
         self._pieces_h = pieces.cpu().numpy().astype(np.int64)
         self._prefix_h = tables.prefix64.cpu().numpy()
+        self._owner = None  # device tier: per-token first-entry tags of dkv_refine_rows (never cleared)
+        self._refine_calls = 0
         self._stage_off = None  # host cold tier: device offsets of the staged cold blobs, by token
         self._stage_host = None  # host cold tier: pinned staging buffer, reused by every refine
         self._stage_dev = None   # ... its device copy
@@ -178,18 +180,49 @@ class PackedStream:
         """K4c: fetch the cold pieces of ``rows`` (stream-local) -> bytes fetched (progressive.py:232).
 
         The fetched count is taken over ``rows`` as given, a repeated row counting each time as in
-        the reference's formula; the gather itself runs over the distinct rows, because the kernel
-        repoints each row's blob and two blocks working on one row could pair one's old pieces with
-        the other's new offset.  Rows already at full precision cost nothing (their cold blob is
-        empty) and are merged like the others, so no host-side filtering is needed; the fetched
-        count is the only value read back."""
+        the reference's formula; each distinct row is merged once.  Rows already at full precision
+        cost nothing (their cold blob is empty) and are merged like the others.  Rows outside the
+        stream raise ValueError and change nothing."""
         if rows.numel() == 0:
             return 0
         if self.cold is None:
             raise ValueError("this stream was packed without a cold tier")
+        if self.cold_on_host:
+            return self._refine_host(rows)
+        counts = self.refine_async(rows).cpu()
+        if int(counts[1]):  # nothing was merged: give the slots back
+            self.refined -= rows.numel()
+            raise ValueError(f"refine rows must lie in 0..{self.n - 1}")
+        return int(counts[0])
+
+    def refine_async(self, rows: torch.Tensor) -> torch.Tensor:
+        """Device cold tier: ``refine`` without a host round trip (dkv_refine_rows).  Returns a device
+        int64 [2]: the bytes fetched and a flag set when a row lies outside the stream (then nothing
+        was merged); reading it is the caller's synchronisation.  Each distinct row's full blob goes
+        to the slot of its first entry, so the refined area grows by ``rows.numel()`` slots."""
+        if self.cold is None or self.cold_on_host:
+            raise ValueError("refine_async needs a device cold tier")
         device = self.blob.device
-        # one device read: the rows themselves (a question selects a few hundred); the byte count
-        # comes from the host mirror of the pieces
+        k = rows.numel()
+        if self.refined + k > self.refine_capacity:
+            raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
+        if self._owner is None:
+            self._owner = torch.zeros(max(self.n, 1), dtype=torch.int64, device=device)
+        self._refine_calls += 1
+        counts = torch.zeros(2, dtype=torch.int64, device=device)
+        if k:
+            rows32 = rows.to(device=device, dtype=torch.int32).contiguous()
+            base = self.hot_used + self.refined * self.tables.full_bytes
+            dkv_hip.refine_rows(self.c_stream(), self.n, self.cold, self.cold_off, rows32, base, self.blob,
+                                self.tok_off, self.pieces, self._owner, self._refine_calls, counts)
+            self.refined += k
+            self.version += 1
+        return counts
+
+    def _refine_host(self, rows: torch.Tensor) -> int:
+        """Host cold tier: the rows come to the host (the cold blobs are gathered there); the byte
+        count comes from the host mirror of the pieces; the gather runs over the distinct rows."""
+        device = self.blob.device
         rows_h = rows.detach().to("cpu", torch.int64).numpy()
         if rows_h.min() < 0 or rows_h.max() >= self.n:
             raise ValueError(f"refine rows must lie in 0..{self.n - 1} (got {rows_h.min()}..{rows_h.max()})")
@@ -204,9 +237,7 @@ class PackedStream:
         if self.refined + k > self.refine_capacity:
             raise ValueError(f"refine capacity {self.refine_capacity} tokens exceeded")
         base = self.hot_used + self.refined * self.tables.full_bytes
-        cold, cold_off = self.cold, self.cold_off
-        if self.cold_on_host:
-            cold, cold_off = self._stage_cold(rows_np, rows)
+        cold, cold_off = self._stage_cold(rows_np, rows)
         dkv_hip.gather_cold(self.c_stream(), cold, cold_off, rows, base, self.blob, self.tok_off, self.pieces)
         self._pieces_h[rows_np] = self.tables.pieces
         self.refined += k

@@ -159,9 +159,16 @@ class QuestionStage:
         return self.idx
 
     def gather(self) -> int:
-        """K4c on both streams; returns the bytes fetched (progressive.py:232)."""
-        rows = self.idx.long()
-        return sum(self.w.streams[k].refine(rows) for k in ("key", "value"))
+        """K4c on both streams; returns the bytes fetched (progressive.py:232).  With device cold
+        tiers both streams refine on the device and one read brings back both byte counts."""
+        streams = [self.w.streams[k] for k in ("key", "value")]
+        if any(st.cold_on_host for st in streams):
+            rows = self.idx.long()
+            return sum(st.refine(rows) for st in streams)
+        counts = (streams[0].refine_async(self.idx) + streams[1].refine_async(self.idx)).cpu()
+        if int(counts[1]):
+            raise ValueError("refine rows out of range")
+        return int(counts[0])
 
 
 def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, refine_capacity: int = 0,

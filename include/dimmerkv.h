@@ -306,6 +306,22 @@ int dkv_gather_cold(const dkv_stream_t* s, const uint8_t* cold, const int64_t* c
                     int32_t k, uint8_t* refined, int64_t refined_base_off, int64_t* tok_off, int16_t* pieces,
                     void* stream);
 
+/* ---- K4c for any token list, with the reference's byte count ------------
+ * Replaces scripts/progressive.py:224-236 refine (the fetched count of :232
+ * and the merge) for k tokens `rows` of a stream of n tokens that may repeat,
+ * without a host round trip: fetched[0] += sum over the k entries as given of
+ * full size - hot prefix of the token's pieces before the call (a repeated
+ * token counts each time, as in the reference); each distinct token is merged
+ * once, from its first entry r, into refined + r*full_bytes (so the refined
+ * area must hold k full blobs); an entry outside 0..n-1 sets fetched[1] and
+ * then no token is merged.  fetched[0..1] must be 0 on entry.  `owner` is an
+ * int64 [n] array kept by the caller, zero at first: each call tags it with
+ * `version`, which must be > 0 and grow from call to call on that array.
+ * Calls that overlap on one owner array race. */
+int dkv_refine_rows(const dkv_stream_t* s, int32_t n, const uint8_t* cold, const int64_t* cold_tok_off,
+                    const int32_t* rows, int32_t k, uint8_t* refined, int64_t refined_base_off, int64_t* tok_off,
+                    int16_t* pieces, int64_t* owner, int32_t version, int64_t* fetched, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -117,9 +117,11 @@ def test_refine_then_attend():
 @pytest.mark.parametrize("tier", ["device", "host"])
 def test_refine_with_repeated_rows(tier):
     """Rows given more than once: ``fetched`` counts each occurrence (the reference's formula over
-    the rows as given, scripts/progressive.py:232), the gather runs once per distinct row, and the
-    refined tier is byte for byte the tier refined with the distinct rows; rows outside the stream
-    raise before anything runs."""
+    the rows as given, scripts/progressive.py:232) and each distinct row is merged once.  The host
+    tier gathers the sorted distinct rows, so its refined tier is byte for byte the tier refined
+    with them; the device tier (dkv_refine_rows) puts each row at its first entry's slot, so its
+    tokens decode to the same values with the same pieces.  Rows outside the stream raise and
+    change nothing."""
     from hot_tier import OrderTables, PackedStream
 
     shape = synth.ModelShape(2, 8, 64, 32, 1024)
@@ -138,11 +140,19 @@ def test_refine_with_repeated_rows(tier):
     assert fetched == pr.fetched_bytes({"key": case.order}, {"key": case.pieces["key"]}, rows)
     b.refine(torch.from_numpy(np.unique(rows)).to(DEV))
     torch.cuda.synchronize()
-    assert a.refined == b.refined == len(np.unique(rows))
-    assert torch.equal(a.pieces, b.pieces) and torch.equal(a.tok_off, b.tok_off)
-    assert torch.equal(a.blob, b.blob)
+    assert torch.equal(a.pieces, b.pieces)
+    if tier == "host":
+        assert a.refined == b.refined == len(np.unique(rows))
+        assert torch.equal(a.tok_off, b.tok_off) and torch.equal(a.blob, b.blob)
+    else:
+        assert a.refined == len(rows) and b.refined == len(np.unique(rows))
+        assert torch.equal(a.dequantize(), b.dequantize())
+    state = (a.refined, a.pieces.clone(), a.tok_off.clone(), a.blob.clone())
     with pytest.raises(ValueError, match="refine rows"):
         a.refine(torch.tensor([0, case.ctx.middle], device=DEV))
+    torch.cuda.synchronize()
+    assert a.refined == state[0] and torch.equal(a.pieces, state[1]) and torch.equal(a.tok_off, state[2])
+    assert torch.equal(a.blob, state[3])
 
 
 def test_refine_from_host_cold_tier_matches_device_tier():
