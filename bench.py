@@ -181,16 +181,17 @@ def cpu_baseline(w, seconds: float):
 def question_stage(w):
     """The question before the decode (the configuration's first three steps): score the hot tier
     with 64 query tokens using the first 2 planes (28 layers), select the top 1 %, gather their
-    cold planes.  Scoring and selection are timed over 3 repetitions after one warm-up; the gather
+    cold planes.  Scoring and selection are timed over 10 repetitions after two warm-ups; the gather
     runs once (it changes the cache the decode then reads)."""
     import torch
 
     q = w.question
-    q.score()
-    q.select()
+    for _ in range(2):
+        q.score()
+        q.select()
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    reps = 3
+    reps = 10
     ev[0].record()
     for _ in range(reps):
         q.score()

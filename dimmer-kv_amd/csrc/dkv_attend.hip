@@ -73,6 +73,13 @@ DKV_DEVICE uint16_t f16_bits(float v) {
   return b;
 }
 
+// f16_bits(lo) | f16_bits(hi) << 16 as one v_cvt_pk_f16_f32 (both rounded to nearest even).
+DKV_DEVICE uint32_t pack_f16x2(float lo, float hi) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const half2_t v = {(half_t)lo, (half_t)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 DKV_DEVICE half8 lds_half8(const half_t* p) { return *(const half8*)p; }
 
 // The query type as a compile-time tag: a kernel section instantiated per type issues its query
@@ -135,6 +142,44 @@ DKV_DEVICE typename QueryFrag<T>::type load_query_frag(const void* q, long idx) 
     return load_query8_t<DKV_F32>(q, idx);
   else
     return *(const uint4*)((const uint16_t*)q + idx);
+}
+
+// 8 query elements as loaded, before conversion (two 16-byte words for fp32), so that a batch of
+// loads goes out before the first conversion waits for its data.
+template <int T>
+struct RawQuery8 {
+  uint4 w;
+};
+template <>
+struct RawQuery8<DKV_F32> {
+  float4 x, y;
+};
+
+template <int T>
+DKV_DEVICE RawQuery8<T> load_raw_query8(const void* q, long idx) {
+  RawQuery8<T> r;
+  if constexpr (T == DKV_F32) {
+    r.x = *(const float4*)((const float*)q + idx);
+    r.y = *(const float4*)((const float*)q + idx + 4);
+  } else {
+    r.w = *(const uint4*)((const uint16_t*)q + idx);
+  }
+  return r;
+}
+
+template <int T>
+DKV_DEVICE half8 query_frag_half(const typename QueryFrag<T>::type& f);
+
+template <int T>
+DKV_DEVICE half8 raw_query8_half(const RawQuery8<T>& r) {
+  if constexpr (T == DKV_F32) {
+    half8 h;
+    h[0] = (half_t)r.x.x; h[1] = (half_t)r.x.y; h[2] = (half_t)r.x.z; h[3] = (half_t)r.x.w;
+    h[4] = (half_t)r.y.x; h[5] = (half_t)r.y.y; h[6] = (half_t)r.y.z; h[7] = (half_t)r.y.w;
+    return h;
+  } else {
+    return query_frag_half<T>(r.w);
+  }
 }
 
 template <int T>
@@ -702,10 +747,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
           for (int e = 0; e < 4; e += 2) {
             const float klo0 = acc[tb][rb][v4 * 4 + e], khi0 = acc[tb][rb2][v4 * 4 + e];
             const float klo1 = acc[tb][rb][v4 * 4 + e + 1], khi1 = acc[tb][rb2][v4 * 4 + e + 1];
-            lo[e / 2] = (uint32_t)f16_bits(klo0 * cv[e] - khi0 * sv[e]) |
-                        ((uint32_t)f16_bits(klo1 * cv[e + 1] - khi1 * sv[e + 1]) << 16);
-            hi[e / 2] = (uint32_t)f16_bits(khi0 * cv[e] + klo0 * sv[e]) |
-                        ((uint32_t)f16_bits(khi1 * cv[e + 1] + klo1 * sv[e + 1]) << 16);
+            lo[e / 2] = pack_f16x2(klo0 * cv[e] - khi0 * sv[e], klo1 * cv[e + 1] - khi1 * sv[e + 1]);
+            hi[e / 2] = pack_f16x2(khi0 * cv[e] + klo0 * sv[e], khi1 * cv[e + 1] + klo1 * sv[e + 1]);
           }
           const int clo = (rb % DB) * 4 + v4, chi = (rb2 % DB) * 4 + v4;
           own[hh][clo][0] = lo[0];
@@ -770,83 +813,149 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // any order (heads outer: one head's key fragments in registers at a time).  The scores come with
   // the tokens in the accumulator registers and the rows across the lanes, so a row's quarter
   // statistics are 32 values in the lane and one exchange with lane l32 + 32.
+  // The workgroup's query rows go to LDS once, as fp16, in chunks of up to QROWS rows per head: the
+  // four token quarters of a head read the same rows, which loaded per wave would cross each CU's
+  // load path four times.
   auto row_blocks_quarters = [&](auto qtype) {
-    using QF = typename QueryFrag<decltype(qtype)::value>::type;
+    constexpr int QT = decltype(qtype)::value;
     // each wave stages its probabilities in LDS so that every global store writes whole 128-byte lines
-    constexpr int SROW = 72;  // staging row: 64 tokens + 8 halves of padding
-    half_t* stage = lds + wave * 32 * SROW;
+    constexpr int SROW = 72;                                // staging row: 64 tokens + 8 halves of padding
+    constexpr int QSTR = D + 8;                             // staged query row (conflict-free b128 reads)
+    constexpr int LDS_HALVES = 2 * 2 * kTileTok * kStride;  // the lds array
+    constexpr int STAGE_HALVES = (kK2Threads / 64) * 32 * SROW;
+    constexpr int QROWS = (LDS_HALVES - STAGE_HALVES) / (HPW * QSTR) / 32 * 32;  // 192 at D = 64 and 128
+    static_assert(QROWS >= 32, "query chunk");
+    constexpr int C8 = D / 8;                               // 8-element pieces per query row
+    half_t* qlds = lds;                                         // [HPW][QROWS][QSTR]
+    // this lane's piece of a staged probability row: tokens (lane & 7) * 8 .. + 8 of the wave's quarter
+    const long pstride = (long)a.ntiles * kTileTok;
+    uint16_t* pbase = a.probs + (long)tile * kTileTok + tq * 64 + (lane & 7) * 8;
+    const long lane_row = (long)(lane >> 3) * pstride;
+    half_t* stage = lds + HPW * QROWS * QSTR + wave * 32 * SROW;
+    constexpr int RPP = kK2Threads / C8;         // rows per staging pass
+    constexpr int PPH = QROWS / RPP;             // passes per head
+    static_assert(QROWS % RPP == 0, "staging passes");
+    const int c8 = tid % C8, rsub = tid / C8;
+    // row r of head h0 + hl is query row b * Hq * q_len + (h0 + hl) * RH + r
+    const long qrow0 = (long)b * a.Hq * a.q_len + (long)h0 * RH;
+    for (int c0 = 0; c0 < RH; c0 += QROWS) {
+      const int nblk = (min(QROWS, RH - c0) + 31) / 32;
+      if (c0 > 0) __syncthreads();  // the previous chunk's rows are read (the first: the RoPE rows)
+      // QROWS rows per head, rows past the end repeating row RH - 1 (their loads all hit one row's
+      // lines; the rows are never read): every load unconditional and issued before any is used
+      RawQuery8<QT> qv[HPW * PPH];
 #pragma unroll
-    for (int hh = 0; hh < HPWAVE; ++hh) {
-      const int h = h0 + hs * HPWAVE + hh;
-      auto quarter = [&](const QF (&qf)[KS], int mb) {
-        floatx16 sacc[2];
-        block_mfma(qtype, QueryType<1>{}, sacc, kf[hh], qf);
-        // The maximum is taken over the raw dot products (the scale is positive) and the scale folds
-        // into the exponent: p = 2^(q.k * scale * log2(e) - max * scale * log2(e)), one fma and one
-        // exp2 per score.  Tokens past the tile's end (last tile only) score -inf.
-        if (count < kTileTok) {
+      for (int p = 0; p < HPW * PPH; ++p) {
+        const int hl = p / PPH, rl = (p % PPH) * RPP + rsub;
+        qv[p] = load_raw_query8<QT>(a.query, (qrow0 + hl * RH + min(c0 + rl, RH - 1)) * D + c8 * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int p = 0; p < HPW * PPH; ++p) {
+        const int hl = p / PPH, rl = (p % PPH) * RPP + rsub;
+        *(half8*)(qlds + (hl * QROWS + rl) * QSTR + c8 * 8) = raw_query8_half<QT>(qv[p]);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int hh = 0; hh < HPWAVE; ++hh) {
+        const int hl = hs * HPWAVE + hh;
+        const int h = h0 + hl;
+        // the fp16 query fragments of row block mb of the chunk
+        auto read_queries = [&](half8 (&qf)[KS], int mb) {
+          const half_t* src = qlds + (hl * QROWS + mb * 32 + l32) * QSTR + lhi * 8;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) qf[ks] = lds_half8(src + ks * 16);
+        };
+        auto quarter = [&](const half8 (&qf)[KS], int mb) {
+          floatx16 sacc[2];
+          block_mfma(QueryType<DKV_F32>{}, QueryType<1>{}, sacc, kf[hh], qf);  // fp16 fragments as they are
+          // The maximum is taken over the raw dot products (the scale is positive) and the scale folds
+          // into the exponent: p = 2^(q.k * scale * log2(e) - max * scale * log2(e)), one fma and one
+          // exp2 per score.  Tokens past the tile's end (last tile only) score -inf.
+          if (count < kTileTok) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const int n = tq * 64 + tb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+                sacc[tb][v] = n < count ? sacc[tb][v] : -INFINITY;
+              }
+          }
+          float mraw = -INFINITY;
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int n = tq * 64 + tb * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-              sacc[tb][v] = n < count ? sacc[tb][v] : -INFINITY;
+            for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sacc[tb][v]);
+          mraw = max_xor32(mraw);
+          const float c2 = a.scaling * 1.44269504088896341f;
+          const float off2 = mraw == -INFINITY ? 0.0f : mraw * c2;
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              sacc[tb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[tb][v], c2, -off2));  // -inf -> 0
+          const float mx = mraw * a.scaling;  // the quarter maximum of the scaled scores (-inf if empty)
+          const int row0 = c0 + mb * 32;      // first row of the block
+          // the fp16 probabilities: pw[tb][j] holds tokens tb*32 + 8j + 4lhi .. + 3 of row l32
+          uint2 pw[2][4];
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              pw[tb][j] = make_uint2(pack_f16x2(sacc[tb][4 * j], sacc[tb][4 * j + 1]),
+                                     pack_f16x2(sacc[tb][4 * j + 2], sacc[tb][4 * j + 3]));
+          // the quarter sum of the fp32 probabilities (lanes l32 and l32 + 32 hold the row's halves)
+          float sm = 0.0f;
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sm += sacc[tb][v];
+          sm = sum_xor32(sm);
+          // row l32 of the block into the staging rows
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(uint2*)(stage + l32 * SROW + tb * 32 + 8 * j + 4 * lhi) = pw[tb][j];
+          __builtin_amdgcn_wave_barrier();  // LDS runs a wave's accesses in order: the reads see the writes
+          // lane L then holds 8 tokens of rows L/8 + 8k: eight lanes write one row's 128 bytes.  In the
+          // last, partial block rows past the end were computed from row RH - 1's query and key bits,
+          // so they store the same bytes there.
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+          u32x4 pv[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) pv[k] = *(const u32x4*)(stage + ((lane >> 3) + 8 * k) * SROW + (lane & 7) * 8);
+          // the four reads go out together, ahead of the branch (the compiler would otherwise read and
+          // wait once per store inside it)
+          asm volatile("" ::"v"(pv[0]), "v"(pv[1]), "v"(pv[2]), "v"(pv[3]));
+          if (row0 + 32 <= RH) {  // a whole block: rows row0 + (lane >> 3) + 8 k, 8 rows apart
+            uint16_t* dst = pbase + (long)(h * RH + row0) * pstride + lane_row;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) *(u32x4*)(dst + 8 * k * pstride) = pv[k];
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const long r = (long)h * RH + min(row0 + (lane >> 3) + 8 * k, RH - 1);
+              *(u32x4*)(pbase + r * pstride) = pv[k];
             }
-        }
-        float mraw = -INFINITY;
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mraw = fmaxf(mraw, sacc[tb][v]);
-        mraw = fmaxf(mraw, __shfl_xor(mraw, 32));
-        const float c2 = a.scaling * 1.44269504088896341f;
-        const float off2 = mraw == -INFINITY ? 0.0f : mraw * c2;
-        float sm = 0.0f;
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            sacc[tb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[tb][v], c2, -off2));  // -inf -> 0
-            sm += sacc[tb][v];
           }
-        sm += __shfl_xor(sm, 32);
-        const float mx = mraw * a.scaling;  // the quarter maximum of the scaled scores (-inf if empty)
-        // row l32 of the block, tokens tb*32 + 8j + 4lhi .. + 3 into the staging rows
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            *(uint2*)(stage + l32 * SROW + tb * 32 + 8 * j + 4 * lhi) =
-                make_uint2((uint32_t)f16_bits(sacc[tb][4 * j]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 1]) << 16),
-                           (uint32_t)f16_bits(sacc[tb][4 * j + 2]) | ((uint32_t)f16_bits(sacc[tb][4 * j + 3]) << 16));
-        __builtin_amdgcn_wave_barrier();  // LDS runs a wave's accesses in order: the reads see the writes
-        // lane L then holds 8 tokens of rows L/8 + 8k: eight lanes write one row's 128 bytes.  Every
-        // store is unconditional, so the compiler knows how many are in flight and the next block's
-        // query loads are waited for without waiting for these stores.  Rows past the end were
-        // computed from row RH - 1's query and key bits, so they store the same bytes there.
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint4 pv = *(const uint4*)(stage + ((lane >> 3) + 8 * k) * SROW + (lane & 7) * 8);
-          const long r = (long)h * RH + min(mb * 32 + (lane >> 3) + 8 * k, RH - 1);
-          *(uint4*)(a.probs + r * ((long)a.ntiles * kTileTok) + (long)tile * kTileTok + tq * 64 + (lane & 7) * 8) = pv;
+          __builtin_amdgcn_wave_barrier();  // the next block's staging writes stay behind these reads
+          // lanes l32 and l32 + 32 hold the same statistics
+          const long r_all = (long)h * RH + min(row0 + l32, RH - 1);
+          a.sub_max[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = mx;
+          a.sub_sum[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = sm;
+        };
+        // two fragment buffers: the next row block's fragments are read while this block's MFMAs run
+        half8 qa[KS], qb[KS];
+        read_queries(qa, 0);
+        for (int mb = 0; mb < nblk; mb += 2) {
+          read_queries(qb, min(mb + 1, nblk - 1));
+          __builtin_amdgcn_sched_barrier(0);
+          quarter(qa, mb);
+          if (mb + 1 >= nblk) break;
+          read_queries(qa, min(mb + 2, nblk - 1));
+          __builtin_amdgcn_sched_barrier(0);
+          quarter(qb, mb + 1);
         }
-        __builtin_amdgcn_wave_barrier();  // the next block's staging writes stay behind these reads
-        // lanes l32 and l32 + 32 hold the same statistics
-        const long r_all = (long)h * RH + min(mb * 32 + l32, RH - 1);
-        a.sub_max[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = mx;
-        a.sub_sum[sub_index(r_all, tile * 4 + tq, a.ntiles * 4)] = sm;
-      };
-      // two query buffers: the next row block's fragments load while this block's MFMAs run
-      QF qa[KS], qb[KS];
-      load_queries(qtype, qa, h, 0);
-      for (int mb = 0; mb < mblocks; mb += 2) {
-        load_queries(qtype, qb, h, min(mb + 1, mblocks - 1));
-        __builtin_amdgcn_sched_barrier(0);
-        quarter(qa, mb);
-        if (mb + 1 >= mblocks) break;
-        load_queries(qtype, qa, h, min(mb + 2, mblocks - 1));
-        __builtin_amdgcn_sched_barrier(0);
-        quarter(qb, mb + 1);
       }
     }
   };
@@ -2305,16 +2414,24 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
                                                             int32_t* __restrict__ out) {
   constexpr int kWaves = kTopkThreads / 64;
   __shared__ uint32_t hist[kWaves][256];  // one histogram per wave: fewer LDS atomic collisions
+  __shared__ uint32_t total[256];
   __shared__ uint32_t sh_prefix, sh_k;
-  __shared__ int scan_g[kTopkThreads];
-  __shared__ int scan_e[kTopkThreads];
+  __shared__ int wsum_g[kWaves], wsum_e[kWaves];
+  // the keys of thread t's range at kbuf[t * ps ..], ps = per rounded up to odd (conflict-free reads)
+  __shared__ uint32_t kbuf[kTopkThreads * (kTopkCache + 1)];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (n + kTopkThreads - 1) / kTopkThreads;
   const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
   const bool cached = per <= kTopkCache;
   uint32_t key[kTopkCache];
+  if (cached) {
+    // coalesced loads into LDS, then each thread's contiguous range into registers
+    const int ps = per | 1;
+    for (int e = tid; e < n; e += kTopkThreads) kbuf[(e / per) * ps + e % per] = order_key(s[e]);
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kTopkCache; ++j) key[j] = cached ? order_key(s[min(i0 + j, n - 1)]) : 0u;  // n >= 1
+    for (int j = 0; j < kTopkCache; ++j) key[j] = kbuf[tid * ps + min(j, per - 1)];
+  }
   auto key_at = [&](int j) { return cached ? key[j] : order_key(s[i0 + j]); };
   uint32_t prefix = 0, pmask = 0;
   uint32_t kk = (uint32_t)k;
@@ -2332,16 +2449,20 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
       }
     }
     __syncthreads();
+    if (tid < 256) {  // the waves' histograms summed per bucket
+      uint32_t v = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v += hist[w][tid];
+      total[tid] = v;
+    }
+    __syncthreads();
     if (wave == 0) {
       // lane l owns buckets 255 - 4l .. 252 - 4l (descending); suffix counts by a wave scan
       uint32_t c[4], tot = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) v += hist[w][255 - 4 * lane - j];
-        c[j] = v;
-        tot += v;
+        c[j] = total[255 - 4 * lane - j];
+        tot += c[j];
       }
       uint32_t incl = tot;  // inclusive scan over lanes (higher buckets first)
 #pragma unroll
@@ -2370,7 +2491,6 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     kk = sh_k;
     prefix = sh_prefix;
     pmask |= 255u << shift;
-    __syncthreads();
   }
   const uint32_t T = prefix;  // key of the k-th largest value
   int cg = 0, ce = 0;
@@ -2379,24 +2499,34 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     cg += u > T;
     ce += u == T;
   }
-  scan_g[tid] = cg;
-  scan_e[tid] = ce;
-  __syncthreads();
-  // inclusive scans (Hillis-Steele)
-  for (int o = 1; o < kTopkThreads; o <<= 1) {
-    const int vg = tid >= o ? scan_g[tid - o] : 0;
-    const int ve = tid >= o ? scan_e[tid - o] : 0;
-    __syncthreads();
-    scan_g[tid] += vg;
-    scan_e[tid] += ve;
-    __syncthreads();
+  // exclusive prefix counts over the threads (index order): a scan within each wave, then the
+  // waves' totals
+  int ig = cg, ie = ce;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int tg = __shfl_up(ig, o), te = __shfl_up(ie, o);
+    if (lane >= o) {
+      ig += tg;
+      ie += te;
+    }
   }
-  const int total_g = scan_g[kTopkThreads - 1];
+  if (lane == 63) {
+    wsum_g[wave] = ig;
+    wsum_e[wave] = ie;
+  }
+  __syncthreads();
+  int base_g = 0, base_e = 0, total_g = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int g = wsum_g[w], e = wsum_e[w];
+    base_g += w < wave ? g : 0;
+    base_e += w < wave ? e : 0;
+    total_g += g;
+  }
   const int need_e = k - total_g;  // equal-key elements to take, lowest index first
-  int eq_before = scan_e[tid] - ce;
-  int g_before = scan_g[tid] - cg;
+  int eq_before = base_e + ie - ce;
   // selected before this thread's range = greater elements + min(equal, need)
-  int pos = g_before + min(eq_before, need_e);
+  int pos = base_g + ig - cg + min(eq_before, need_e);
   for (int i = i0; i < i1; ++i) {
     const uint32_t u = key_at(i - i0);
     if (u > T) {

@@ -58,6 +58,9 @@ def _gpu_importance(case, ctx, plane_cap):
     ("1b2", 600, 4, 8, "float32"),
     ("3b2", 1300, 16, 2, "bfloat16"),  # the scoring epilogue is instantiated per query type
     ("1b2", 800, 8, 2, "float16"),
+    # more than 192 query rows per KV head: the scoring epilogue stages its query rows in two chunks
+    ("1b2", 700, 64, 2, "bfloat16"),
+    ("3b2", 600, 72, 2, "float32"),
 ])
 def test_question_scoring_and_topk(shape_name, tokens, q_len, plane_cap, qdtype):
     import dkv_hip
