@@ -1840,7 +1840,7 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
 // Decoding writes probabilities in the value side's layout (and may split the rank); question
 // scoring writes them row-major for the importance kernel and never splits.
 int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hipStream_t st, bool scoring = false,
-                       float* sub_max = nullptr, float* sub_sum = nullptr) {
+                       float* sub_max = nullptr, float* sub_sum = nullptr, uint16_t* probs = nullptr) {
   if (L.ntiles == 0) return DKV_OK;
   K2Args k{};
   k.coef = (const uint16_t*)(ws + L.coef);
@@ -1853,7 +1853,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.rope_sin = a->rope_sin;
   k.rope_rows = a->rope_rows;
   k.query = a->query;
-  k.probs = (uint16_t*)(ws + L.probs);
+  k.probs = probs ? probs : (uint16_t*)(ws + L.probs);
   k.sub_max = sub_max;
   k.sub_sum = sub_sum;
   k.tile_max = (float*)(ws + L.tile_max);
@@ -2133,26 +2133,27 @@ struct RowStatsArgs {
   int Hkv, Hq, q_len, E, query_dtype, nsub;
 };
 
-constexpr int kStatThreads = 256;
-constexpr int kStatWaves = kStatThreads / 64;
-constexpr int kStatKeys = kStatThreads / 2;  // exact keys scored per pass: two lanes per key
-
-// One workgroup per RPW consecutive rows of one query head (RPW divides q_len): the softmax
+// One workgroup (wg) per RPW consecutive rows of one query head (RPW divides q_len): the softmax
 // statistics of each row over the compressed tokens (merged from K2's per-quarter maxima and sums),
 // the exact context tokens and the question's own keys up to the row's position (causal).  The
 // rows share their KV head, so each exact key is loaded once for all of them.  Every global load
 // of the first round (the rows' quarter statistics, their query rows, the first pass of exact keys)
-// is unconditional and goes out before any is used.  Lanes 2 k and 2 k + 1 score key k of a pass,
-// each over half of the head dimension.
-template <int D, int RPW>
-__global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a) {
-  constexpr int U = D / 8;                             // float4 per lane: half a key row
+// is unconditional and goes out before any is used.  A pass scores 128 keys: the KL = NT / 128
+// consecutive lanes KL k .. KL k + KL - 1 score key k, each over 1 / KL of the head dimension.
+template <int D, int RPW, int NT>
+DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
+  constexpr int kStatThreads = NT;
+  constexpr int kStatWaves = NT / 64;
+  constexpr int KL = NT / 128;                         // lanes per key (2 or 4)
+  static_assert(KL == 2 || KL == 4, "lanes per key");
+  constexpr int kStatKeys = NT / KL;                   // exact keys scored per pass
+  constexpr int U = D / (4 * KL);                      // float4 per lane: 1 / KL of a key row
   constexpr int QW = (RPW * D + kStatThreads - 1) / kStatThreads;  // query elements per thread
   __shared__ __attribute__((aligned(16))) float q[RPW][D];
   __shared__ float red[2][kStatWaves][RPW];
-  const int row0 = blockIdx.x * RPW;
+  const int row0 = wg * RPW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kj = tid >> 1, kh = tid & 1;
+  const int kj = tid / KL, kh = tid % KL;
   const int gq = a.Hq / a.Hkv;
   const int qh = row0 / a.q_len, qi0 = row0 % a.q_len;
   const int h = qh / gq;
@@ -2230,10 +2231,12 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a)
         float dot = 0.0f;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const float4 q4 = *(const float4*)&q[i][kh * (D / 2) + 4 * u];
+          const float4 q4 = *(const float4*)&q[i][kh * (D / KL) + 4 * u];
           dot += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
         }
-        sc[i] = (dot + __shfl_xor(dot, 1)) * a.scaling;
+        dot += lane_xor1(dot);  // the key's KL lanes (each sum is the same in all of them)
+        if constexpr (KL == 4) dot += lane_xor2(dot);
+        sc[i] = dot * a.scaling;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -2303,7 +2306,7 @@ __global__ __launch_bounds__(kStatThreads) void row_stats_kernel(RowStatsArgs a)
 struct ImportanceArgs {
   const uint16_t* probs;  // fp16 [R_total][ntiles * 256], relative to each quarter's maximum (K2)
   const float* sub_max;   // [R_total][ntiles * 4] quarter maxima (K2)
-  const float* stat;      // [R_total][2]: M and 1 / L (row_stats_kernel)
+  const float* stat;      // [R_total][2]: M and 1 / L (row_stats_rows)
   float* importance;      // [n]
   int R_total, n, ntiles;
 };
@@ -2312,9 +2315,9 @@ constexpr int kImpThreads = 512;
 constexpr int kImpWaves = kImpThreads / 64;
 constexpr int kImpBatch = 12;  // row iterations whose loads go out together
 
-__global__ __launch_bounds__(kImpThreads) void importance_kernel(ImportanceArgs a) {
+// sub: the tile quarter (tile sub / 4, quarter sub % 4)
+DKV_DEVICE void importance_quarter(const ImportanceArgs& a, int sub) {
   __shared__ float part[kImpWaves][64];
-  const int sub = blockIdx.x;  // tile quarter: tile sub / 4, quarter sub % 4
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int rl = lane >> 3, tc = lane & 7;
   const long pos = (long)sub * 64 + tc * 8;
@@ -2371,29 +2374,53 @@ __global__ __launch_bounds__(kImpThreads) void importance_kernel(ImportanceArgs 
   }
 }
 
+// K4a per layer after K2: this layer's row statistics (the first n_stat_wg workgroups) beside the
+// previous layer's importance (the others, one per tile quarter), whose probabilities, quarter
+// maxima and row statistics sit in the other half of their double buffers.  The statistics are a
+// chain of dependent loads on few workgroups and the importance a stream over the probabilities,
+// so one launch overlaps them.  Layers are added to the importance in order, one launch late.
+// (registers capped for two workgroups per CU: both roles then run beside each other on every CU)
+template <int D, int RPW>
+__global__ __launch_bounds__(kImpThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void score_stats_kernel(RowStatsArgs rs, ImportanceArgs im, int n_stat_wg) {
+  if ((int)blockIdx.x < n_stat_wg)
+    row_stats_rows<D, RPW, kImpThreads>(rs, blockIdx.x);
+  else
+    importance_quarter(im, blockIdx.x - n_stat_wg);
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = 0.0f;
 }
 
+// Probabilities, quarter maxima and row statistics are double-buffered by layer parity: the
+// importance of layer l - 1 is computed while layer l's statistics are.
 struct ScoreLayout {
   Layout base;
-  size_t sub_max, sub_sum, stat, total;
+  size_t probs2, sub_max[2], sub_sum, stat[2], total;
 };
 
-// The attend layout up to the tile statistics (decoded keys, probabilities), then the per-quarter
-// statistics and the per-row statistics.
+// The attend layout up to the tile statistics (decoded keys, probabilities), then the second
+// probability buffer, the per-quarter statistics and the per-row statistics.
 ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   ScoreLayout S{};
   S.base = make_layout(a);
   const size_t per_quarter = align256((size_t)((S.base.R_total + 7) / 8 * 8) * S.base.ntiles * 4 * 4);
+  const size_t per_stat = align256((size_t)S.base.R_total * 2 * 4);
   size_t off = S.base.w_part;
-  S.sub_max = off;
-  off += per_quarter;
+  S.probs2 = off;
+  off += align256((size_t)S.base.R_total * S.base.n_slots * 2);
+  for (int i = 0; i < 2; ++i) {
+    S.sub_max[i] = off;
+    off += per_quarter;
+  }
   S.sub_sum = off;
   off += per_quarter;
-  S.stat = off;
-  off += align256((size_t)S.base.R_total * 2 * 4);
+  for (int i = 0; i < 2; ++i) {
+    S.stat[i] = off;
+    off += per_stat;
+  }
   S.total = off;
   return S;
 }
@@ -2569,15 +2596,20 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
               "dkv_score_layer: workspace %zu B < required %zu B", workspace_bytes, S.total);
   char* ws = (char*)workspace;
   hipStream_t st = dkv::as_stream(stream);
-  rc = launch_keys_scores(a, S.base, ws, st, /*scoring=*/true, (float*)(ws + S.sub_max), (float*)(ws + S.sub_sum));
+  // layer parity picks the halves of the double buffers: this layer's K2 output and statistics go
+  // to `cur`, the previous layer's wait in `prv` for their importance
+  const int cur = a->layer & 1, prv = cur ^ 1;
+  uint16_t* probs[2] = {(uint16_t*)(ws + S.base.probs), (uint16_t*)(ws + S.probs2)};
+  rc = launch_keys_scores(a, S.base, ws, st, /*scoring=*/true, (float*)(ws + S.sub_max[cur]),
+                          (float*)(ws + S.sub_sum), probs[cur]);
   if (rc) return rc;
   RowStatsArgs e{};
   e.query = a->query;
   e.key_exact = a->key_exact;
   e.key_question = key_question;
-  e.sub_max = (const float*)(ws + S.sub_max);
+  e.sub_max = (const float*)(ws + S.sub_max[cur]);
   e.sub_sum = (const float*)(ws + S.sub_sum);
-  e.stat = (float*)(ws + S.stat);
+  e.stat = (float*)(ws + S.stat[cur]);
   e.scaling = a->scaling;
   e.Hkv = a->kv_heads;
   e.Hq = a->q_heads;
@@ -2585,33 +2617,42 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   e.E = E;
   e.query_dtype = a->query_dtype;
   e.nsub = S.base.ntiles * 4;
-  // eight rows of one query head per workgroup when the question length allows it
+  auto importance_args = [&](int buf) {
+    ImportanceArgs im{};
+    im.probs = probs[buf];
+    im.sub_max = (const float*)(ws + S.sub_max[buf]);
+    im.stat = (const float*)(ws + S.stat[buf]);
+    im.importance = importance;
+    im.R_total = S.base.R_total;
+    im.n = S.base.n_total;
+    im.ntiles = S.base.ntiles;
+    return im;
+  };
+  // eight rows of one query head per statistics workgroup when the question length allows it
   const bool rows8 = a->q_len % 8 == 0;
-  const dim3 sgrid((unsigned)(rows8 ? S.base.R_total / 8 : S.base.R_total));
-  if (a->head_dim == 128) {
-    if (rows8)
-      hipLaunchKernelGGL((row_stats_kernel<128, 8>), sgrid, dim3(kStatThreads), 0, st, e);
-    else
-      hipLaunchKernelGGL((row_stats_kernel<128, 1>), sgrid, dim3(kStatThreads), 0, st, e);
-  } else {
-    if (rows8)
-      hipLaunchKernelGGL((row_stats_kernel<64, 8>), sgrid, dim3(kStatThreads), 0, st, e);
-    else
-      hipLaunchKernelGGL((row_stats_kernel<64, 1>), sgrid, dim3(kStatThreads), 0, st, e);
-  }
-  rc = dkv::check_launch("row_stats");
+  const int n_stat = rows8 ? S.base.R_total / 8 : S.base.R_total;
+  const int n_imp = S.base.n_total > 0 ? S.base.ntiles * 4 : 0;
+  auto launch = [&](int n_stat_wg, const ImportanceArgs& im, int n_imp_wg) {
+    const dim3 grid((unsigned)(n_stat_wg + n_imp_wg)), block(kImpThreads);
+    if (a->head_dim == 128) {
+      if (rows8)
+        hipLaunchKernelGGL((score_stats_kernel<128, 8>), grid, block, 0, st, e, im, n_stat_wg);
+      else
+        hipLaunchKernelGGL((score_stats_kernel<128, 1>), grid, block, 0, st, e, im, n_stat_wg);
+    } else {
+      if (rows8)
+        hipLaunchKernelGGL((score_stats_kernel<64, 8>), grid, block, 0, st, e, im, n_stat_wg);
+      else
+        hipLaunchKernelGGL((score_stats_kernel<64, 1>), grid, block, 0, st, e, im, n_stat_wg);
+    }
+    return dkv::check_launch("score_stats");
+  };
+  // this layer's statistics, and the previous layer's importance (none before layer 0)
+  rc = launch(n_stat, importance_args(prv), a->layer > 0 ? n_imp : 0);
   if (rc) return rc;
-  if (S.base.n_total == 0) return DKV_OK;
-  ImportanceArgs im{};
-  im.probs = (const uint16_t*)(ws + S.base.probs);
-  im.sub_max = (const float*)(ws + S.sub_max);
-  im.stat = (const float*)(ws + S.stat);
-  im.importance = importance;
-  im.R_total = S.base.R_total;
-  im.n = S.base.n_total;
-  im.ntiles = S.base.ntiles;
-  hipLaunchKernelGGL(importance_kernel, dim3((unsigned)S.base.ntiles * 4), dim3(kImpThreads), 0, st, im);
-  return dkv::check_launch("importance");
+  // the last layer adds its own importance at once
+  if (a->layer == a->layers - 1 && n_imp > 0) return launch(0, importance_args(cur), n_imp);
+  return DKV_OK;
 }
 
 extern "C" size_t dkv_topk_workspace_bytes(int32_t n) {

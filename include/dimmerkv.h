@@ -264,9 +264,12 @@ int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, size_t worksp
  * query positions, the GQA group and the KV heads; the softmax spans the
  * compressed tokens, the exact tokens and the question's own keys (causal).
  * Uses the attend arguments (batch must be 1; out/value fields unused);
- * key_question is [Hkv][q_len][d] f32 (RoPE applied).  Adds this layer's
- * contribution into importance [n] (f32) in a fixed order; call
- * dkv_score_begin once before the first layer. */
+ * key_question is [Hkv][q_len][d] f32 (RoPE applied).  Call dkv_score_begin
+ * once, then this for layers 0 .. layers-1 in order, on one workspace and
+ * stream: each layer's contribution is added into importance [n] (f32) in
+ * layer order, one call late (the call for layer l adds layer l-1's beside
+ * computing layer l's softmax statistics), and the call for the last layer
+ * adds its own too, so the vector is complete after that call. */
 size_t dkv_score_workspace_bytes(const dkv_attend_args_t* a);
 int dkv_score_begin(float* importance, int32_t n, void* stream);
 int dkv_score_layer(const dkv_attend_args_t* a, const float* key_question, float* importance, void* workspace,
