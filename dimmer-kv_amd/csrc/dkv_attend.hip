@@ -2443,6 +2443,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   __shared__ uint32_t hist[kWaves][256];  // one histogram per wave: fewer LDS atomic collisions
   __shared__ uint32_t total[256];
   __shared__ uint32_t sh_prefix, sh_k;
+  __shared__ uint32_t wmin[kWaves], wmax[kWaves];
   __shared__ int wsum_g[kWaves], wsum_e[kWaves];
   // the keys of thread t's range at kbuf[t * ps ..], ps = per rounded up to odd (conflict-free reads)
   __shared__ uint32_t kbuf[kTopkThreads * (kTopkCache + 1)];
@@ -2452,14 +2453,46 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
   const bool cached = per <= kTopkCache;
   uint32_t key[kTopkCache];
   if (cached) {
-    // coalesced loads into LDS, then each thread's contiguous range into registers
+    // coalesced loads into LDS, then each thread's contiguous range into registers; element e
+    // belongs to thread e / per (computed in fp32: e < 2^15 and per <= 32 keep it exact)
     const int ps = per | 1;
-    for (int e = tid; e < n; e += kTopkThreads) kbuf[(e / per) * ps + e % per] = order_key(s[e]);
+    const float inv_per = 1.0f / (float)per;
+    for (int e = tid; e < n; e += kTopkThreads) {
+      const int q = (int)(((float)e + 0.5f) * inv_per);
+      kbuf[q * ps + (e - q * per)] = order_key(s[e]);
+    }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kTopkCache; ++j) key[j] = kbuf[tid * ps + min(j, per - 1)];
   }
   auto key_at = [&](int j) { return cached ? key[j] : order_key(s[i0 + j]); };
+  // The keys' range [kmin, kmax]: the select runs on v = (key - kmin) << lz, which puts the range's
+  // top bit at bit 31, so the first 8-bit digit already spreads the keys over the buckets (raw
+  // float keys of similar magnitude share their top byte, and LDS atomics on one bucket serialize).
+  uint32_t lo = 0xffffffffu, hi = 0u;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t u = key_at(i - i0);
+    lo = min(lo, u);
+    hi = max(hi, u);
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    lo = min(lo, (uint32_t)__shfl_xor((int)lo, o));
+    hi = max(hi, (uint32_t)__shfl_xor((int)hi, o));
+  }
+  if (lane == 0) {
+    wmin[wave] = lo;
+    wmax[wave] = hi;
+  }
+  __syncthreads();
+  uint32_t kmin = wmin[0], kmax = wmax[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    kmin = min(kmin, wmin[w]);
+    kmax = max(kmax, wmax[w]);
+  }
+  const int lz = kmax > kmin ? __clz(kmax - kmin) : 0;
+  auto vkey = [&](uint32_t u) { return (u - kmin) << lz; };  // order-preserving on [kmin, kmax]
   uint32_t prefix = 0, pmask = 0;
   uint32_t kk = (uint32_t)k;
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -2467,20 +2500,22 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     __syncthreads();
     if (cached) {
 #pragma unroll
-      for (int j = 0; j < kTopkCache; ++j)
-        if (i0 + j < i1 && (key[j] & pmask) == prefix) atomicAdd(&hist[wave][(key[j] >> shift) & 255u], 1u);
+      for (int j = 0; j < kTopkCache; ++j) {
+        const uint32_t v = vkey(key[j]);
+        if (i0 + j < i1 && (v & pmask) == prefix) atomicAdd(&hist[wave][(v >> shift) & 255u], 1u);
+      }
     } else {
       for (int i = i0; i < i1; ++i) {
-        const uint32_t u = order_key(s[i]);
-        if ((u & pmask) == prefix) atomicAdd(&hist[wave][(u >> shift) & 255u], 1u);
+        const uint32_t v = vkey(order_key(s[i]));
+        if ((v & pmask) == prefix) atomicAdd(&hist[wave][(v >> shift) & 255u], 1u);
       }
     }
     __syncthreads();
     if (tid < 256) {  // the waves' histograms summed per bucket
-      uint32_t v = 0;
+      uint32_t c = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) v += hist[w][tid];
-      total[tid] = v;
+      for (int w = 0; w < kWaves; ++w) c += hist[w][tid];
+      total[tid] = c;
     }
     __syncthreads();
     if (wave == 0) {
@@ -2519,7 +2554,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(const float* __restr
     prefix = sh_prefix;
     pmask |= 255u << shift;
   }
-  const uint32_t T = prefix;  // key of the k-th largest value
+  const uint32_t T = (prefix >> lz) + kmin;  // key of the k-th largest value
   int cg = 0, ce = 0;
   for (int i = i0; i < i1; ++i) {
     const uint32_t u = key_at(i - i0);
