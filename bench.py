@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--traffic-file", default=None,
                    help="rocprofv3 FETCH/WRITE summary of K2 for this workload "
                         "(default profiles/keys_scores_<config>[_dkvtc]_traffic.txt)")
+    p.add_argument("--encode", action="store_true",
+                   help="time the progressive encoder's stages at the 3B 16K workload; one JSON line")
     p.add_argument("--storage", action="store_true",
                    help="measure kvtc byte storage at 3b-16k-3pct (dkvtc): encode, DEFLATE, restore; one JSON line")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -320,6 +322,54 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
     print(json.dumps(result), flush=True)
 
 
+def encode_bench(reps: int = 3):
+    """The progressive encoder at the 3B 16K workload (Llama-3.2-3B shape, 16,384 tokens, 3 % budget,
+    2-plane floor; the reference's ProgressiveCodec.encode with kvtc's floor rule): one JSON line with
+    the time of each stage, from HIP events recorded by ProgressiveCodec.encode at its stage
+    boundaries (median of ``reps`` encodes after one warm-up).  The stages: the PCA projection of
+    each stream (fp32, as the reference), quantize8 with the 9-level error table and the per-rung
+    errors (dkv_quantize8), the greedy allocation (sort), packing both tiers (dkv_pack_planes) and
+    the exact tokens' copies."""
+    import statistics
+
+    import torch
+
+    import progressive
+    import synth
+
+    dev = "cuda"
+    shape, tokens, budget = synth.SHAPE_3B, 16384, 0.03
+    ctx = synth.make_context(shape, tokens, seed=4040, device=dev)
+    model = synth.RopeModel(shape, dev)
+    codec = progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), synth.order_checkpoint(shape), dev, model)
+    keys, values = synth.prefill_cache(ctx, device=dev, dtype=torch.float16, compute_device=dev)
+    floor = codec.orders["key"].rungs.index(2 * shape.groups)  # every group at 2 planes
+    runs = []
+    for rep in range(reps + 1):
+        marks = []
+        stored = codec.encode(keys, values, budget, 32, floor_rung=floor, marks=marks)
+        torch.cuda.synchronize()
+        if rep:
+            runs.append({name: marks[i - 1][1].elapsed_time(ev) for i, (name, ev) in enumerate(marks) if i})
+    stages = {name: statistics.median(r[name] for r in runs) for name in runs[0]}
+    middle = stored.end - stored.start
+    features = shape.layers * shape.kv_heads * shape.head_dim
+    proj_ms = stages["key projection"] + stages["value projection"]
+    proj_flop = 2 * 2 * middle * features * shape.rank
+    total = sum(stages.values())
+    result = {
+        "metric": "progressive encode ms (3B shape, 16,384 tokens, 3 %, 2-plane floor)",
+        "value": round(total, 2), "unit": "ms", "higher_is_better": False, "data": "synthetic",
+        "stages_ms": {k: round(v, 3) for k, v in stages.items()},
+        "from_coefficients_ms": round(total - proj_ms - stages["exact tokens"], 2),
+        "projection": {"tflop": round(proj_flop / 1e12, 3), "achieved_tflops": round(proj_flop / proj_ms / 1e9, 1),
+                       "peak_tflops": 157.3, "dtype": "fp32",
+                       "frac": round(proj_flop / proj_ms / 1e9 / 157.3, 3)},
+        "middle_tokens": middle, "encodes": reps,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -330,6 +380,9 @@ def main():
         return
     if args.storage:
         storage_bench()
+        return
+    if args.encode:
+        encode_bench()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): this build runs the decode path on a "
