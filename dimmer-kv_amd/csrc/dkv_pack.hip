@@ -528,6 +528,107 @@ extern "C" int dkv_quantize8(const float* coef, int32_t n, int32_t groups, uint8
 }
 
 // ---------------------------------------------------------------------------
+// Centred token-matrix rows of the middle tokens, the encoders' input to the PCA projection
+// (scripts/kvtc.py:137-140 to_matrix with :40-43 derotate and :50-53 token_matrix, then
+// (matrix[start:end] - mean), :189 and scripts/progressive.py:147-148): row t - start, column
+// f = (l * H + h) * D + d holds x - mean[f], x the cache element [l][0][h][t][d] as fp32 and, for
+// keys, first de-rotated at position t: (k * cos - rotate_half(k) * sin) / (cos^2 + sin^2).  Every
+// operation is rounded on its own, as the reference's separate tensor operations round them (no
+// contraction), so the rows are bit-identical to that torch arithmetic.  One thread per 4
+// consecutive columns of a row: consecutive threads write consecutive 16 bytes of the row.
+// ---------------------------------------------------------------------------
+template <int T>
+DKV_DEVICE float4 load_elem4(const void* base, long idx) {
+  if constexpr (T == DKV_F32) {
+    return *(const float4*)((const float*)base + idx);
+  } else {
+    const uint2 w = *(const uint2*)((const uint16_t*)base + idx);
+    const uint16_t e[4] = {(uint16_t)(w.x & 0xffffu), (uint16_t)(w.x >> 16), (uint16_t)(w.y & 0xffffu),
+                           (uint16_t)(w.y >> 16)};
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = T == DKV_BF16 ? bf16_bits_to_float(e[i]) : half_bits_to_float(e[i]);
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+template <int T, bool ROTATE>
+__global__ __launch_bounds__(256) void centered_rows_kernel(const uint64_t* __restrict__ layer_ptrs, int L, int H,
+                                                            int tokens, int D, const float* __restrict__ cos,
+                                                            const float* __restrict__ sin,
+                                                            const float* __restrict__ mean, int start, long quads,
+                                                            float* __restrict__ out) {
+  const long q = (long)blockIdx.x * 256 + threadIdx.x;
+  if (q >= quads) return;
+  const int D4 = D / 4;
+  const int d4 = (int)(q % D4);
+  const long r = q / D4;  // (t, l, h) with h fastest
+  const int h = (int)(r % H), l = (int)((r / H) % L);
+  const int t = start + (int)(r / ((long)H * L));
+  const int d = 4 * d4;
+  const void* base = (const void*)layer_ptrs[l];
+  const long row = (long)h * tokens + t;  // the cache element [l][0][h][t][.]
+  const float4 x = load_elem4<T>(base, row * D + d);
+  const long f = ((long)l * H + h) * D + d;
+  const float4 mu = *(const float4*)(mean + f);
+  float v[4] = {x.x, x.y, x.z, x.w};
+  if constexpr (ROTATE) {
+    const int half = D / 2;
+    // rotate_half: -k[d + D/2] for d < D/2, k[d - D/2] above
+    const bool lower = d < half;
+    const float4 p = load_elem4<T>(base, row * D + (lower ? d + half : d - half));
+    const float4 c4 = *(const float4*)(cos + (long)t * D + d);
+    const float4 s4 = *(const float4*)(sin + (long)t * D + d);
+    const float pv[4] = {p.x, p.y, p.z, p.w}, cv[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+      const float rh = lower ? -pv[i] : pv[i];
+      const float num = v[i] * cv[i] - rh * sv[i];
+      const float den = cv[i] * cv[i] + sv[i] * sv[i];
+      v[i] = num / den;
+    }
+  }
+  float4 o;
+  {
+#pragma clang fp contract(off)
+    o = make_float4(v[0] - mu.x, v[1] - mu.y, v[2] - mu.z, v[3] - mu.w);
+  }
+  *(float4*)(out + (long)(t - start) * ((long)L * H * D) + f) = o;
+}
+
+extern "C" int dkv_centered_rows(const uint64_t* layer_ptrs, int32_t dtype, int32_t layers, int32_t heads,
+                                 int32_t tokens, int32_t head_dim, const float* cos, const float* sin,
+                                 const float* mean, int32_t start, int32_t end, float* out, void* stream) {
+  DKV_REQUIRE(layer_ptrs && mean && out, DKV_EINVAL, "dkv_centered_rows: null pointer");
+  DKV_REQUIRE((cos == nullptr) == (sin == nullptr), DKV_EINVAL, "dkv_centered_rows: cos and sin go together");
+  DKV_REQUIRE(dtype == DKV_F32 || dtype == DKV_F16 || dtype == DKV_BF16, DKV_EINVAL,
+              "dkv_centered_rows: dtype %d not supported", dtype);
+  DKV_REQUIRE(layers > 0 && heads > 0 && tokens >= 0 && head_dim > 0 && head_dim % 8 == 0, DKV_ESHAPE,
+              "dkv_centered_rows: bad shape (layers=%d heads=%d tokens=%d head_dim=%d)", layers, heads, tokens,
+              head_dim);
+  DKV_REQUIRE(0 <= start && start <= end && end <= tokens, DKV_ESHAPE,
+              "dkv_centered_rows: rows %d..%d outside 0..%d", start, end, tokens);
+  const long quads = (long)(end - start) * layers * heads * (head_dim / 4);
+  if (quads == 0) return DKV_OK;
+  const dim3 grid((unsigned)((quads + 255) / 256));
+  hipStream_t st = dkv::as_stream(stream);
+#define DKV_CENTERED(T_, R_)                                                                                    \
+  hipLaunchKernelGGL((centered_rows_kernel<T_, R_>), grid, dim3(256), 0, st, layer_ptrs, layers, heads, tokens, \
+                     head_dim, cos, sin, mean, start, quads, out)
+  const bool rot = cos != nullptr;
+  if (dtype == DKV_F16) {
+    if (rot) DKV_CENTERED(DKV_F16, true); else DKV_CENTERED(DKV_F16, false);
+  } else if (dtype == DKV_BF16) {
+    if (rot) DKV_CENTERED(DKV_BF16, true); else DKV_CENTERED(DKV_BF16, false);
+  } else {
+    if (rot) DKV_CENTERED(DKV_F32, true); else DKV_CENTERED(DKV_F32, false);
+  }
+#undef DKV_CENTERED
+  return dkv::check_launch("dkv_centered_rows");
+}
+
+// ---------------------------------------------------------------------------
 // K4c: merge hot + cold segments of selected tokens into full blobs.
 // One workgroup per selected token; one thread per group.
 // ---------------------------------------------------------------------------

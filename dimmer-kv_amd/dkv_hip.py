@@ -29,7 +29,7 @@ EXPORTS = [
     "dkv_attend_scores", "dkv_attend_values",
     "dkv_score_workspace_bytes", "dkv_score_begin", "dkv_score_layer", "dkv_topk_workspace_bytes", "dkv_topk",
     "dkv_gather_cold", "dkv_refine_rows", "dkv_wire_pack", "dkv_wire_unpack", "dkv_attend_layer_noalloc",
-    "dkv_quantize8",
+    "dkv_quantize8", "dkv_centered_rows",
 ]
 NOALLOC_MAX_BYTES = 64 << 20  # DKV_NOALLOC_MAX_BYTES: the static workspace of dkv_attend_layer_noalloc
 
@@ -171,6 +171,22 @@ def wire_unpack(data, rung, ladder: Ladder, wire: Wire, codes, low, scale) -> No
 def unpack_dequant(stream: Stream, t0: int, nt: int, out: torch.Tensor) -> None:
     _check(lib().dkv_unpack_dequant(ctypes.byref(stream), c_i32(t0), c_i32(nt), c_vp(ptr(out)),
                                     c_i32(dtype_code(out.dtype)), c_vp(stream_handle())), "dkv_unpack_dequant")
+
+
+def centered_rows(tensors, cos, sin, mean, start: int, end: int, out) -> None:
+    """Per-layer caches [1, H, T, D] (fp16/bf16/fp32, one device) -> out f32 [end - start, L*H*D]:
+    the token-matrix rows start..end - 1 minus ``mean``, keys de-rotated when cos/sin are given."""
+    first = tensors[0]
+    if first.dtype not in _DTYPE:
+        raise ValueError(f"centered_rows: cache dtype {first.dtype} not supported")
+    if any(t.shape != first.shape or t.dtype != first.dtype or t.device != first.device for t in tensors):
+        raise ValueError("centered_rows: the layers' caches must share shape, dtype and device")
+    ptrs = torch.tensor([ptr(t) for t in tensors], dtype=torch.int64).to(first.device)
+    _, heads, tokens, head_dim = first.shape
+    _check(lib().dkv_centered_rows(c_vp(ptr(ptrs)), c_i32(_DTYPE[first.dtype]), c_i32(len(tensors)), c_i32(heads),
+                                   c_i32(tokens), c_i32(head_dim), c_vp(ptr(cos)), c_vp(ptr(sin)), c_vp(ptr(mean)),
+                                   c_i32(start), c_i32(end), c_vp(ptr(out)), c_vp(stream_handle())),
+           "dkv_centered_rows")
 
 
 def quantize8(coef, codes, low, span, errors=None) -> None:

@@ -130,8 +130,7 @@ def encode_bytes(codec, keys, values, choice: dict, exact_recent: int) -> bytes:
     wire[:HEADER_BYTES] = torch.tensor(np.asarray([tokens, start, end], "<i4").view(np.uint8), device=device)
     for kind, tensors, rungs, layout in prepared:
         stream = codec.streams[kind]
-        matrix = codec.to_matrix(tensors, kind, cos, sin)
-        coefficients = (matrix[start:end] - stream.mean) @ stream.basis  # the codec's compress arithmetic
+        coefficients = codec.centered(tensors, kind, cos, sin, start, end) @ stream.basis  # compress's arithmetic
         wire[layout.rung_ids:layout.rung_ids + middle] = rungs.to(torch.uint8)
         groups = coefficients.shape[1] // codec.group
         codes = torch.zeros(middle, groups, codec.group, dtype=torch.uint8, device=device)
@@ -148,7 +147,8 @@ def encode_bytes(codec, keys, values, choice: dict, exact_recent: int) -> bytes:
         w, keep = layout.device_tables(device, base)
         dkv_hip.wire_pack(codes, low.view(torch.int16), scale.view(torch.int16), rungs.to(torch.int16).contiguous(),
                           ladder.c_ladder(), w, wire)
-        if layout.exact_rows is not None:
+        if layout.exact_rows is not None:  # tokens kept at the exact rung: their token-matrix rows as they are
+            matrix = codec.to_matrix(tensors, kind, cos, sin)
             rows_bytes = _fp16_bytes(matrix[start:end][rungs == exact_rung])
             wire[layout.exact_rows:layout.exact_rows + rows_bytes.numel()] = rows_bytes
         exact = token_matrix(tensors)

@@ -176,6 +176,19 @@ int dkv_unpack_dequant(const dkv_stream_t* s, int32_t t0, int32_t nt, void* out,
 int dkv_quantize8(const float* coef, int32_t n, int32_t groups, uint8_t* codes, uint16_t* low, uint16_t* span,
                   float* errors, void* stream);
 
+/* Centred token-matrix rows, the encoders' input to the PCA projection
+ * (scripts/kvtc.py:137-140 to_matrix with :40-43 derotate and :50-53
+ * token_matrix, then (matrix[start:end] - mean) as at :189 and
+ * scripts/progressive.py:147-148): layer_ptrs is a device array of `layers`
+ * device pointers to the per-layer caches [1][heads][tokens][head_dim] of
+ * dtype DKV_F16 / DKV_BF16 / DKV_F32; out f32 [end-start][layers*heads*head_dim]
+ * gets x - mean[f] with x de-rotated at its position (cos/sin f32
+ * [tokens][head_dim]) for keys, or as is when cos and sin are NULL (values).
+ * Bit-identical to that torch arithmetic (each operation rounded on its own). */
+int dkv_centered_rows(const uint64_t* layer_ptrs, int32_t dtype, int32_t layers, int32_t heads, int32_t tokens,
+                      int32_t head_dim, const float* cos, const float* sin, const float* mean, int32_t start,
+                      int32_t end, float* out, void* stream);
+
 /* Reference dequantize on unpacked codes (scripts/progressive.py:47-55):
  * codes u8 [n][G][64], low/span f16 [n][G], planes u8 [n or 1][G] -> f32 [n][64G]. */
 int dkv_dequantize_codes(const uint8_t* codes, const uint16_t* low, const uint16_t* span, const uint8_t* planes,

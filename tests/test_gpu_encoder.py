@@ -44,6 +44,30 @@ def test_quantize8_kernel_bit_exact_with_degenerate_group():
     np.testing.assert_allclose(table, pr.error_table(x, c0, l0, s0), rtol=2e-5, atol=1e-12)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_centered_rows_bit_exact(dtype):
+    """dkv_centered_rows (KVTCCodec.centered on GPU caches) equals the torch arithmetic it replaces,
+    (to_matrix(caches)[start:end] - mean) with the keys de-rotated (scripts/kvtc.py:40-43, :137-140,
+    :189), bit for bit, for keys and values, head_dim 64 and 128 (every rotate_half branch), with
+    positions whose cos^2 + sin^2 differs from 1 in the last bits."""
+    import kvtc
+
+    for shape, tokens, start, end in [(synth.ModelShape(2, 8, 64, 32, 1024), 300, 4, 268),
+                                      (synth.ModelShape(3, 8, 128, 24, 2048), 257, 0, 257)]:
+        print(f"[case] centered rows {dtype} head_dim={shape.head_dim} rows {start}..{end}", flush=True)
+        ctx = synth.make_context(shape, tokens, seed=11)
+        model = synth.RopeModel(shape, DEV)
+        codec = kvtc.KVTCCodec(synth.kvtc_checkpoint(ctx), DEV, model)
+        keys, values = synth.prefill_cache(ctx, device=DEV, dtype=dtype)
+        cos, sin = kvtc.rope_tables(model, tokens, DEV)
+        for kind, caches in (("key", keys), ("value", values)):
+            caches = [t.to(DEV) for t in caches]
+            want = codec.to_matrix(caches, kind, cos, sin)[start:end] - codec.streams[kind].mean
+            got = codec.centered(caches, kind, cos, sin, start, end)
+            assert got.shape == want.shape and torch.equal(got, want), \
+                f"{kind}: max diff {(got - want).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("budget,weighted", [(0.25, False), (0.2, True)])
 def test_encode_stages_match_oracle(budget, weighted):
     import kvtc
