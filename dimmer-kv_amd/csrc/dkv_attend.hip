@@ -825,16 +825,16 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
     constexpr int STAGE_HALVES = (kK2Threads / 64) * 32 * SROW;
     constexpr int QROWS = (LDS_HALVES - STAGE_HALVES) / (HPW * QSTR) / 32 * 32;  // 192 at D = 64 and 128
     static_assert(QROWS >= 32, "query chunk");
-    constexpr int C8 = D / 8;                               // 8-element pieces per query row
-    half_t* qlds = lds;                                         // [HPW][QROWS][QSTR]
+    constexpr int C8 = D / 8;             // 8-element pieces per query row
+    constexpr int RPP = kK2Threads / C8;  // rows per staging pass
+    constexpr int PPH = QROWS / RPP;      // passes per head
+    static_assert(QROWS % RPP == 0, "staging passes");
+    half_t* qlds = lds;  // [HPW][QROWS][QSTR]
+    half_t* stage = lds + HPW * QROWS * QSTR + wave * 32 * SROW;
     // this lane's piece of a staged probability row: tokens (lane & 7) * 8 .. + 8 of the wave's quarter
     const long pstride = (long)a.ntiles * kTileTok;
     uint16_t* pbase = a.probs + (long)tile * kTileTok + tq * 64 + (lane & 7) * 8;
     const long lane_row = (long)(lane >> 3) * pstride;
-    half_t* stage = lds + HPW * QROWS * QSTR + wave * 32 * SROW;
-    constexpr int RPP = kK2Threads / C8;         // rows per staging pass
-    constexpr int PPH = QROWS / RPP;             // passes per head
-    static_assert(QROWS % RPP == 0, "staging passes");
     const int c8 = tid % C8, rsub = tid / C8;
     // row r of head h0 + hl is query row b * Hq * q_len + (h0 + hl) * RH + r
     const long qrow0 = (long)b * a.Hq * a.q_len + (long)h0 * RH;
