@@ -44,6 +44,14 @@ def test_validation_errors_map_to_reference_exceptions():
     rc = lib.dkv_dequantize_codes(ctypes.c_void_p(8), ctypes.c_void_p(8), ctypes.c_void_p(8), ctypes.c_void_p(8),
                                   ctypes.c_int32(3), ctypes.c_int32(5), ctypes.c_int32(2), ctypes.c_void_p(8), None)
     assert rc == -2  # planes_rows must be 1 or n
+    # centred token-matrix rows: cos without sin, rows outside the tokens (checked before any launch)
+    vp = ctypes.c_void_p(8)
+    rc = lib.dkv_centered_rows(vp, ctypes.c_int32(1), ctypes.c_int32(2), ctypes.c_int32(8), ctypes.c_int32(16),
+                               ctypes.c_int32(64), vp, None, vp, ctypes.c_int32(0), ctypes.c_int32(16), vp, None)
+    assert rc == -1 and b"cos and sin" in lib.dkv_last_error()
+    rc = lib.dkv_centered_rows(vp, ctypes.c_int32(1), ctypes.c_int32(2), ctypes.c_int32(8), ctypes.c_int32(16),
+                               ctypes.c_int32(64), None, None, vp, ctypes.c_int32(4), ctypes.c_int32(17), vp, None)
+    assert rc == -2 and b"outside" in lib.dkv_last_error()
     with pytest.raises(AssertionError):
         dkv_hip._check(-5, "budget")
     with pytest.raises(RuntimeError):
