@@ -147,12 +147,15 @@ def encode_bytes(codec, keys, values, choice: dict, exact_recent: int) -> bytes:
         w, keep = layout.device_tables(device, base)
         dkv_hip.wire_pack(codes, low.view(torch.int16), scale.view(torch.int16), rungs.to(torch.int16).contiguous(),
                           ladder.c_ladder(), w, wire)
-        if layout.exact_rows is not None:  # tokens kept at the exact rung: their token-matrix rows as they are
-            matrix = codec.to_matrix(tensors, kind, cos, sin)
-            rows_bytes = _fp16_bytes(matrix[start:end][rungs == exact_rung])
+        # the token-matrix rows of the tokens stored as they are (the exact rung's, in token order, then the sinks
+        # and the recent window), converted from those tokens only: the conversion is per token
+        if layout.exact_rows is not None:
+            idx = start + torch.nonzero(rungs == exact_rung).flatten()
+            rows = codec.to_matrix([t.index_select(2, idx) for t in tensors], kind, cos[idx], sin[idx])
+            rows_bytes = _fp16_bytes(rows)
             wire[layout.exact_rows:layout.exact_rows + rows_bytes.numel()] = rows_bytes
-        exact = token_matrix(tensors)
-        tail = _fp16_bytes(torch.cat([exact[:start], exact[end:]]))
+        outside = [torch.cat([t[:, :, :start], t[:, :, end:]], dim=2) for t in tensors]
+        tail = _fp16_bytes(token_matrix(outside))
         wire[layout.exact_tokens:layout.end] = tail
         del keep
     host = torch.empty(base, dtype=torch.uint8, pin_memory=True)
