@@ -217,7 +217,8 @@ struct DecodeArgs {
   int batch, n_total, ntiles, n_slots, G, plane_cap;
 };
 
-constexpr int kDecodeTok = 128;  // slots per decode block
+constexpr int kDecodeSlots = 256;      // slots per decode workgroup: one thread per (slot, group)
+constexpr int kMaxTableRows = 4096;    // rows of a stream table one decode workgroup stages in LDS
 
 // Block -> (slot block, group) with the group fastest and consecutive ids on
 // one XCD, so the blocks reading the same tokens' blobs share that XCD's L2.
@@ -225,6 +226,44 @@ DKV_DEVICE int2 decode_block(int G, int nblocks) {
   const int per_xcd = (nblocks + 7) / 8;
   const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
   return make_int2(lin / G, lin % G);  // (slot block, group); slot block may be out of range
+}
+
+// Rows of a stream's per-token table: piece counts 0..K of the plane format, rungs of the ladder.
+DKV_DEVICE int table_rows(const dkv_stream_t& s) {
+  return s.format == DKV_FMT_LADDER ? s.ladder.rungs : s.order.pieces + 1;
+}
+
+// Group g's column of the stream table staged in LDS as (planes or bits, segment offset) per
+// row, so that a thread's segment address follows from its token's row without a dependent
+// global load.  The caller synchronises before reading it.
+DKV_DEVICE void stage_table_column(const dkv_stream_t& s, int G, int g, int2* tab) {
+  const bool ladder = s.format == DKV_FMT_LADDER;
+  const uint8_t* cnt = ladder ? s.ladder.bits : s.order.planes;
+  const int32_t* off = ladder ? s.ladder.seg_off : s.order.seg_off;
+  const int rows = table_rows(s);
+  for (int r = threadIdx.x; r < rows; r += blockDim.x)
+    tab[r] = make_int2(cnt[(long)r * G + g], off[(long)r * G + g]);
+}
+
+// The (token, group) segment of `slot`'s token, whole: header and code words, with its plane count
+// (plane format, capped at plane_cap) or bit width (ladder).  Padding slots and rows outside the
+// table give an empty segment.  tok_row / tok_off are the token's table row and blob offset,
+// loaded by the caller beside the table column.
+struct SegmentWords {
+  uint32_t header;
+  uint32_t w[16];
+  int m;  // planes (plane format) or bits (ladder); 0 for an empty segment
+};
+
+DKV_DEVICE SegmentWords load_token_segment(const dkv_stream_t& s, const int2* tab, int t, int row, long tok_off,
+                                           int plane_cap) {
+  SegmentWords sw;
+  const bool ok = t >= 0 && row >= 0 && row < table_rows(s);
+  const int2 e = ok ? tab[row] : make_int2(0, 0);
+  const int m = s.format == DKV_FMT_LADDER ? e.x : min(e.x, plane_cap);
+  sw.m = m;
+  load_segment_words(s.blob + tok_off + e.y, 2 * m, sw.header, sw.w);
+  return sw;
 }
 
 // Token held by `slot`, or -1 for a padding slot.
@@ -263,48 +302,50 @@ DKV_DEVICE long sub_index(long row, int t, int nsub) { return ((row >> 3) * nsub
 // ks*16 + (l/32)*8 .. +8 of slot 32j + l%32, so K2 loads each operand with one
 // coalesced 16-byte load per lane.  Values are the affine dequantization of
 // the codes truncated to min(m, plane_cap) planes.  One thread per (slot,
-// group, half).  The decoded keys depend on the stream only, so one decode
+// group): two load rounds (the token's row and blob offset beside the
+// group's table column, then the segment in 16-byte pieces) and eight
+// 16-byte stores.  The decoded keys depend on the stream only, so one decode
 // serves every layer.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(2 * kDecodeTok) void decode_keys_kernel(DecodeArgs a) {
-  const int nsb = a.n_slots / kDecodeTok;
+__global__ __launch_bounds__(kDecodeSlots) void decode_keys_kernel(DecodeArgs a) {
+  extern __shared__ int2 tab[];
+  const int nsb = a.n_slots / kDecodeSlots;
   const int2 bg = decode_block(a.G, nsb * a.G);
   const int sb = bg.x, g = bg.y;
-  if (sb >= nsb) return;
-  const int slot = sb * kDecodeTok + (threadIdx.x >> 1);
-  const int half = threadIdx.x & 1;
+  if (sb >= nsb) return;  // the whole block
+  const int slot = sb * kDecodeSlots + threadIdx.x;
   const int t = slot_token(a, slot);
-  uint32_t vals[16];
-  if (t >= 0 && a.s.format == DKV_FMT_LADDER) {
-    const int G = a.G;
-    const int r = a.s.pieces[t];
-    const bool ok = r >= 0 && r < a.s.ladder.rungs;
-    const int b = ok ? a.s.ladder.bits[(long)r * G + g] : 0;
-    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + (ok ? a.s.ladder.seg_off[(long)r * G + g] : 0);
-    uint32_t cw[8], header;
-    load_ladder_half(seg, b, half, cw, header);
-    ladder_half_f16(cw, header, vals);
-  } else if (t >= 0) {
-    const int G = a.G;
-    const int kp = a.s.pieces[t];
-    const int m = a.s.order.planes[(long)kp * G + g];
-    const int mu = min(m, a.plane_cap);
-    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + a.s.order.seg_off[(long)kp * G + g];
-    uint32_t pl[8], header;
-    load_segment(seg, mu, half, pl, header);
-    unpack_half_f16(pl, affine_from_header(header, mu), vals);
-  } else {
+  const int row = t >= 0 ? a.s.pieces[t] : 0;
+  const long toff = t >= 0 ? a.s.tok_off[t] : 0;
+  stage_table_column(a.s, a.G, g, tab);
+  __syncthreads();
+  const SegmentWords sw = load_token_segment(a.s, tab, t, row, toff, a.plane_cap);
+  uint32_t vals[2][16];  // half h: components 32h .. 32h+31 as packed fp16 pairs
+  if (a.s.format == DKV_FMT_LADDER) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) vals[j] = 0u;
+    for (int h = 0; h < 2; ++h) {
+      uint32_t cw[8];
+      ladder_segment_half(sw.w, sw.m, h, cw);
+      ladder_half_f16(cw, sw.header, vals[h]);
+    }
+  } else {
+    const AffineDq dq = affine_from_header(sw.header, sw.m);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t pl[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) pl[q] = sw.w[2 * q + h];
+      unpack_half_f16(pl, dq, vals[h]);
+    }
   }
-  // components half*32 + 8*c .. +8 (c = 0..3): ks = 2*half + c/2, lane half = c%2
+  // components 8c .. 8c+7 (c = 0..7) go to step ks = c/2, lane half c%2 of the slot's 32-slot block
   const long blk = (long)g * (a.n_slots / 32) + slot / 32;
   const int l32 = slot % 32;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int ks = 2 * half + c / 2, lh = c % 2;
-    uint4* dst = (uint4*)(a.coef + ((blk * 4 + ks) * 64 + lh * 32 + l32) * 8);
-    *dst = make_uint4(vals[4 * c], vals[4 * c + 1], vals[4 * c + 2], vals[4 * c + 3]);
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t* v = &vals[c / 4][4 * (c % 4)];
+    uint4* dst = (uint4*)(a.coef + ((blk * 4 + c / 2) * 64 + (c % 2) * 32 + l32) * 8);
+    *dst = make_uint4(v[0], v[1], v[2], v[3]);
   }
 }
 
@@ -1324,74 +1365,69 @@ struct K3aArgs {
 // components of one 16-slot block are 512 contiguous bytes, plus the
 // per-(group, slot) affine form (scale = span / 256, offset = low + span *
 // 2^-(m+1); 0 and 0 for a group without planes or a padding slot).  One block
-// = 128 slots x one group, whose codes are one contiguous 8 KB run.
+// = 256 slots x one group, one thread per slot, whose codes are one contiguous
+// 16 KB run; the codes are transposed through LDS.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(2 * kDecodeTok) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
-  __shared__ uint32_t tile[64][kDecodeTok / 4 + 1];  // [component][slot / 4], bytes of 4 slots per word
-  const int nsb = a.n_slots / kDecodeTok;
+__global__ __launch_bounds__(kDecodeSlots) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
+  __shared__ uint32_t tile[64][kDecodeSlots / 4 + 1];  // [component][slot / 4], bytes of 4 slots per word
+  extern __shared__ int2 tab[];
+  const int nsb = a.n_slots / kDecodeSlots;
   const int2 bg = decode_block(a.G, nsb * a.G);
   const int sb = bg.x, g = bg.y;
-  if (sb >= nsb) return;
-  const int tl = threadIdx.x >> 1, half = threadIdx.x & 1;
-  const int slot = sb * kDecodeTok + tl;
+  if (sb >= nsb) return;  // the whole block
+  const int tl = threadIdx.x;
+  const int slot = sb * kDecodeSlots + tl;
   const int t = slot_token(a, slot);
-  uint32_t cw[8];
-  float2 aff = make_float2(0.0f, 0.0f);
-  if (t >= 0 && a.s.format == DKV_FMT_LADDER) {
+  const int row = t >= 0 ? a.s.pieces[t] : 0;
+  const long toff = t >= 0 ? a.s.tok_off[t] : 0;
+  stage_table_column(a.s, a.G, g, tab);
+  __syncthreads();
+  const SegmentWords sw = load_token_segment(a.s, tab, t, row, toff, 8);
+  uint32_t cw[2][8];  // byte i of cw[h][w] is component 32h + 4w + i
+  float2 aff;
+  if (a.s.format == DKV_FMT_LADDER) {
     // value = code * scale + low: the affine pair is (scale, low)
-    const int G = a.G;
-    const int r = a.s.pieces[t];
-    const bool ok = r >= 0 && r < a.s.ladder.rungs;
-    const int b = ok ? a.s.ladder.bits[(long)r * G + g] : 0;
-    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + (ok ? a.s.ladder.seg_off[(long)r * G + g] : 0);
-    uint32_t header;
-    load_ladder_half(seg, b, half, cw, header);
-    aff = make_float2(half_bits_to_float((uint16_t)(header >> 16)), half_bits_to_float((uint16_t)(header & 0xffffu)));
-  } else if (t >= 0) {
-    const int G = a.G;
-    const int kp = a.s.pieces[t];
-    const int m = a.s.order.planes[(long)kp * G + g];
-    const uint8_t* seg = a.s.blob + a.s.tok_off[t] + a.s.order.seg_off[(long)kp * G + g];
-    uint32_t pl[8], header;
-    load_segment(seg, m, half, pl, header);
-    cw[0] = assemble_codes<0>(pl);
-    cw[1] = assemble_codes<1>(pl);
-    cw[2] = assemble_codes<2>(pl);
-    cw[3] = assemble_codes<3>(pl);
-    cw[4] = assemble_codes<4>(pl);
-    cw[5] = assemble_codes<5>(pl);
-    cw[6] = assemble_codes<6>(pl);
-    cw[7] = assemble_codes<7>(pl);
-    const AffineDq dq = affine_from_header(header, m);
-    aff = make_float2(dq.scale, dq.offset);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) ladder_segment_half(sw.w, sw.m, h, cw[h]);
+    aff = make_float2(half_bits_to_float((uint16_t)(sw.header >> 16)),
+                      half_bits_to_float((uint16_t)(sw.header & 0xffffu)));
   } else {
 #pragma unroll
-    for (int w = 0; w < 8; ++w) cw[w] = 0u;
+    for (int h = 0; h < 2; ++h) {
+      uint32_t pl[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) pl[q] = sw.w[2 * q + h];
+      cw[h][0] = assemble_codes<0>(pl);
+      cw[h][1] = assemble_codes<1>(pl);
+      cw[h][2] = assemble_codes<2>(pl);
+      cw[h][3] = assemble_codes<3>(pl);
+      cw[h][4] = assemble_codes<4>(pl);
+      cw[h][5] = assemble_codes<5>(pl);
+      cw[h][6] = assemble_codes<6>(pl);
+      cw[h][7] = assemble_codes<7>(pl);
+    }
+    const AffineDq dq = affine_from_header(sw.header, sw.m);
+    aff = make_float2(dq.scale, dq.offset);
   }
-  if (half == 0) vaff[(long)g * a.n_slots + slot] = aff;
-  // byte i of cw[w] is component half*32 + 4w + i of token t
+  vaff[(long)g * a.n_slots + slot] = aff;
   uint8_t* tb8 = (uint8_t*)&tile[0][0];
-  constexpr int ROWB = (kDecodeTok / 4 + 1) * 4;
+  constexpr int ROWB = (kDecodeSlots / 4 + 1) * 4;
 #pragma unroll
-  for (int w = 0; w < 8; ++w)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tb8[(half * 32 + 4 * w + i) * ROWB + tl] = (uint8_t)(cw[w] >> (8 * i));
+    for (int w = 0; w < 8; ++w)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tb8[(h * 32 + 4 * w + i) * ROWB + tl] = (uint8_t)(cw[h][w] >> (8 * i));
   __syncthreads();
-  // 8 blocks of 16 slots x 64 components = 8 KB contiguous: thread k writes bytes 32k .. 32k+31,
-  // the 16 slots of block k / 32 for components 2 (k % 32) and 2 (k % 32) + 1
-  const int blk = threadIdx.x >> 5, c = 2 * (threadIdx.x & 31);
-  uint4 v, v2;
-  v.x = tile[c][blk * 4 + 0];
-  v.y = tile[c][blk * 4 + 1];
-  v.z = tile[c][blk * 4 + 2];
-  v.w = tile[c][blk * 4 + 3];
-  v2.x = tile[c + 1][blk * 4 + 0];
-  v2.y = tile[c + 1][blk * 4 + 1];
-  v2.z = tile[c + 1][blk * 4 + 2];
-  v2.w = tile[c + 1][blk * 4 + 3];
-  uint4* dst = (uint4*)(vcodes + vcode_index(g, c, (long)sb * kDecodeTok + blk * 16, a.n_slots));
-  dst[0] = v;
-  dst[1] = v2;
+  // the block's 16 blocks of 16 slots x 64 components are 16 KB of contiguous codes; store j of
+  // wave wv writes 16-slot block 4j + wv, component = lane: 1 KB of consecutive bytes per store
+  const int wv = tl >> 6, c = tl & 63;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int b16 = 4 * j + wv;
+    const uint4 v = make_uint4(tile[c][b16 * 4], tile[c][b16 * 4 + 1], tile[c][b16 * 4 + 2], tile[c][b16 * 4 + 3]);
+    *(uint4*)(vcodes + vcode_index(g, c, (long)sb * kDecodeSlots + b16 * 16, a.n_slots)) = v;
+  }
 }
 
 // 8 codes (bytes of lo, hi) -> 8 fp16 values equal to the codes.  (0x6400 | c)
@@ -1956,8 +1992,11 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   d.n_slots = L.n_slots;
   d.G = dkv::stream_groups(a->key);
   d.plane_cap = plane_cap;
-  const dim3 grid((unsigned)(((long)d.G * (L.n_slots / kDecodeTok) + 7) / 8 * 8));
-  hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), d);
+  const int key_rows = a->key.format == DKV_FMT_LADDER ? a->key.ladder.rungs : a->key.order.pieces + 1;
+  DKV_REQUIRE(key_rows <= kMaxTableRows, DKV_ESHAPE, "dkv_attend_prepare: key stream table has %d rows (at most %d)",
+              key_rows, kMaxTableRows);
+  const dim3 grid((unsigned)(((long)d.G * (L.n_slots / kDecodeSlots) + 7) / 8 * 8));
+  hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(kDecodeSlots), key_rows * sizeof(int2), dkv::as_stream(stream), d);
   rc = dkv::check_launch("decode_keys");
   if (rc || !a->value.blob) return rc;
   rc = dkv::check_stream(&a->value, "dkv_attend_prepare");
@@ -1967,7 +2006,10 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   DecodeArgs v = d;
   v.s = a->value;
   v.plane_cap = 8;
-  hipLaunchKernelGGL(decode_values_kernel, grid, dim3(2 * kDecodeTok), 0, dkv::as_stream(stream), v,
+  const int value_rows = a->value.format == DKV_FMT_LADDER ? a->value.ladder.rungs : a->value.order.pieces + 1;
+  DKV_REQUIRE(value_rows <= kMaxTableRows, DKV_ESHAPE,
+              "dkv_attend_prepare: value stream table has %d rows (at most %d)", value_rows, kMaxTableRows);
+  hipLaunchKernelGGL(decode_values_kernel, grid, dim3(kDecodeSlots), value_rows * sizeof(int2), dkv::as_stream(stream), v,
                      (uint8_t*)((char*)workspace + L.vcodes), (float2*)((char*)workspace + L.vaff));
   return dkv::check_launch("decode_values");
 }

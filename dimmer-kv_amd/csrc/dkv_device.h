@@ -178,13 +178,8 @@ DKV_DEVICE uint32_t spread_pairs(uint32_t x) {  // 4 two-bit fields (8 bits) -> 
   return (x & 0x3u) | ((x & 0xcu) << 6) | ((x & 0x30u) << 12) | ((x & 0xc0u) << 18);
 }
 
-DKV_DEVICE void load_ladder_half(const uint8_t* seg, int b, int half, uint32_t (&cw)[8], uint32_t& header) {
-  const uint32_t* w = (const uint32_t*)seg;
-  header = b > 0 ? w[0] : 0u;
-  const uint32_t* c = w + 1 + b * half;
-  uint32_t raw[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) raw[k] = k < b ? c[k] : 0u;
+// The b packed words of one half (raw[k], k < b; the rest ignored) -> the code-word form.
+DKV_DEVICE void ladder_half_codes(const uint32_t (&raw)[8], int b, uint32_t (&cw)[8]) {
   if (b == 4) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -200,6 +195,59 @@ DKV_DEVICE void load_ladder_half(const uint8_t* seg, int b, int half, uint32_t (
 #pragma unroll
     for (int k = 0; k < 8; ++k) cw[k] = raw[k];  // b == 8 (b == 0: all zero)
   }
+}
+
+DKV_DEVICE void load_ladder_half(const uint8_t* seg, int b, int half, uint32_t (&cw)[8], uint32_t& header) {
+  const uint32_t* w = (const uint32_t*)seg;
+  header = b > 0 ? w[0] : 0u;
+  const uint32_t* c = w + 1 + b * half;
+  uint32_t raw[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) raw[k] = k < b ? c[k] : 0u;
+  ladder_half_codes(raw, b, cw);
+}
+
+// A whole (token, group) segment: the header word and its first nwords code words (nwords even,
+// at most 16; the rest 0), read with one 16-byte load per four words (two for a final pair).
+// Plane segments hold word 2p + h = half h of plane p (nwords = 2m); ladder segments the b words
+// of half 0, then the b words of half 1 (nwords = 2b).  Segments are 4-byte aligned, which the
+// multi-word global loads accept.
+DKV_DEVICE void load_segment_words(const uint8_t* seg, int nwords, uint32_t& header, uint32_t (&w)[16]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const uint32_t* p = (const uint32_t*)seg;
+  header = nwords > 0 ? p[0] : 0u;
+  // full pieces and the final pair load into registers of their own and meet in selects after
+  // the loads, so no load waits for another (a shared destination would order them)
+  u32x4 v[4];
+  u32x2 tail = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = u32x4{0u, 0u, 0u, 0u};
+    if (4 * k + 4 <= nwords) __builtin_memcpy(&v[k], p + 1 + 4 * k, 16);
+  }
+  const int kt = nwords >> 2;  // the piece holding a final pair (nwords % 4 == 2)
+  if (nwords & 2) __builtin_memcpy(&tail, p + 1 + 4 * kt, 8);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const bool pair = (nwords & 2) && k == kt;
+    w[4 * k] = pair ? tail.x : v[k].x;
+    w[4 * k + 1] = pair ? tail.y : v[k].y;
+    w[4 * k + 2] = v[k].z;
+    w[4 * k + 3] = v[k].w;
+  }
+}
+
+// Half h (0 or 1) of a loaded ladder segment with b bits in the code-word form.
+DKV_DEVICE void ladder_segment_half(const uint32_t (&w)[16], int b, int h, uint32_t (&cw)[8]) {
+  uint32_t raw[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    // the half's words start at w[b * h]: select among the constant offsets b = 2, 4, 8
+    const uint32_t w2 = k + 2 < 16 ? w[k + 2] : 0u, w4 = k + 4 < 16 ? w[k + 4] : 0u, w8 = w[k + 8];
+    raw[k] = h == 0 ? w[k] : (b == 8 ? w8 : b == 4 ? w4 : w2);
+  }
+  ladder_half_codes(raw, b, cw);
 }
 
 // Ladder coefficient in the reference's fp32 operation order
