@@ -93,3 +93,25 @@ def test_noalloc_refuses_contexts_beyond_its_static_workspace():
     rc = lib.dkv_attend_layer_noalloc(ctypes.byref(a), None)
     assert rc == -3  # DKV_EWORKSPACE
     assert b"static maximum" in lib.dkv_last_error()
+
+
+def test_prepare_refuses_stream_tables_beyond_the_decode_lds_column():
+    """The decode kernels stage one group's column of the stream table in LDS; a ladder with more
+    rungs than that column holds is refused before any launch."""
+    lib = dkv_hip.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: refused before any device work
+    ladder = dkv_hip.Ladder(32, 5000, fake, fake, fake)
+    stream = dkv_hip.Stream(fake, fake, fake, dkv_hip.Order(), dkv_hip.DKV_FMT_LADDER, ladder)
+    cu_host = (ctypes.c_int32 * 2)(0, 1000)
+    a = dkv_hip.AttendArgs()
+    a.batch, a.q_len, a.layers, a.layer, a.kv_heads, a.head_dim, a.q_heads, a.rank = 1, 1, 28, 0, 8, 128, 24, 2048
+    a.scaling = 128 ** -0.5
+    a.key, a.value = stream, stream
+    a.cu_seqlens = a.positions = a.key_basis = a.value_basis = a.mean_k = a.mean_v = 256
+    a.rope_cos = a.rope_sin = a.query = a.out = 256
+    a.rope_rows = 1001
+    a.cu_seqlens_host = ctypes.cast(cu_host, ctypes.c_void_p).value
+    need = lib.dkv_attend_workspace_bytes(ctypes.byref(a))
+    assert need > 0
+    rc = lib.dkv_attend_prepare(ctypes.byref(a), ctypes.c_int32(8), fake, ctypes.c_size_t(need), None)
+    assert rc == -2 and b"table has 5000 rows" in lib.dkv_last_error()
