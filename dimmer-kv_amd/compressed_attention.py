@@ -375,7 +375,7 @@ class CompressedContext:
             self._score_prepared = None
         state = (self.score_plane_cap, self.key.version)
         if self._score_prepared != state:
-            dkv_hip.attend_prepare(args, self._score_workspace, self.score_plane_cap)
+            dkv_hip.attend_prepare(args, self._score_workspace, self.score_plane_cap, values=False)
             self._score_prepared = state
         dkv_hip.score_layer(args, key_question, self.importance, self._score_workspace)
 

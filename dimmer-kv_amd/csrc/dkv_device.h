@@ -243,9 +243,9 @@ DKV_DEVICE void ladder_segment_half(const uint32_t (&w)[16], int b, int h, uint3
   uint32_t raw[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
-    // the half's words start at w[b * h]: select among the constant offsets b = 2, 4, 8
-    const uint32_t w2 = k + 2 < 16 ? w[k + 2] : 0u, w4 = k + 4 < 16 ? w[k + 4] : 0u, w8 = w[k + 8];
-    raw[k] = h == 0 ? w[k] : (b == 8 ? w8 : b == 4 ? w4 : w2);
+    // the half's words start at w[b * h]: select among the constant offsets b = 2, 4, 8 (for
+    // b = 0 every word is 0)
+    raw[k] = h == 0 ? w[k] : (b == 8 ? w[k + 8] : b == 4 ? w[k + 4] : w[k + 2]);
   }
   ladder_half_codes(raw, b, cw);
 }

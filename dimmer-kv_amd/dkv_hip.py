@@ -221,8 +221,12 @@ def attend_workspace_bytes(args: AttendArgs) -> int:
     return n
 
 
-def attend_prepare(args: AttendArgs, workspace: torch.Tensor, plane_cap: int = 8) -> None:
-    """K1 into the workspace: every token's key codes decoded (to ``plane_cap`` planes) for K2."""
+def attend_prepare(args: AttendArgs, workspace: torch.Tensor, plane_cap: int = 8, values: bool = True) -> None:
+    """K1 into the workspace: every token's key codes decoded (to ``plane_cap`` planes) for K2, and
+    the value codes for K3 unless ``values`` is False (question scoring reads keys only)."""
+    if not values:
+        args = AttendArgs.from_buffer_copy(args)
+        args.value = Stream()  # no value blob: the library decodes the keys alone
     _check(lib().dkv_attend_prepare(ctypes.byref(args), c_i32(plane_cap), c_vp(ptr(workspace)),
                                     c_sz(workspace.numel()), c_vp(stream_handle())), "dkv_attend_prepare")
 

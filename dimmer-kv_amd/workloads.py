@@ -149,7 +149,7 @@ class QuestionStage:
     def score(self) -> torch.Tensor:
         """K1 (first plane_cap planes) + K4a over every layer -> importance [n]."""
         dkv_hip.score_begin(self.importance)
-        dkv_hip.attend_prepare(self.args[0], self.workspace, self.plane_cap)
+        dkv_hip.attend_prepare(self.args[0], self.workspace, self.plane_cap, values=False)
         for layer, a in enumerate(self.args):
             dkv_hip.score_layer(a, self.key_question[layer], self.importance, self.workspace)
         return self.importance
