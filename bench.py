@@ -252,6 +252,8 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
 
     data, encode_ms = timed(lambda: kvtc_storage.encode_bytes(codec, keys, values, codec.last_choice, m.recent))
     packed, deflate_ms = timed(lambda: kvtc_storage.deflate(data))
+    deflate_threads = min(16, os.cpu_count() or 1)
+    packed_mt, deflate_mt_ms = timed(lambda: kvtc_storage.deflate(data, threads=deflate_threads))
     _, inflate_ms = timed(lambda: kvtc_storage.inflate(packed))
     _, restore_ms = timed(lambda: kvtc_storage.restore_context(codec, data, model))
     _, decode_ms = timed(lambda: kvtc_storage.decode_bytes(codec, data))
@@ -310,6 +312,8 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
         "stored_bytes": len(data), "fp16_fraction": round(len(data) / (4 * features * tokens), 5),
         "deflated_bytes": len(packed),
         "encode_ms": round(encode_ms, 2), "deflate_ms": round(deflate_ms, 1), "inflate_ms": round(inflate_ms, 1),
+        "deflate_threaded": {"threads": deflate_threads, "ms": round(deflate_mt_ms, 1), "bytes": len(packed_mt),
+                             "inflates_to_input": kvtc_storage.inflate(packed_mt) == data},
         "restore_context_ms": round(restore_ms, 2), "decode_bytes_ms": round(decode_ms, 2),
         "wire_pack_us": round(pack_us, 1), "wire_unpack_us": round(unpack_us, 1),
         "wire_kernel_bytes": {"sections": int(section_bytes), "codes_and_affine": int(code_bytes),

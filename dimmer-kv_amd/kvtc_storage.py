@@ -31,8 +31,36 @@ WIDTHS = (2, 4, 8)
 HEADER_BYTES = 12  # int32 tokens, start, end
 
 
-def deflate(data: bytes, level: int = 6) -> bytes:
-    return zlib.compress(data, level)
+DEFLATE_PIECE = 1 << 20  # bytes per independently compressed piece of the threaded DEFLATE
+DEFLATE_WINDOW = 1 << 15  # DEFLATE's back-reference window
+
+
+def deflate(data: bytes, level: int = 6, threads: int = 1) -> bytes:
+    """zlib stream of ``data``.  ``threads`` = 1 is ``zlib.compress(data, level)`` itself, the
+    reference's bytes.  ``threads`` > 1 compresses 1 MiB pieces on that many threads (zlib releases
+    the GIL) and joins them into one zlib stream: each piece is raw DEFLATE primed with the
+    preceding 32 KiB as its window, ended by a sync flush (the last by the final block), behind the
+    standard header and before the adler32 of the whole input.  ``zlib.decompress`` reads it like
+    any zlib stream; its bytes differ from the one-thread form (blocks end at piece boundaries)."""
+    if threads <= 1 or len(data) <= DEFLATE_PIECE:
+        return zlib.compress(data, level)
+    from concurrent.futures import ThreadPoolExecutor
+
+    view = memoryview(data)
+    starts = range(0, len(data), DEFLATE_PIECE)
+
+    def piece(start: int) -> bytes:
+        end = min(start + DEFLATE_PIECE, len(data))
+        if start:
+            c = zlib.compressobj(level, zlib.DEFLATED, -15, zdict=view[max(0, start - DEFLATE_WINDOW):start])
+        else:
+            c = zlib.compressobj(level, zlib.DEFLATED, -15)
+        return c.compress(view[start:end]) + c.flush(zlib.Z_FINISH if end == len(data) else zlib.Z_SYNC_FLUSH)
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        body = b"".join(pool.map(piece, starts))
+    header = zlib.compress(b"", level)[:2]  # CMF/FLG of a zlib stream at this level
+    return header + body + zlib.adler32(data).to_bytes(4, "big")
 
 
 def inflate(data: bytes) -> bytes:

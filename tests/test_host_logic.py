@@ -131,3 +131,29 @@ def test_ladder_tables_match_oracle():
         hot_tier.LadderTables(bits * 0 + 3, None, "cpu")
     with pytest.raises(ValueError, match="groups of 64"):
         hot_tier.LadderTables(bits, None, "cpu", group=32)
+
+
+def test_threaded_deflate_is_one_zlib_stream():
+    """kvtc_storage.deflate: one thread gives zlib.compress's bytes (the reference's stored form);
+    several threads give one zlib stream of the same input, across piece boundaries and for inputs
+    of at most one piece, with a size within a fraction of a percent."""
+    import zlib
+
+    import kvtc_storage
+
+    rng = np.random.default_rng(3)
+    piece = kvtc_storage.DEFLATE_PIECE
+    big = (rng.integers(0, 16, 5 * piece + 123, dtype=np.uint8) * rng.integers(0, 2, 5 * piece + 123,
+                                                                           dtype=np.uint8)).tobytes()
+    assert kvtc_storage.deflate(big) == zlib.compress(big, 6)
+    threaded = kvtc_storage.deflate(big, threads=4)
+    assert zlib.decompress(threaded) == big
+    assert kvtc_storage.inflate(threaded) == big
+    assert len(threaded) < 1.002 * len(zlib.compress(big, 6))
+    # a long repeat across a piece boundary is still found through the primed window
+    rep = rng.integers(0, 256, 20_000, dtype=np.uint8).tobytes()
+    crossing = bytes(piece - 10_000) + rep + rep
+    assert zlib.decompress(kvtc_storage.deflate(crossing, threads=2)) == crossing
+    for n in (0, 1, piece, piece + 1, 2 * piece):
+        d = rng.integers(0, 4, n, dtype=np.uint8).tobytes()
+        assert zlib.decompress(kvtc_storage.deflate(d, threads=3)) == d
