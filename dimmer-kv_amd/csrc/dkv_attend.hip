@@ -23,10 +23,15 @@
 //                      coefficient-space partial sums.
 //   K3b basis_apply  : sum the partials over the splits and multiply once by
 //                      the value basis of the KV head (per 128-component
-//                      chunk); beside them, one workgroup per output row
-//                      merges the tiles' softmax statistics with the exact
-//                      tokens (sinks, recent, new) in one softmax.
-//   K3c finish       : out = row scale * (sum of chunk partials) + row base.
+//                      chunk and 64-dimension slice); beside them, one
+//                      workgroup per output row computes the exact tail
+//                      (sinks, recent window, new tokens): its scores, their
+//                      maximum and exponential sum, and the weighted values.
+//   K3c finish       : per output row, merge the tiles' softmax statistics
+//                      (Mc, Lc) with the exact tail's (Me, Le, ve) in one
+//                      softmax: out = (ec (sum of chunk partials + Lc mean_v)
+//                      + ee ve) / (ec Lc + ee Le), ec and ee taking Mc and Me
+//                      to the common maximum.
 #include <math.h>
 
 #include <mutex>
