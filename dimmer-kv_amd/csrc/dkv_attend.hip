@@ -218,7 +218,7 @@ DKV_DEVICE half8 query_frag_half(const typename QueryFrag<T>::type& f) {
 struct DecodeArgs {
   dkv_stream_t s;
   const int32_t* cu_seqlens;
-  uint16_t* coef;  // keys: fp16 in MFMA fragment order (see decode_keys_kernel)
+  uint16_t* coef;  // keys: fp16 in MFMA fragment order (see decode_keys_block)
   int batch, n_total, ntiles, n_slots, G, plane_cap;
 };
 
@@ -227,9 +227,9 @@ constexpr int kMaxTableRows = 4096;    // rows of a stream table one decode work
 
 // Block -> (slot block, group) with the group fastest and consecutive ids on
 // one XCD, so the blocks reading the same tokens' blobs share that XCD's L2.
-DKV_DEVICE int2 decode_block(int G, int nblocks) {
+DKV_DEVICE int2 decode_block(int G, int nblocks, int id) {
   const int per_xcd = (nblocks + 7) / 8;
-  const int lin = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  const int lin = (id & 7) * per_xcd + (id >> 3);
   return make_int2(lin / G, lin % G);  // (slot block, group); slot block may be out of range
 }
 
@@ -267,7 +267,10 @@ DKV_DEVICE SegmentWords load_token_segment(const dkv_stream_t& s, const int2* ta
   const int2 e = ok ? tab[row] : make_int2(0, 0);
   const int m = s.format == DKV_FMT_LADDER ? e.x : min(e.x, plane_cap);
   sw.m = m;
-  load_segment_words(s.blob + tok_off + e.y, 2 * m, sw.header, sw.w);
+  if (s.format == DKV_FMT_LADDER)
+    load_ladder_segment(s.blob + tok_off + e.y, m, sw.header, sw.w);
+  else
+    load_segment_words(s.blob + tok_off + e.y, 2 * m, sw.header, sw.w);
   return sw;
 }
 
@@ -312,10 +315,9 @@ DKV_DEVICE long sub_index(long row, int t, int nsub) { return ((row >> 3) * nsub
 // 16-byte stores.  The decoded keys depend on the stream only, so one decode
 // serves every layer.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kDecodeSlots) void decode_keys_kernel(DecodeArgs a) {
-  extern __shared__ int2 tab[];
+DKV_DEVICE void decode_keys_block(const DecodeArgs& a, int2* tab, int id) {
   const int nsb = a.n_slots / kDecodeSlots;
-  const int2 bg = decode_block(a.G, nsb * a.G);
+  const int2 bg = decode_block(a.G, nsb * a.G, id);
   const int sb = bg.x, g = bg.y;
   if (sb >= nsb) return;  // the whole block
   const int slot = sb * kDecodeSlots + threadIdx.x;
@@ -1373,11 +1375,10 @@ struct K3aArgs {
 // = 256 slots x one group, one thread per slot, whose codes are one contiguous
 // 16 KB run; the codes are transposed through LDS.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kDecodeSlots) void decode_values_kernel(DecodeArgs a, uint8_t* vcodes, float2* vaff) {
+DKV_DEVICE void decode_values_block(const DecodeArgs& a, uint8_t* vcodes, float2* vaff, int2* tab, int id) {
   __shared__ uint32_t tile[64][kDecodeSlots / 4 + 1];  // [component][slot / 4], bytes of 4 slots per word
-  extern __shared__ int2 tab[];
   const int nsb = a.n_slots / kDecodeSlots;
-  const int2 bg = decode_block(a.G, nsb * a.G);
+  const int2 bg = decode_block(a.G, nsb * a.G, id);
   const int sb = bg.x, g = bg.y;
   if (sb >= nsb) return;  // the whole block
   const int tl = threadIdx.x;
@@ -1433,6 +1434,19 @@ __global__ __launch_bounds__(kDecodeSlots) void decode_values_kernel(DecodeArgs 
     const uint4 v = make_uint4(tile[c][b16 * 4], tile[c][b16 * 4 + 1], tile[c][b16 * 4 + 2], tile[c][b16 * 4 + 3]);
     *(uint4*)(vcodes + vcode_index(g, c, (long)sb * kDecodeSlots + b16 * 16, a.n_slots)) = v;
   }
+}
+
+// K1 as one launch: blocks [0, key_blocks) decode the keys, the rest (when a value stream is given)
+// the values.  Not every block is resident at once, so the value blocks start as the key blocks
+// drain and their segment reads overlap the key blocks' operand writes.  Block ids of each part
+// keep the XCD pattern (key_blocks is a multiple of 8).
+__global__ __launch_bounds__(kDecodeSlots) void decode_codes_kernel(DecodeArgs k, DecodeArgs v, uint8_t* vcodes,
+                                                                    float2* vaff, int key_blocks) {
+  extern __shared__ int2 tab[];
+  if ((int)blockIdx.x < key_blocks)
+    decode_keys_block(k, tab, blockIdx.x);
+  else
+    decode_values_block(v, vcodes, vaff, tab, blockIdx.x - key_blocks);
 }
 
 // 8 codes (bytes of lo, hi) -> 8 fp16 values equal to the codes.  (0x6400 | c)
@@ -2000,23 +2014,26 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
   const int key_rows = a->key.format == DKV_FMT_LADDER ? a->key.ladder.rungs : a->key.order.pieces + 1;
   DKV_REQUIRE(key_rows <= kMaxTableRows, DKV_ESHAPE, "dkv_attend_prepare: key stream table has %d rows (at most %d)",
               key_rows, kMaxTableRows);
-  const dim3 grid((unsigned)(((long)d.G * (L.n_slots / kDecodeSlots) + 7) / 8 * 8));
-  hipLaunchKernelGGL(decode_keys_kernel, grid, dim3(kDecodeSlots), key_rows * sizeof(int2), dkv::as_stream(stream), d);
-  rc = dkv::check_launch("decode_keys");
-  if (rc || !a->value.blob) return rc;
-  rc = dkv::check_stream(&a->value, "dkv_attend_prepare");
-  if (rc) return rc;
-  DKV_REQUIRE(dkv::stream_groups(a->value) == dkv::stream_groups(a->key), DKV_ESHAPE,
-              "dkv_attend_prepare: K/V group mismatch");
+  const int key_blocks = (int)(((long)d.G * (L.n_slots / kDecodeSlots) + 7) / 8 * 8);
   DecodeArgs v = d;
-  v.s = a->value;
-  v.plane_cap = 8;
-  const int value_rows = a->value.format == DKV_FMT_LADDER ? a->value.ladder.rungs : a->value.order.pieces + 1;
-  DKV_REQUIRE(value_rows <= kMaxTableRows, DKV_ESHAPE,
-              "dkv_attend_prepare: value stream table has %d rows (at most %d)", value_rows, kMaxTableRows);
-  hipLaunchKernelGGL(decode_values_kernel, grid, dim3(kDecodeSlots), value_rows * sizeof(int2), dkv::as_stream(stream), v,
-                     (uint8_t*)((char*)workspace + L.vcodes), (float2*)((char*)workspace + L.vaff));
-  return dkv::check_launch("decode_values");
+  int value_blocks = 0, rows = key_rows;
+  if (a->value.blob) {
+    rc = dkv::check_stream(&a->value, "dkv_attend_prepare");
+    if (rc) return rc;
+    DKV_REQUIRE(dkv::stream_groups(a->value) == dkv::stream_groups(a->key), DKV_ESHAPE,
+                "dkv_attend_prepare: K/V group mismatch");
+    const int value_rows = a->value.format == DKV_FMT_LADDER ? a->value.ladder.rungs : a->value.order.pieces + 1;
+    DKV_REQUIRE(value_rows <= kMaxTableRows, DKV_ESHAPE,
+                "dkv_attend_prepare: value stream table has %d rows (at most %d)", value_rows, kMaxTableRows);
+    v.s = a->value;
+    v.plane_cap = 8;
+    value_blocks = key_blocks;
+    rows = std::max(rows, value_rows);
+  }
+  hipLaunchKernelGGL(decode_codes_kernel, dim3((unsigned)(key_blocks + value_blocks)), dim3(kDecodeSlots),
+                     rows * sizeof(int2), dkv::as_stream(stream), d, v, (uint8_t*)((char*)workspace + L.vcodes),
+                     (float2*)((char*)workspace + L.vaff), key_blocks);
+  return dkv::check_launch("decode_codes");
 }
 
 static int check_values(const dkv_attend_args_t* a, int& E_total) {

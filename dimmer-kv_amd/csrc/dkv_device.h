@@ -209,9 +209,8 @@ DKV_DEVICE void load_ladder_half(const uint8_t* seg, int b, int half, uint32_t (
 
 // A whole (token, group) segment: the header word and its first nwords code words (nwords even,
 // at most 16; the rest 0), read with one 16-byte load per four words (two for a final pair).
-// Plane segments hold word 2p + h = half h of plane p (nwords = 2m); ladder segments the b words
-// of half 0, then the b words of half 1 (nwords = 2b).  Segments are 4-byte aligned, which the
-// multi-word global loads accept.
+// Plane segments hold word 2p + h = half h of plane p (nwords = 2m).  Segments are 4-byte aligned,
+// which the multi-word global loads accept.
 DKV_DEVICE void load_segment_words(const uint8_t* seg, int nwords, uint32_t& header, uint32_t (&w)[16]) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -238,15 +237,38 @@ DKV_DEVICE void load_segment_words(const uint8_t* seg, int nwords, uint32_t& hea
   }
 }
 
-// Half h (0 or 1) of a loaded ladder segment with b bits in the code-word form.
+// A whole ladder segment with b bits (0, 2, 4 or 8): the header word, half h's b words in
+// w[8h .. 8h+b-1] (the rest 0).  Each half is read from its own address (word 1 + b h), so the
+// registers it lands in do not depend on b.
+DKV_DEVICE void load_ladder_segment(const uint8_t* seg, int b, uint32_t& header, uint32_t (&w)[16]) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const uint32_t* p = (const uint32_t*)seg;
+  header = b > 0 ? p[0] : 0u;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t* base = p + 1 + b * h;
+    u32x4 v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
+    u32x2 pair = {0u, 0u};
+    if (b >= 4) __builtin_memcpy(&v0, base, 16);
+    if (b == 8) __builtin_memcpy(&v1, base + 4, 16);
+    if (b == 2) __builtin_memcpy(&pair, base, 8);
+    w[8 * h + 0] = b == 2 ? pair.x : v0.x;
+    w[8 * h + 1] = b == 2 ? pair.y : v0.y;
+    w[8 * h + 2] = v0.z;
+    w[8 * h + 3] = v0.w;
+    w[8 * h + 4] = v1.x;
+    w[8 * h + 5] = v1.y;
+    w[8 * h + 6] = v1.z;
+    w[8 * h + 7] = v1.w;
+  }
+}
+
+// Half h (0 or 1) of a ladder segment loaded by load_ladder_segment, in the code-word form.
 DKV_DEVICE void ladder_segment_half(const uint32_t (&w)[16], int b, int h, uint32_t (&cw)[8]) {
   uint32_t raw[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    // the half's words start at w[b * h]: select among the constant offsets b = 2, 4, 8 (for
-    // b = 0 every word is 0)
-    raw[k] = h == 0 ? w[k] : (b == 8 ? w[k + 8] : b == 4 ? w[k + 4] : w[k + 2]);
-  }
+  for (int k = 0; k < 8; ++k) raw[k] = w[8 * h + k];
   ladder_half_codes(raw, b, cw);
 }
 
