@@ -252,11 +252,15 @@ size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);
  * scripts/progressive.py:47-55 dequantize at each token's hot planes): decodes
  * every compressed token's key codes, truncated to min(planes, plane_cap)
  * bit-planes (8 = all hot planes; scoring "with the first 2 planes" passes 2),
- * into the workspace in the MFMA operand layout.  The decoded keys depend on
- * the key stream only: call it once before the layers of a decode step (and
- * again after the stream changes, e.g. dkv_gather_cold); every later
- * dkv_attend_layer / dkv_attend_scores / dkv_score_layer on the same
- * workspace reads it. */
+ * into the workspace in the MFMA operand layout, and, when a->value.blob is
+ * non-null, every token's value codes (all hot planes) with their affine
+ * pairs for K3; a null value blob decodes the keys alone (question scoring
+ * reads no values).  The decoded codes depend on the streams only: call it
+ * once before the layers of a decode step (and again after a stream
+ * changes, e.g. dkv_gather_cold); every later dkv_attend_layer /
+ * dkv_attend_scores / dkv_score_layer on the same workspace reads it.  Each
+ * stream's table (pieces + 1 rows, or rungs) holds at most 4,096 rows
+ * (DKV_ESHAPE otherwise). */
 int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap, void* workspace, size_t workspace_bytes,
                        void* stream);
 int dkv_attend_layer(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream);
