@@ -57,6 +57,11 @@ def parse():
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (5 launches): the known-size kernel that "
                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    p.add_argument("--model", action="store_true",
+                   help="time greedy decoding through a random-weight HF Llama-3.2-1B-shaped model over an "
+                        "8K-token context compressed by --method (dkvtc@0.02:snap:floor1 or prog@0.02:r0.01), "
+                        "direct over the codes and over the rebuilt cache; one JSON line")
+    p.add_argument("--new-tokens", type=int, default=32, help="tokens generated per reply in --model")
     p.add_argument("--gemm-reference", action="store_true",
                    help="only time the bare fp16 GEMM of K2's key-rebuild shape at 3b-16k-3pct through "
                         "torch.matmul (hipBLASLt): a library figure beside the fused kernel; one JSON line")
@@ -119,17 +124,23 @@ def read_traffic(path: str):
     return None
 
 
-def host_cores() -> int:
-    """The cores this process may run on (its CPU affinity), capped by OMP_NUM_THREADS when that is set:
-    the host's share for this GPU."""
+def host_cores() -> tuple[int, str]:
+    """The cores this process may run on (its CPU affinity), capped by OMP_NUM_THREADS when that is set
+    (the host's share for this GPU), and a note of how the count was reached.  A cap below the affinity
+    is printed as a warning and recorded in the note, since it slows the CPU baseline."""
     try:
-        n = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
+        affinity = os.cpu_count() or 1
+    n, note = affinity, f"CPU affinity {affinity}"
     omp = os.environ.get("OMP_NUM_THREADS", "")
     if omp.isdigit() and int(omp) > 0:
-        n = min(n, int(omp))
-    return max(1, n)
+        note += f", OMP_NUM_THREADS={omp}"
+        if int(omp) < affinity:
+            n = int(omp)
+            print(f"[bench] warning: OMP_NUM_THREADS={omp} caps the CPU baseline below the {affinity} cores of "
+                  "this process's affinity", file=sys.stderr, flush=True)
+    return max(1, n), note
 
 
 def cpu_baseline(w, seconds: float):
@@ -144,7 +155,7 @@ def cpu_baseline(w, seconds: float):
     from oracle import attention_ref
 
     s = w.shape
-    cores = host_cores()
+    cores, core_note = host_cores()
     coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
     kb = w.synthetic_basis_host
     positions = w.context.positions.long().cpu()
@@ -175,9 +186,32 @@ def cpu_baseline(w, seconds: float):
     per_layer = float(np.median(passes))
     return {"value": 1.0 / (per_layer * s.layers), "unit": "tok/s", "cores": cores, "kind": "port",
             "sample": f"numpy fp32 oracle (oracle/attention_ref.attend over K1-decoded coefficients) of the same "
-                      f"workload on {cores} host cores: one warm-up layer, then 3 passes over {per_pass} of "
+                      f"workload on {cores} host cores ({core_note}): one warm-up layer, then 3 passes over {per_pass} of "
                       f"{s.layers} layers; median pass {per_layer * 1e3:.0f} ms/layer (passes "
                       f"{', '.join(f'{p * 1e3:.0f}' for p in passes)} ms), scaled x{s.layers}"}
+
+
+def held_memory(w) -> dict:
+    """GPU memory held for the conversation(s) of a workload, in MiB: the context's parts
+    (CompressedContext.held_bytes: packed codes as allocated, the decode workspace), the exact
+    cache the workload keeps beside it (float32 keys and values of the sinks, recent window and new
+    token, all layers), and the question stage's scoring workspace and importance vector.  The bases
+    (per model) are listed apart.  ``code_bytes`` is the reference's accounting of the packed content
+    (scripts/compressed_attention.py:91-94)."""
+    ctx = w.context
+    parts = ctx.held_bytes()
+    parts.pop("total")
+    if ctx.exact_cache is None:
+        parts["exact_cache"] = sum(t.numel() * t.element_size() for t in (w.key_exact, w.value_exact))
+    q = getattr(w, "question", None)
+    if q is not None:
+        parts["score_workspace"] = q.workspace.numel() + q.importance.numel() * 4 + q.idx.numel() * 4
+    mib = {k: round(v / 2**20, 2) for k, v in parts.items()}
+    mib["held_total"] = round(sum(parts.values()) / 2**20, 2)
+    mib["code_bytes_reference_accounting"] = round(ctx.code_bytes() / 2**20, 2)
+    mib["bases_per_model"] = round(ctx.basis_bytes() / 2**20, 2)
+    mib["unit"] = "MiB"
+    return mib
 
 
 def question_stage(w):
@@ -326,6 +360,161 @@ def storage_bench(reps: int = 3, cpu_tokens: int = 1024):
     print(json.dumps(result), flush=True)
 
 
+def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question: int = 12, seed: int = 8080):
+    """Greedy decoding through a Hugging Face Llama model, the way the reference times its direct
+    path (scripts/compressed_attention.py:140-169 ``greedy_answer``; scripts/test_compressed_attention.py):
+    a Llama-3.2-1B-shaped model (16 layers, 32 query / 8 KV heads x 64, MLP 8192, vocabulary 128,256)
+    with random bf16 weights from a local config (nothing is downloaded), an ``tokens``-token context
+    prefilled through the dimmer hook with score capture (dimmer.prefill_with_scores), compressed by
+    ``Methods.apply`` at 2 % (``dkvtc@0.02:snap:floor1``, or ``prog@0.02:r0.01``, whose question is
+    first scored over the codes and the top 1 % refined), then a question of ``question`` random
+    tokens answered with ``new_tokens`` greedy tokens: directly over the codes (CompressedContext
+    through the hook) and over the rebuilt cache (the hook's eager attention).  The bases are random
+    orthonormal rank-1,024 bases with the prefill's mean (a calibration stand-in), so the
+    replies are not meaningful text; the two paths' replies are compared as the reference does.
+
+    Decode tok/s = new_tokens / (time of a 1 + new_tokens reply - time of the question step alone),
+    each the median of 3 after a warm-up, with the host waiting for every token's argmax as
+    ``greedy_answer`` does.  A separate instrumented reply splits each decode token's time into the
+    attention hook's host time (Python and the C-ABI argument blocks, summed over the layers), its
+    device time (HIP events around each call: the exact tail's conversion and the decode kernels)
+    and the time outside those kernels (the model's own layers, logits, argmax, host waits)."""
+    import statistics
+
+    import torch
+
+    import common
+    import dimmer
+    import methods
+    import synth
+    from compressed_attention import CompressedContext, greedy_answer
+    from transformers import LlamaForCausalLM
+
+    class Tokenizer:  # ids as text; no special tokens
+        eos_token_id = -1
+        all_special_ids: list = []
+
+        def decode(self, ids, skip_special_tokens=True):
+            return " ".join(str(i) for i in ids)
+
+    dev = "cuda"
+    name = {"dkvtc": "dkvtc@0.02:snap:floor1", "prog": "prog@0.02:r0.01"}[method]
+    shape = synth.SHAPE_1B
+    config = synth.llama_config(shape)
+    config.intermediate_size, config.vocab_size, config.tie_word_embeddings = 8192, 128256, True
+    torch.manual_seed(seed)
+    model = LlamaForCausalLM(config).to(device=dev, dtype=torch.bfloat16).eval()
+    dimmer.install(model)
+    g = torch.Generator("cpu").manual_seed(seed + 1)
+    ids = torch.randint(0, config.vocab_size, (1, tokens), generator=g).to(dev)
+    tail = torch.randint(0, config.vocab_size, (1, question), generator=g).to(dev)
+    with torch.no_grad():
+        cache, scores = dimmer.prefill_with_scores(model, ids)
+    keys, values = common.cache_tensors(cache)
+    keys, values = [k.clone() for k in keys], [v.clone() for v in values]
+    del cache
+    # calibration stand-in: random orthonormal bases, the prefill's mean token vector per stream
+    import kvtc
+
+    ck = synth.kvtc_checkpoint(synth.make_context(shape, 64, seed=seed + 2))
+    cos, sin = kvtc.rope_tables(model, tokens, dev)
+    for kind, tensors in (("key", keys), ("value", values)):
+        rows = [kvtc.derotate(t, cos, sin) if kind == "key" else t.float() for t in tensors]
+        ck[kind]["mean"] = kvtc.token_matrix(rows).mean(dim=0).cpu()
+    m = methods.Methods("synthetic/llama-3.2", device=dev, model=model, kvtc=ck,
+                        progressive=synth.order_checkpoint(shape))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    compressed = m.apply(name, keys, values, scores)
+    torch.cuda.synchronize()
+    compress_s = time.perf_counter() - t0
+    refine_ms = fetched = None
+    if method == "dkvtc":
+        context = CompressedContext(m.codec("kvtc"), keys, values, model)
+        exact_kv = ([l.keys for l in context.exact_cache.layers], [l.values for l in context.exact_cache.layers])
+        rebuilt_kv = (compressed.keys, compressed.values)
+    else:
+        stored = compressed.stored
+        exact_kv = (stored.exact["key"], stored.exact["value"])
+        ask = common.build_cache([t.clone() for t in exact_kv[0]], [t.clone() for t in exact_kv[1]], model)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            _, _, fetched = compressed.refine(tail[0], tokens, exact_cache=ask)
+        torch.cuda.synchronize()
+        refine_ms = (time.perf_counter() - t0) * 1e3
+        context = stored.context(config.num_attention_heads,
+                                 common.build_cache([t.clone() for t in exact_kv[0]], [t.clone() for t in exact_kv[1]],
+                                                    model))
+        rebuilt_kv = stored.hot()
+    tok = Tokenizer()
+
+    def reply(direct: bool, n: int):
+        kv = exact_kv if direct else rebuilt_kv
+        cache = common.build_cache([t.clone() for t in kv[0]], [t.clone() for t in kv[1]], model)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        with torch.no_grad():
+            text, _ = greedy_answer(model, tok, context if direct else None, cache, tail, tokens,
+                                    max_new_tokens=n, stop_at_eos=False)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t, text
+
+    out = {}
+    for direct in (True, False):
+        reply(direct, 2)  # warm-up
+        first = statistics.median(reply(direct, 1)[0] for _ in range(3))
+        runs = [reply(direct, 1 + new_tokens) for _ in range(3)]
+        whole = statistics.median(r[0] for r in runs)
+        out[direct] = {"tok_s": new_tokens / (whole - first), "question_ms": first * 1e3, "reply": runs[0][1],
+                       "ms_per_token": (whole - first) / new_tokens * 1e3}
+    # instrumented reply: the attention hook's host and device time per decode token
+    plain = context.attend
+    calls = []
+
+    def timed(module, query, key, value, attention_mask, scaling):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t = time.perf_counter()
+        start.record()
+        result = plain(module, query, key, value, attention_mask, scaling)
+        end.record()
+        calls.append((query.shape[2], time.perf_counter() - t, start, end))
+        return result
+
+    context.attend = timed
+    try:
+        reply(True, 1 + new_tokens)
+    finally:
+        context.attend = plain
+    steps = [c for c in calls if c[0] == 1]
+    per = len(steps) / shape.layers
+    host_ms = sum(c[1] for c in steps) * 1e3 / per
+    device_ms = sum(c[2].elapsed_time(c[3]) for c in steps) / per
+    direct = out[True]
+    held = {k: round(v / 2**20, 2) for k, v in context.held_bytes().items()}
+    result = {
+        "metric": f"greedy decode tok/s through HF Llama (1B shape, {tokens}-token context, {name})",
+        "value": round(direct["tok_s"], 2), "unit": "tok/s", "higher_is_better": True, "data": "synthetic",
+        "model": "Llama-3.2-1B shape, random bf16 weights (local config)",
+        "method": name, "context_tokens": tokens, "question_tokens": question, "new_tokens": new_tokens,
+        "rebuilt_tok_s": round(out[False]["tok_s"], 2),
+        "same_reply_as_rebuilt": direct["reply"] == out[False]["reply"],
+        "question_ms": {"direct": round(direct["question_ms"], 2), "rebuilt": round(out[False]["question_ms"], 2)},
+        "per_token_ms": {"wall": round(direct["ms_per_token"], 3), "attention_host": round(host_ms, 3),
+                         "attention_device": round(device_ms, 3),
+                         "outside_attention_kernels": round(direct["ms_per_token"] - device_ms, 3),
+                         "layers": shape.layers},
+        "compress_s": round(compress_s, 2),
+        "held_MiB": held,
+        "reference_context": "FINDINGS.md:794-798, 927: 38.6-40.5 tok/s direct (22-29 tok/s for "
+                             "dkvtc@0.02-0.03), 1B, ~8K tokens, RTX 5060 laptop GPU: other hardware and real "
+                             "weights, not a like-for-like comparison",
+    }
+    if refine_ms is not None:
+        result["refine"] = {"ms": round(refine_ms, 2), "fetched_bytes": fetched}
+    print(json.dumps(result), flush=True)
+
+
 def encode_bench(reps: int = 3):
     """The progressive encoder at the 3B 16K workload (Llama-3.2-3B shape, 16,384 tokens, 3 % budget,
     2-plane floor; the reference's ProgressiveCodec.encode with kvtc's floor rule): one JSON line with
@@ -387,6 +576,9 @@ def main():
         return
     if args.encode:
         encode_bench()
+        return
+    if args.model:
+        model_bench(args.method, args.new_tokens)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): this build runs the decode path on a "
@@ -516,6 +708,7 @@ def main():
     }
     if question is not None:
         result["question"] = question
+    result["memory"] = held_memory(w)
     if not args.no_cpu_baseline and args.workload != "3b-ragged-32":
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)

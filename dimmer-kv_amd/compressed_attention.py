@@ -245,6 +245,33 @@ class CompressedContext:
         layers = self.exact_cache.layers
         return sum((l.keys.numel() + l.values.numel()) * l.keys.element_size() for l in layers)
 
+    def workspace_bytes(self) -> int:
+        """The working memory this context keeps once allocated: the per-step decode workspace (key
+        operands, value codes and affine pairs decoded once per step, per-layer probabilities and
+        partials; dkv_attend_workspace_bytes) and, after a question, the scoring workspace
+        (dkv_score_workspace_bytes)."""
+        return sum(t.numel() for t in (self._workspace, self._score_workspace) if t is not None)
+
+    def held_bytes(self) -> dict:
+        """GPU memory held for this conversation, in parts (bytes): ``codes`` the packed streams as
+        allocated (``code_bytes`` is the reference's accounting of their content), ``exact_rung``
+        float32 rows of exact-rung tokens, ``exact_cache`` the sinks and recent window kept here,
+        ``decode_workspace`` and ``score_workspace`` (see ``workspace_bytes``), and ``total``.  The
+        bases (``basis_bytes``) are per model and not included."""
+        extra = 0
+        if self.extra is not None:
+            extra = sum(t.numel() * t.element_size() for kind in ("key", "value") for t in self.extra[kind])
+        parts = {
+            "codes": self.key.device_bytes() + self.value.device_bytes() + self.cu.numel() * 4
+                     + self.positions.numel() * self.positions.element_size(),
+            "exact_rung": extra,
+            "exact_cache": self.exact_bytes(),
+            "decode_workspace": 0 if self._workspace is None else self._workspace.numel(),
+            "score_workspace": 0 if self._score_workspace is None else self._score_workspace.numel(),
+        }
+        parts["total"] = sum(parts.values())
+        return parts
+
     # ----- attention -----
     def _exact_offsets(self, lengths: tuple[int, ...]):
         if lengths not in self._cu_exact:

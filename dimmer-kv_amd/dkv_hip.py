@@ -179,10 +179,32 @@ def centered_rows(tensors, cos, sin, mean, start: int, end: int, out) -> None:
     first = tensors[0]
     if first.dtype not in _DTYPE:
         raise ValueError(f"centered_rows: cache dtype {first.dtype} not supported")
-    if any(t.shape != first.shape or t.dtype != first.dtype or t.device != first.device for t in tensors):
-        raise ValueError("centered_rows: the layers' caches must share shape, dtype and device")
-    ptrs = torch.tensor([ptr(t) for t in tensors], dtype=torch.int64).to(first.device)
+    if first.dim() != 4 or first.shape[0] != 1:
+        raise ValueError(f"centered_rows: caches must be [1, heads, tokens, head_dim] (got {tuple(first.shape)})")
+    if any(t.shape != first.shape or t.dtype != first.dtype or t.device != first.device or not t.is_contiguous()
+           for t in tensors):
+        raise ValueError("centered_rows: the layers' caches must be contiguous and share shape, dtype and device")
     _, heads, tokens, head_dim = first.shape
+    width = len(tensors) * heads * head_dim
+    if not 0 <= start <= end <= tokens:
+        raise ValueError(f"centered_rows: need 0 <= start <= end <= {tokens} (got {start}, {end})")
+
+    def need(t, name, ok_shape, want):
+        if (t is None or t.dtype != torch.float32 or t.device != first.device or not t.is_contiguous()
+                or not ok_shape(tuple(t.shape))):
+            got = "None" if t is None else f"{t.dtype} {tuple(t.shape)} on {t.device}"
+            raise ValueError(f"centered_rows: {name} must be a contiguous float32 tensor {want} on {first.device} "
+                             f"(got {got})")
+
+    if (cos is None) != (sin is None):
+        raise ValueError("centered_rows: give both cos and sin (keys) or neither (values)")
+    if cos is not None:
+        for t, name in ((cos, "cos"), (sin, "sin")):
+            need(t, name, lambda sh: len(sh) == 2 and sh[0] >= end and sh[1] == head_dim,
+                 f"[>= {end} positions, {head_dim}]")
+    need(mean, "mean", lambda sh: sh == (width,), f"[{width}]")
+    need(out, "out", lambda sh: sh == (end - start, width), f"[{end - start}, {width}]")
+    ptrs = torch.tensor([ptr(t) for t in tensors], dtype=torch.int64).to(first.device)
     _check(lib().dkv_centered_rows(c_vp(ptr(ptrs)), c_i32(_DTYPE[first.dtype]), c_i32(len(tensors)), c_i32(heads),
                                    c_i32(tokens), c_i32(head_dim), c_vp(ptr(cos)), c_vp(ptr(sin)), c_vp(ptr(mean)),
                                    c_i32(start), c_i32(end), c_vp(ptr(out)), c_vp(stream_handle())),

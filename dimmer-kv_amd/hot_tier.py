@@ -72,6 +72,11 @@ def _nonnull(t: torch.Tensor) -> torch.Tensor:
     return t if t.numel() else torch.zeros(1, dtype=t.dtype, device=t.device)[:0]
 
 
+def _nbytes(*tensors) -> int:
+    """Bytes of the device allocations among ``tensors`` (None and host tensors count 0)."""
+    return sum(t.numel() * t.element_size() for t in tensors if t is not None and t.is_cuda)
+
+
 def _exclusive_cumsum(sizes: torch.Tensor) -> tuple[torch.Tensor, int]:
     off = _nonnull(torch.zeros(sizes.numel(), dtype=torch.int64, device=sizes.device))
     if sizes.numel() > 1:
@@ -176,6 +181,13 @@ class PackedStream:
     def cold_bytes(self) -> int:
         return int((self.tables.full_bytes - self.tables.prefix64[self.pieces.long()]).sum())
 
+    def device_bytes(self) -> int:
+        """GPU memory this stream holds: the hot blob as allocated (with the room for refined tokens),
+        the per-token offsets and piece counts, a device cold tier and its offsets, and the refine
+        bookkeeping (first-entry tags, the host tier's device staging)."""
+        return _nbytes(self.blob, self.tok_off, self.pieces, self.cold, self.cold_off, self._owner, self._stage_off,
+                       self._stage_dev)
+
     def refine(self, rows: torch.Tensor) -> int:
         """K4c: fetch the cold pieces of ``rows`` (stream-local) -> bytes fetched (progressive.py:232).
 
@@ -189,17 +201,25 @@ class PackedStream:
             raise ValueError("this stream was packed without a cold tier")
         if self.cold_on_host:
             return self._refine_host(rows)
-        counts = self.refine_async(rows).cpu()
-        if int(counts[1]):  # nothing was merged: give the slots back
-            self.refined -= rows.numel()
+        return self.settle_refine(self.refine_async(rows).cpu(), rows.numel())
+
+    def settle_refine(self, counts: torch.Tensor, k: int) -> int:
+        """The result of a ``refine_async`` of ``k`` rows, once its counts are on the host: the bytes
+        fetched, or, when a row lay outside the stream (the kernel then merged nothing), the ``k``
+        slots and the version bump given back and ValueError raised.  Every caller of
+        ``refine_async`` settles its counts here."""
+        if int(counts[1]):
+            self.refined -= k
+            self.version -= 1
             raise ValueError(f"refine rows must lie in 0..{self.n - 1}")
         return int(counts[0])
 
     def refine_async(self, rows: torch.Tensor) -> torch.Tensor:
         """Device cold tier: ``refine`` without a host round trip (dkv_refine_rows).  Returns a device
         int64 [2]: the bytes fetched and a flag set when a row lies outside the stream (then nothing
-        was merged); reading it is the caller's synchronisation.  Each distinct row's full blob goes
-        to the slot of its first entry, so the refined area grows by ``rows.numel()`` slots."""
+        was merged); the caller reads it (its synchronisation) and passes it to ``settle_refine``.
+        Each distinct row's full blob goes to the slot of its first entry, so the refined area grows
+        by ``rows.numel()`` slots (the host tier's ``refine`` uses one slot per distinct row)."""
         if self.cold is None or self.cold_on_host:
             raise ValueError("refine_async needs a device cold tier")
         device = self.blob.device
@@ -358,6 +378,10 @@ class LadderStream:
     def hot_bytes(self) -> int:
         """Bytes held for this stream's tokens: the rung sizes (scripts/kvtc.py:243 accounting)."""
         return self.used
+
+    def device_bytes(self) -> int:
+        """GPU memory this stream holds: the blob as allocated, the per-token offsets and rungs."""
+        return _nbytes(self.blob, self.tok_off, self.pieces)
 
     def refine(self, rows: torch.Tensor) -> int:
         raise ValueError("kvtc ladder streams have no cold tier to refine from")

@@ -211,15 +211,18 @@ def budget_per_stream(shape: ModelShape, tokens: int, sinks: int, recent: int, b
 def make_context(shape: ModelShape, tokens: int, seed: int, sinks: int = 4, recent: int = 32,
                  budget: float | None = None, zero_frac: float = 0.05, floor: int = 2, p: float | None = None,
                  mean_scale: float = 0.01, device="cpu", basis=None, mean=None,
-                 budget_over_middle: bool = False) -> SyntheticContext:
+                 budget_over_middle: bool = False, budget_shape: ModelShape | None = None) -> SyntheticContext:
     """``basis`` / ``mean`` (dicts by stream) let several conversations share one model's tables.
     ``budget_over_middle`` applies ``budget`` to the compressed tokens alone (budget x FP16 bytes per
-    compressed token) instead of the whole conversation with its exact tokens."""
+    compressed token) instead of the whole conversation with its exact tokens.  ``budget_shape`` is
+    the model whose FP16 bytes the budget is a fraction of (default ``shape``): a few-layer slice of a
+    model then gets the plane maps the whole model's budget gives."""
     middle = max(0, tokens - min(sinks, tokens) - recent)
     stream_budget = None
     if budget is not None:
-        stream_budget = (budget * shape.exact_bytes - 1 if budget_over_middle
-                         else budget_per_stream(shape, tokens, sinks, recent, budget))
+        bshape = budget_shape or shape
+        stream_budget = (budget * bshape.exact_bytes - 1 if budget_over_middle
+                         else budget_per_stream(bshape, tokens, sinks, recent, budget))
     if basis is None:
         basis = {"key": orthonormal_basis(shape.features, shape.rank, seed + 1, device),
                  "value": orthonormal_basis(shape.features, shape.rank, seed + 2, device)}

@@ -136,10 +136,11 @@ class QuestionStage:
         self.importance = torch.empty(w.context.key.n, dtype=torch.float32, device=queries.device)
 
     @classmethod
-    def build(cls, w, ctx, seed, fraction, q_len=64):
+    def build(cls, w, ctx, seed, fraction, q_len=64, query_scale=1.0):
+        """``q_len`` question tokens of N(0, query_scale^2) bf16 queries per layer, random question keys."""
         s = w.shape
         device = w.queries.device
-        queries = synth.make_queries(s, q_len, seed, device, torch.bfloat16)
+        queries = synth.make_queries(s, q_len, seed, device, torch.bfloat16, query_scale)
         g = torch.Generator("cpu").manual_seed(seed + 1)
         key_question = (torch.randn(s.layers, s.kv_heads, q_len, s.head_dim, generator=g) * 0.5).to(device)
         e_ctx = w.key_exact.shape[2] - w.q_len  # context exact tokens (sinks + recent)
@@ -165,10 +166,17 @@ class QuestionStage:
         if any(st.cold_on_host for st in streams):
             rows = self.idx.long()
             return sum(st.refine(rows) for st in streams)
-        counts = (streams[0].refine_async(self.idx) + streams[1].refine_async(self.idx)).cpu()
-        if int(counts[1]):
-            raise ValueError("refine rows out of range")
-        return int(counts[0])
+        k = self.idx.numel()
+        counts = torch.stack([st.refine_async(self.idx) for st in streams]).cpu()  # one synchronisation
+        fetched, error = 0, None
+        for st, c in zip(streams, counts):
+            try:
+                fetched += st.settle_refine(c, k)
+            except ValueError as e:  # settle the other stream too before raising
+                error = e
+        if error is not None:
+            raise error
+        return fetched
 
 
 def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, refine_capacity: int = 0,
@@ -188,18 +196,21 @@ def _pack_streams(coefs: dict, planes: dict, shape: synth.ModelShape, device, re
 def build_decode(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", q_len: int = 1, query_scale: float = 1.0,
                  shape: synth.ModelShape | None = None, tokens: int | None = None, budget: float | None = None,
                  query_dtype: torch.dtype | None = None, keep_host_basis: bool = False,
-                 refine_fraction: float = 0.0, cold_tier: str = "device") -> DecodeWorkload:
-    """A single-conversation decode workload (configs 0-2).  ``keep_host_basis`` keeps float32
-    host copies of the bases (for the CPU baseline); ``refine_fraction`` > 0 keeps a cold tier
-    (in device memory, or pinned host memory with ``cold_tier="host"``) and room to refine that
-    fraction of the tokens (the question stage)."""
+                 refine_fraction: float = 0.0, cold_tier: str = "device", budget_shape: synth.ModelShape | None = None,
+                 question_scale: float = 1.0) -> DecodeWorkload:
+    """A single-conversation decode workload (a ``WORKLOADS`` entry, or any shape and length).
+    ``keep_host_basis`` keeps float32 host copies of the bases (for the CPU baseline);
+    ``refine_fraction`` > 0 keeps a cold tier (in device memory, or pinned host memory with
+    ``cold_tier="host"``) and room to refine that fraction of the tokens, and builds the question
+    stage (64 bf16 query tokens of N(0, question_scale^2)).  ``budget_shape`` draws the plane maps
+    for that model's budget (a few-layer slice of a larger model)."""
     if name in WORKLOADS:
         s0, t0, b0, qd0 = WORKLOADS[name]
         shape, tokens = shape or s0, tokens or t0
         budget = b0 if budget is None else budget
         query_dtype = query_dtype or qd0
     ctx = synth.make_context(shape, tokens, seed, budget=budget, device=device,
-                             budget_over_middle=name in BUDGET_OVER_MIDDLE)
+                             budget_over_middle=name in BUDGET_OVER_MIDDLE, budget_shape=budget_shape)
     capacity = int(round(refine_fraction * ctx.middle)) + 1 if refine_fraction > 0 else 0
     streams = _pack_streams(ctx.coef, ctx.planes, shape, device, capacity, cold_tier)
     cos, sin = synth.rope_tables(shape, tokens + max(q_len, 64), device)
@@ -224,7 +235,7 @@ def build_decode(name: str = "3b-16k-3pct", seed: int = 2024, device="cuda", q_l
     if keep_host_basis:
         w.synthetic_basis_host = {k: v.cpu().numpy() for k, v in ctx.basis.items()}
     if refine_fraction > 0:
-        w.question = QuestionStage.build(w, ctx, seed + 70, refine_fraction)
+        w.question = QuestionStage.build(w, ctx, seed + 70, refine_fraction, query_scale=question_scale)
     # drop the float32 device bases now that the fp16 kernel layouts exist
     ctx.basis.clear()
     w.synthetic = ctx

@@ -309,7 +309,10 @@ int dkv_topk(const float* scores, int32_t n, int32_t k, int32_t* idx_out, void* 
  * (dkv_attend_workspace_bytes) exceeds the maximum is rejected with
  * DKV_EWORKSPACE before anything is launched.  Every call decodes the codes
  * again (the array keeps only the last call's contents); calls in sequence are
- * independent, calls that overlap on one GPU race. */
+ * independent, calls that overlap on one GPU race.  The first call on a device
+ * looks up that device's address of the array (hipGetSymbolAddress) and must
+ * not be made under stream capture; later calls can be captured into a HIP
+ * graph. */
 #define DKV_NOALLOC_MAX_BYTES ((size_t)64 << 20)
 int dkv_attend_layer_noalloc(const dkv_attend_args_t* a, void* stream);
 

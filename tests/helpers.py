@@ -193,3 +193,38 @@ def assert_sensitive(ref: np.ndarray, uniform: np.ndarray, base, what="", rel_fr
     assert np.abs(diff).max() > factor * rel_max * moved, \
         f"{what}: uniform attention's largest difference {np.abs(diff).max():.3e} is within {factor} x the bar"
     return float(gap)
+
+
+def importance_bar(ref: np.ndarray, atol_rel=2e-3, rtol=1e-2) -> np.ndarray:
+    """The question-importance bar per token: atol_rel x max|ref| + rtol x |ref|."""
+    ref = np.asarray(ref, dtype=np.float64)
+    return atol_rel * np.abs(ref).max() + rtol * np.abs(ref)
+
+
+def assert_importance_close(got: np.ndarray, ref: np.ndarray, alternatives: dict | None = None, what="",
+                            rel_fro=1e-2, factor=20.0) -> tuple[float, float]:
+    """Question importance against the oracle: every token within ``importance_bar`` and a relative
+    Frobenius bound on the part of the importance the question moves (ref - mean(ref)).
+
+    ``alternatives`` maps a name to the importance a wrong kernel would produce (uniform attention,
+    keys rebuilt from 0 planes, ...), computed by the oracle on the same inputs.  Each must miss both
+    bars ``factor`` times over: its largest ratio to the elementwise bar and its relative Frobenius
+    distance.  A check that these alternatives would pass proves nothing, which happens when the
+    question's queries leave the attention nearly uniform."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert np.isfinite(ref).all() and np.isfinite(got).all(), f"{what}: non-finite importance"
+    bar = importance_bar(ref)
+    moved = max(np.linalg.norm(ref - ref.mean()), 1e-30)
+    for name, alt in (alternatives or {}).items():
+        d = np.abs(np.asarray(alt, np.float64) - ref)
+        ratio, fro_alt = float((d / bar).max()), float(np.linalg.norm(d) / moved)
+        assert ratio >= factor, f"{what}: {name} misses the elementwise bar only {ratio:.1f}x (need {factor}x)"
+        assert fro_alt >= factor * rel_fro, f"{what}: {name} is only {fro_alt:.3e} away (bar {rel_fro})"
+        print(f"  {what}: {name} misses the bar {ratio:.0f}x (relative Frobenius {fro_alt:.2e})", flush=True)
+    err = np.abs(got - ref)
+    worst = float((err / bar).max())
+    fro = float(np.linalg.norm(got - ref) / moved)
+    assert worst <= 1.0, f"{what}: importance max err {err.max():.3e} ({worst:.2f} x the bar; max {np.abs(ref).max():.3e})"
+    assert fro <= rel_fro, f"{what}: importance relative Frobenius error {fro:.3e} > {rel_fro}"
+    return float(err.max()), fro

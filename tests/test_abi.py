@@ -73,6 +73,41 @@ def test_cpu_tensors_are_refused():
         dkv_hip.ptr(torch.zeros(3))
 
 
+def test_centered_rows_refuses_wrong_tables_on_the_host():
+    """dkv_centered_rows reads cos/sin as float32 [positions][head_dim] and mean as [L*H*D], and
+    writes [end - start][L*H*D] floats: the binding refuses anything else before the kernel could
+    read or write out of bounds (the half-width attention RoPE table, a short output, an fp16 mean)."""
+    import torch
+
+    layers, heads, tokens, dim = 2, 4, 40, 64
+    caches = [torch.zeros(1, heads, tokens, dim, dtype=torch.float16) for _ in range(layers)]
+    cos = torch.ones(tokens, dim)
+    mean = torch.zeros(layers * heads * dim)
+    out = torch.empty(30, layers * heads * dim)
+    cases = [
+        (dict(cos=cos[:, :dim // 2].contiguous(), sin=cos[:, :dim // 2].contiguous()), "cos must be"),
+        (dict(cos=cos[:20], sin=cos[:20]), "cos must be"),
+        (dict(sin=None), "give both cos and sin"),
+        (dict(mean=mean.half()), "mean must be"),
+        (dict(mean=mean[:-1]), "mean must be"),
+        (dict(out=out[:-1]), "out must be"),
+        (dict(out=out.t()), "out must be"),
+        (dict(end=tokens + 1), "start <= end"),
+    ]
+    for change, message in cases:
+        kw = dict(cos=cos, sin=cos, mean=mean, start=5, end=35, out=out)
+        kw.update(change)
+        if "end" in change:
+            kw["out"] = torch.empty(kw["end"] - 5, layers * heads * dim)
+        with pytest.raises(ValueError, match=message):
+            dkv_hip.centered_rows(caches, kw["cos"], kw["sin"], kw["mean"], kw["start"], kw["end"], kw["out"])
+    with pytest.raises(ValueError, match="caches must be"):
+        dkv_hip.centered_rows([caches[0], caches[1][:, :2]], cos, cos, mean, 5, 35, out)
+    # well-formed host tensors get past the checks and are refused as host memory
+    with pytest.raises(ValueError, match="GPU"):
+        dkv_hip.centered_rows(caches, cos, cos, mean, 5, 35, out)
+
+
 def test_noalloc_refuses_contexts_beyond_its_static_workspace():
     """A 3B-shaped context of 100,000 compressed tokens needs far more than the static workspace:
     refused by the host-side checks, before any device work."""

@@ -99,6 +99,10 @@ def test_encode_stages_match_oracle(budget, weighted):
         assert np.array_equal(g_span.cpu().numpy().view(np.uint16), span.view(np.uint16))
         table = codec.error_table(coef).cpu().numpy()
         np.testing.assert_allclose(table, pr.error_table(c_np, codes, low, span), rtol=2e-5, atol=1e-9)
+        # the reference's signature, with the codes given: they must be quantize8's
+        assert torch.equal(codec.error_table(coef, g_codes, g_low, g_span), codec.error_table(coef))
+        with pytest.raises(ValueError, match="codes are not"):
+            codec.error_table(coef, g_codes ^ 1, g_low, g_span)
         # packed tiers byte for byte at the chosen prefixes
         pieces = stored.stores[kind].hot_pieces.cpu().numpy()
         hot, hot_off, cold, cold_off = packing_ref.pack(codes, low, span, pieces, order)

@@ -126,9 +126,22 @@ def test_prog_direct_matches_rebuilt_and_refine_over_codes():
     # refine: scored over the codes with a fresh exact cache, top tokens get their cold planes
     exact = common.build_cache([t.clone() for t in stored.exact["key"]], [t.clone() for t in stored.exact["value"]],
                                model)
+    packed = stored.stores["key"].packed
+    full = packed.tables.pieces
+    before = packed.pieces.long().cpu().numpy()
     with torch.no_grad():
         _, _, fetched = compressed.refine(tail[0], length, exact_cache=exact)
     assert fetched > 0
+    # the closure selects with dkv_topk (K4b): exactly the top 5 % of the same importance over the codes
+    from oracle import scoring_ref
+
+    count = scoring_ref.select_count(0.05, stored.end - stored.start)
+    after = packed.pieces.long().cpu().numpy()
+    chosen = set(scoring_ref.topk_indices(imp_codes, count).tolist())
+    refined = set(np.nonzero((after == full) & (before != full))[0].tolist())
+    assert refined == {t for t in chosen if before[t] != full}, "refined tokens are not the top-k of the importance"
+    print(f"  refine over the codes: top {count} by dkv_topk, {len(refined)} tokens refined, {fetched} B fetched",
+          flush=True)
     hot_k, hot_v = stored.hot()
     exact = common.build_cache([t.clone() for t in stored.exact["key"]], [t.clone() for t in stored.exact["value"]],
                                model)

@@ -64,6 +64,19 @@ def test_progressive_order_mismatch_raises():
         progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), order, "cpu", synth.RopeModel(shape))
 
 
+def test_progressive_encode_refuses_a_cpu_codec():
+    """The encoder's stages are HIP kernels: a codec built on the CPU says so instead of failing deep
+    inside the binding."""
+    import progressive
+
+    shape, ctx = _small()
+    codec = progressive.ProgressiveCodec(synth.kvtc_checkpoint(ctx), synth.order_checkpoint(shape), "cpu",
+                                         synth.RopeModel(shape))
+    keys, values = synth.prefill_cache(ctx, dtype=torch.float32)
+    with pytest.raises(ValueError, match="runs on the GPU"):
+        codec.encode(keys, values, 0.3, 8)
+
+
 def test_synthetic_checkpoints_match_oracle_tables():
     shape, ctx = _small()
     order = synth.order_checkpoint(shape)["key"]
@@ -157,3 +170,19 @@ def test_threaded_deflate_is_one_zlib_stream():
     for n in (0, 1, piece, piece + 1, 2 * piece):
         d = rng.integers(0, 4, n, dtype=np.uint8).tobytes()
         assert zlib.decompress(kvtc_storage.deflate(d, threads=3)) == d
+
+
+def test_failed_refine_gives_back_slots_and_version():
+    """``PackedStream.settle_refine``: the device kernel flags a row outside the stream and merges
+    nothing, so the refine slots and the version bump that ``refine_async`` took are given back
+    (whichever caller settles: ``refine`` or the question stage's gather of both streams)."""
+    from hot_tier import PackedStream
+
+    st = PackedStream.__new__(PackedStream)
+    st.pieces = torch.zeros(10, dtype=torch.int16)
+    st.refined, st.version = 12, 5  # as refine_async leaves them after taking 4 slots and one version
+    with pytest.raises(ValueError, match="refine rows must lie in 0..9"):
+        st.settle_refine(torch.tensor([0, 1]), 4)
+    assert (st.refined, st.version) == (8, 4)
+    assert st.settle_refine(torch.tensor([2176, 0]), 4) == 2176
+    assert (st.refined, st.version) == (8, 4)

@@ -1,7 +1,8 @@
 """The allocation-free entry point (dkv_attend_layer_noalloc: the K1 decode and one layer with
 the library's static workspace) against the existing entry points with a caller workspace
 (dkv_attend_prepare + dkv_attend_layer): identical outputs on calls in a row, the second
-context smaller than the first, so it runs over what the first left in the static array."""
+context smaller than the first, so it runs over what the first left in the static array; and
+the same calls captured in a HIP graph (after the first, eager call on the device)."""
 
 from __future__ import annotations
 
@@ -53,3 +54,39 @@ def test_noalloc_matches_workspace_entry_points():
         dkv_hip.attend_layer_noalloc(a)
     torch.cuda.synchronize()
     assert torch.equal(big.outs, refs[0])
+
+
+def test_noalloc_calls_replay_from_a_graph():
+    """Two layers of dkv_attend_layer_noalloc recorded in one HIP graph, after an eager call on the
+    device (the first call looks up the static array's address): every replay equals the
+    workspace entry points' output bit for bit, with eager noalloc calls on another, larger
+    context between the replays overwriting the static array."""
+    import dkv_hip
+
+    print("[case] dkv_attend_layer_noalloc under graph capture: 1B shape, 700 tokens", flush=True)
+    w, other = _workload(700, 13), _workload(1500, 14)
+    ref = _with_workspace(w)
+    for a in w.args:  # eager: the device's array address is looked up here, outside any capture
+        dkv_hip.attend_layer_noalloc(a)
+    torch.cuda.synchronize()
+    assert torch.equal(w.outs, ref)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for a in w.args:
+            dkv_hip.attend_layer_noalloc(a)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for a in w.args:
+            dkv_hip.attend_layer_noalloc(a)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        w.outs.fill_(float("nan"))
+        for a in other.args:  # leaves the other context's workspace in the static array
+            dkv_hip.attend_layer_noalloc(a)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(w.outs, ref), f"replay {rep}: max abs diff {(w.outs - ref).abs().max().item():.3e}"
