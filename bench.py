@@ -403,7 +403,8 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
     config = synth.llama_config(shape)
     config.intermediate_size, config.vocab_size, config.tie_word_embeddings = 8192, 128256, True
     torch.manual_seed(seed)
-    model = LlamaForCausalLM(config).to(device=dev, dtype=torch.bfloat16).eval()
+    with torch.device(dev):  # initialise the weights on the GPU
+        model = LlamaForCausalLM(config).to(dtype=torch.bfloat16).eval()
     dimmer.install(model)
     g = torch.Generator("cpu").manual_seed(seed + 1)
     ids = torch.randint(0, config.vocab_size, (1, tokens), generator=g).to(dev)
