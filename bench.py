@@ -143,49 +143,97 @@ def host_cores() -> tuple[int, str]:
     return max(1, n), note
 
 
+def _oracle_conversations(w):
+    """The oracle's inputs for a workload, one entry per conversation it times: (coefficients per stream
+    [n, r] float32, host bases [F, r] per stream, RoPE cos/sin rows [n, d] of its compressed tokens,
+    its batch index, exact-token range, its share of the step's compressed tokens).
+
+    prog@ workloads: the K1-decoded coefficients of the packed streams and the synthetic bases.  dkvtc
+    (``w.codec``): the codec's own coefficients of the kept tokens with its full-rank bases, as the
+    parity tests compare them.  Ragged batches: the shortest, a middle and the longest conversation,
+    which together stand for the batch in proportion to their tokens."""
+    import numpy as np
+    import torch
+
+    s = w.shape
+
+    def rope_rows(positions):
+        cos = w.tables.rope_cos.cpu()[positions].numpy()
+        sin = w.tables.rope_sin.cpu()[positions].numpy()
+        return np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
+
+    if hasattr(w, "codec"):
+        codec = w.codec
+        start, _ = codec.last_span
+        kept = codec.last_choice["key"].cpu().numpy() >= 0
+        coef = {k: codec.last_coefficients[k].float().cpu().numpy()[kept] for k in ("key", "value")}
+        basis = {k: codec.streams[k].basis.cpu().numpy() for k in ("key", "value")}
+        n_extra = 0 if w.context.extra is None else w.context.extra["key"][0].shape[1]
+        cos, sin = rope_rows(torch.from_numpy(np.nonzero(kept)[0] + start))
+        return [(coef, basis, cos, sin, 0, (n_extra, w.key_exact.shape[2]), 1.0)], "codec coefficients of the kept tokens"
+    coef_all = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
+    cu = w.context.cu_host.numpy()
+    e_off = np.concatenate([[0], np.cumsum(w.exact_lengths)])
+    lengths = np.diff(cu)
+    picks = [0] if w.batch == 1 else sorted({int(np.argmin(lengths)), int(np.argsort(lengths)[w.batch // 2]),
+                                              int(np.argmax(lengths))})
+    convs = []
+    for b in picks:
+        t0, t1 = int(cu[b]), int(cu[b + 1])
+        cos, sin = rope_rows(w.context.positions[t0:t1].long().cpu())
+        convs.append(({k: v[t0:t1] for k, v in coef_all.items()}, w.synthetic_basis_host, cos, sin, b,
+                      (int(e_off[b]), int(e_off[b + 1])), (t1 - t0) / max(int(cu[-1]), 1)))
+    what = "K1-decoded coefficients" if w.batch == 1 else \
+        f"K1-decoded coefficients of conversations {picks} ({sum(c[-1] for c in convs):.3f} of the batch's tokens)"
+    return convs, what
+
+
 def cpu_baseline(w, seconds: float):
     """Oracle (numpy fp32) attention of the same workload on every host core this process may use:
     one warm-up layer, then three passes over the layers (all of them when a pass fits a third of
     ``seconds``, else the first k), each pass's mean per-layer time scaled to a step; the reported
-    rate is the median of the three passes."""
+    rate is the median of the three passes.  A ragged batch times three of its conversations per
+    layer and scales their time by the inverse of their share of the batch's compressed tokens."""
     import numpy as np
-    import torch
     from threadpoolctl import threadpool_limits
 
     from oracle import attention_ref
 
     s = w.shape
     cores, core_note = host_cores()
-    coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
-    kb = w.synthetic_basis_host
-    positions = w.context.positions.long().cpu()
-    cos = w.tables.rope_cos.cpu()[positions].numpy()
-    sin = w.tables.rope_sin.cpu()[positions].numpy()
-    cos, sin = np.concatenate([cos, cos], -1), np.concatenate([sin, sin], -1)
+    convs, what = _oracle_conversations(w)
+    share = sum(c[-1] for c in convs)
     wdt = s.kv_heads * s.head_dim
     inputs = {}
 
-    def layer_inputs(layer):
-        if layer not in inputs:
-            inputs[layer] = (w.queries[layer].float().cpu().numpy(), kb["key"][layer * wdt:(layer + 1) * wdt].T,
-                             kb["value"][layer * wdt:(layer + 1) * wdt].T, w.tables.mean_k[layer].cpu().numpy(),
-                             w.tables.mean_v[layer].cpu().numpy(), w.key_exact[layer][None].cpu().numpy(),
-                             w.value_exact[layer][None].cpu().numpy())
-        return inputs[layer]
+    def layer_inputs(layer, conv):
+        key = (layer, conv[4])
+        if key not in inputs:
+            basis, b, (e0, e1) = conv[1], conv[4], conv[5]
+            inputs[key] = (w.queries[layer][b:b + 1].float().cpu().numpy(),
+                           basis["key"][layer * wdt:(layer + 1) * wdt].T, basis["value"][layer * wdt:(layer + 1) * wdt].T,
+                           w.tables.mean_k[layer].cpu().numpy(), w.tables.mean_v[layer].cpu().numpy(),
+                           w.key_exact[layer][None, :, e0:e1].cpu().numpy(),
+                           w.value_exact[layer][None, :, e0:e1].cpu().numpy())
+        return inputs[key]
 
     def run(layer):
-        q, bk, bv, mk, mv, ke, ve = layer_inputs(layer)
-        t0 = time.perf_counter()
-        attention_ref.attend(q, coef["key"], coef["value"], bk, bv, mk, mv, cos, sin, ke, ve)
-        return time.perf_counter() - t0
+        total = 0.0
+        for conv in convs:
+            q, bk, bv, mk, mv, ke, ve = layer_inputs(layer, conv)
+            coef, cos, sin = conv[0], conv[2], conv[3]
+            t0 = time.perf_counter()
+            attention_ref.attend(q, coef["key"], coef["value"], bk, bv, mk, mv, cos, sin, ke, ve)
+            total += time.perf_counter() - t0
+        return total / share  # the whole batch's layer
 
     with threadpool_limits(limits=cores):
         warm = run(0)
-        per_pass = max(1, min(s.layers, int(seconds / 3 / max(warm, 1e-6))))
+        per_pass = max(1, min(s.layers, int(seconds / 3 / max(warm * share, 1e-6))))
         passes = [float(np.mean([run(layer) for layer in range(per_pass)])) for _ in range(3)]
     per_layer = float(np.median(passes))
-    return {"value": 1.0 / (per_layer * s.layers), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"numpy fp32 oracle (oracle/attention_ref.attend over K1-decoded coefficients) of the same "
+    return {"value": w.batch / (per_layer * s.layers), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"numpy fp32 oracle (oracle/attention_ref.attend over {what}) of the same "
                       f"workload on {cores} host cores ({core_note}): one warm-up layer, then 3 passes over {per_pass} of "
                       f"{s.layers} layers; median pass {per_layer * 1e3:.0f} ms/layer (passes "
                       f"{', '.join(f'{p * 1e3:.0f}' for p in passes)} ms), scaled x{s.layers}"}
@@ -193,21 +241,22 @@ def cpu_baseline(w, seconds: float):
 
 def held_memory(w) -> dict:
     """GPU memory held for the conversation(s) of a workload, in MiB: the context's parts
-    (CompressedContext.held_bytes: packed codes as allocated, the decode workspace), the exact
+    (CompressedContext.held_bytes: packed codes as allocated, the decode workspace) and the exact
     cache the workload keeps beside it (float32 keys and values of the sinks, recent window and new
-    token, all layers), and the question stage's scoring workspace and importance vector.  The bases
-    (per model) are listed apart.  ``code_bytes`` is the reference's accounting of the packed content
+    token, all layers); apart from them, the extra working memory of a question (the scoring
+    workspace and the importance vector, released after it) and the bases (per model).  ``code_bytes`` is the reference's accounting of the packed content
     (scripts/compressed_attention.py:91-94)."""
     ctx = w.context
     parts = ctx.held_bytes()
     parts.pop("total")
     if ctx.exact_cache is None:
         parts["exact_cache"] = sum(t.numel() * t.element_size() for t in (w.key_exact, w.value_exact))
-    q = getattr(w, "question", None)
-    if q is not None:
-        parts["score_workspace"] = q.workspace.numel() + q.importance.numel() * 4 + q.idx.numel() * 4
+    parts.pop("score_workspace")
     mib = {k: round(v / 2**20, 2) for k, v in parts.items()}
     mib["held_total"] = round(sum(parts.values()) / 2**20, 2)
+    q = getattr(w, "question", None)
+    if q is not None:  # working memory while a question is scored (released after it)
+        mib["question_extra"] = round((q.workspace.numel() + q.importance.numel() * 4 + q.idx.numel() * 4) / 2**20, 2)
     mib["code_bytes_reference_accounting"] = round(ctx.code_bytes() / 2**20, 2)
     mib["bases_per_model"] = round(ctx.basis_bytes() / 2**20, 2)
     mib["unit"] = "MiB"
@@ -364,14 +413,16 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
     """Greedy decoding through a Hugging Face Llama model, the way the reference times its direct
     path (scripts/compressed_attention.py:140-169 ``greedy_answer``; scripts/test_compressed_attention.py):
     a Llama-3.2-1B-shaped model (16 layers, 32 query / 8 KV heads x 64, MLP 8192, vocabulary 128,256)
-    with random bf16 weights from a local config (nothing is downloaded), an ``tokens``-token context
+    with random fp16 weights from a local config (nothing is downloaded), an ``tokens``-token context
     prefilled through the dimmer hook with score capture (dimmer.prefill_with_scores), compressed by
     ``Methods.apply`` at 2 % (``dkvtc@0.02:snap:floor1``, or ``prog@0.02:r0.01``, whose question is
     first scored over the codes and the top 1 % refined), then a question of ``question`` random
     tokens answered with ``new_tokens`` greedy tokens: directly over the codes (CompressedContext
     through the hook) and over the rebuilt cache (the hook's eager attention).  The bases are random
     orthonormal rank-1,024 bases with the prefill's mean (a calibration stand-in), so the
-    replies are not meaningful text; the two paths' replies are compared as the reference does.
+    replies are not meaningful text.  The two paths are compared as the reference does: their
+    first-step logits, and how many reply tokens agree (random weights leave the logits of a
+    128,256-token vocabulary close together, so replies can part after a few tokens).
 
     Decode tok/s = new_tokens / (time of a 1 + new_tokens reply - time of the question step alone),
     each the median of 3 after a warm-up, with the host waiting for every token's argmax as
@@ -404,7 +455,7 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
     config.intermediate_size, config.vocab_size, config.tie_word_embeddings = 8192, 128256, True
     torch.manual_seed(seed)
     with torch.device(dev):  # initialise the weights on the GPU
-        model = LlamaForCausalLM(config).to(dtype=torch.bfloat16).eval()
+        model = LlamaForCausalLM(config).to(dtype=torch.float16).eval()
     dimmer.install(model)
     g = torch.Generator("cpu").manual_seed(seed + 1)
     ids = torch.randint(0, config.vocab_size, (1, tokens), generator=g).to(dev)
@@ -456,10 +507,10 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
         torch.cuda.synchronize()
         t = time.perf_counter()
         with torch.no_grad():
-            text, _ = greedy_answer(model, tok, context if direct else None, cache, tail, tokens,
-                                    max_new_tokens=n, stop_at_eos=False)
+            text, logits = greedy_answer(model, tok, context if direct else None, cache, tail, tokens,
+                                         max_new_tokens=n, stop_at_eos=False)
         torch.cuda.synchronize()
-        return time.perf_counter() - t, text
+        return time.perf_counter() - t, text, logits
 
     out = {}
     for direct in (True, False):
@@ -467,8 +518,8 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
         first = statistics.median(reply(direct, 1)[0] for _ in range(3))
         runs = [reply(direct, 1 + new_tokens) for _ in range(3)]
         whole = statistics.median(r[0] for r in runs)
-        out[direct] = {"tok_s": new_tokens / (whole - first), "question_ms": first * 1e3, "reply": runs[0][1],
-                       "ms_per_token": (whole - first) / new_tokens * 1e3}
+        out[direct] = {"tok_s": new_tokens / (whole - first), "question_ms": first * 1e3, "reply": runs[0][1].split(),
+                       "logits": runs[0][2], "ms_per_token": (whole - first) / new_tokens * 1e3}
     # instrumented reply: the attention hook's host and device time per decode token
     plain = context.attend
     calls = []
@@ -496,10 +547,15 @@ def model_bench(method: str, new_tokens: int = 32, tokens: int = 8192, question:
     result = {
         "metric": f"greedy decode tok/s through HF Llama (1B shape, {tokens}-token context, {name})",
         "value": round(direct["tok_s"], 2), "unit": "tok/s", "higher_is_better": True, "data": "synthetic",
-        "model": "Llama-3.2-1B shape, random bf16 weights (local config)",
+        "model": "Llama-3.2-1B shape, random fp16 weights (local config)",
         "method": name, "context_tokens": tokens, "question_tokens": question, "new_tokens": new_tokens,
         "rebuilt_tok_s": round(out[False]["tok_s"], 2),
-        "same_reply_as_rebuilt": direct["reply"] == out[False]["reply"],
+        "vs_rebuilt": {
+            "first_step_logit_max_diff": round(float((direct["logits"] - out[False]["logits"]).abs().max()), 5),
+            "logit_scale": round(float(out[False]["logits"].abs().max()), 3),
+            "reply_tokens_agreeing": next((i for i, (a, b) in enumerate(zip(direct["reply"], out[False]["reply"]))
+                                           if a != b), new_tokens),
+            "reply_tokens": new_tokens},
         "question_ms": {"direct": round(direct["question_ms"], 2), "rebuilt": round(out[False]["question_ms"], 2)},
         "per_token_ms": {"wall": round(direct["ms_per_token"], 3), "attention_host": round(host_ms, 3),
                          "attention_device": round(device_ms, 3),
@@ -600,9 +656,8 @@ def main():
             print("--method dkvtc runs at 1b-8k-2pct or 3b-16k-3pct", file=sys.stderr)
             sys.exit(2)
         w = workloads.build_dkvtc(args.workload, device=dev)
-        args.no_cpu_baseline = True
     elif args.workload == "3b-ragged-32":
-        w = workloads.build_ragged(device=dev)
+        w = workloads.build_ragged(device=dev, keep_host_basis=not args.no_cpu_baseline)
     else:
         w = workloads.build_decode(args.workload, device=dev, keep_host_basis=not args.no_cpu_baseline,
                                    refine_fraction=0.01 if args.workload == "3b-16k-3pct" and not args.no_question else 0.0,
@@ -710,7 +765,7 @@ def main():
     if question is not None:
         result["question"] = question
     result["memory"] = held_memory(w)
-    if not args.no_cpu_baseline and args.workload != "3b-ragged-32":
+    if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

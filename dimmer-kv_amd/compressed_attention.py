@@ -256,8 +256,9 @@ class CompressedContext:
         """GPU memory held for this conversation, in parts (bytes): ``codes`` the packed streams as
         allocated (``code_bytes`` is the reference's accounting of their content), ``exact_rung``
         float32 rows of exact-rung tokens, ``exact_cache`` the sinks and recent window kept here,
-        ``decode_workspace`` and ``score_workspace`` (see ``workspace_bytes``), and ``total``.  The
-        bases (``basis_bytes``) are per model and not included."""
+        ``decode_workspace`` and, while a question is scored, ``score_workspace`` (see
+        ``workspace_bytes``), and ``total``.  The bases (``basis_bytes``) are per model and not
+        included."""
         extra = 0
         if self.extra is not None:
             extra = sum(t.numel() * t.element_size() for kind in ("key", "value") for t in self.extra[kind])
@@ -372,7 +373,11 @@ class CompressedContext:
         dkv_hip.score_begin(self.importance)
 
     def end_scoring(self) -> torch.Tensor:
+        """The importance vector; the scoring workspace goes back to the allocator, so a context holds
+        it only while a question is scored."""
         importance, self.importance = self.importance, None
+        self._score_workspace = None
+        self._score_prepared = None
         return importance
 
     def _score(self, layer: int, query: torch.Tensor, key: torch.Tensor, scaling) -> None:

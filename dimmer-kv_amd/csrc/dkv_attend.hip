@@ -1827,7 +1827,9 @@ inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
 // Workspace: [decoded key coefficients][decoded value codes][value affine][probabilities][tile statistics]
 // [split partials][chunk partials][exact-tail results][K2 rank-slice partial scores].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
-Layout make_layout(const dkv_attend_args_t* a) {
+// `values` false: no value-decode areas (question scoring decodes and reads the keys alone), so
+// every later area starts right after the key operands.
+Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   Layout L{};
   L.ntiles = 0;
   L.nsplits = 0;
@@ -1844,9 +1846,9 @@ Layout make_layout(const dkv_attend_args_t* a) {
   L.coef = off;
   off += align256((size_t)L.n_slots * a->rank * 2);
   L.vcodes = off;
-  off += align256((size_t)L.n_slots * a->rank);
+  if (values) off += align256((size_t)L.n_slots * a->rank);
   L.vaff = off;
-  off += align256((size_t)L.n_slots * (a->rank / 64) * 8);
+  if (values) off += align256((size_t)L.n_slots * (a->rank / 64) * 8);
   L.probs = off;
   off += align256((size_t)L.R_total * L.n_slots * 2);
   L.tile_max = off;
@@ -1996,9 +1998,9 @@ extern "C" int dkv_attend_prepare(const dkv_attend_args_t* a, int32_t plane_cap,
               plane_cap);
   DKV_REQUIRE(a->key.format == DKV_FMT_PLANES || plane_cap == 8, DKV_EINVAL,
               "dkv_attend_prepare: a plane cap needs a bit-plane key stream (ladder streams have no planes)");
-  const Layout L = make_layout(a);
-  // only the decoded areas at the head of the workspace are written, so an attend or a score
-  // workspace (both start with them) will do
+  // only the decoded areas at the head of the workspace are written (the value codes only with a
+  // value stream), so an attend workspace, or a score workspace for the keys alone, will do
+  const Layout L = make_layout(a, a->value.blob != nullptr);
   DKV_REQUIRE(workspace && workspace_bytes >= L.probs, DKV_EWORKSPACE,
               "dkv_attend_prepare: workspace %zu B < required %zu B", workspace_bytes, L.probs);
   DecodeArgs d{};
@@ -2465,11 +2467,12 @@ struct ScoreLayout {
   size_t probs2, sub_max[2], sub_sum, stat[2], total;
 };
 
-// The attend layout up to the tile statistics (decoded keys, probabilities), then the second
-// probability buffer, the per-quarter statistics and the per-row statistics.
+// The attend layout without the value areas up to the tile statistics (decoded keys,
+// probabilities), then the second probability buffer, the per-quarter statistics and the per-row
+// statistics.
 ScoreLayout make_score_layout(const dkv_attend_args_t* a) {
   ScoreLayout S{};
-  S.base = make_layout(a);
+  S.base = make_layout(a, /*values=*/false);
   const size_t per_quarter = align256((size_t)((S.base.R_total + 7) / 8 * 8) * S.base.ntiles * 4 * 4);
   const size_t per_stat = align256((size_t)S.base.R_total * 2 * 4);
   size_t off = S.base.w_part;

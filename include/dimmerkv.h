@@ -255,7 +255,8 @@ size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);
  * into the workspace in the MFMA operand layout, and, when a->value.blob is
  * non-null, every token's value codes (all hot planes) with their affine
  * pairs for K3; a null value blob decodes the keys alone (question scoring
- * reads no values).  The decoded codes depend on the streams only: call it
+ * reads no values, and a score workspace has no room for them).  The decoded
+ * codes depend on the streams only: call it
  * once before the layers of a decode step (and again after a stream
  * changes, e.g. dkv_gather_cold); every later dkv_attend_layer /
  * dkv_attend_scores / dkv_score_layer on the same workspace reads it.  Each
