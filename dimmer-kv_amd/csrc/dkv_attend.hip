@@ -44,8 +44,29 @@ namespace {
 constexpr int kTileTok = 256;    // tokens per K2 workgroup
 constexpr int kK2Threads = 512;  // 8 waves: 4 token quarters x 2 row halves
 constexpr int kStride = 72;      // LDS row stride in halves for [row][64] tiles (64 + 8 pad)
-constexpr int kSplitTok = 1024;  // tokens per K3a split
+constexpr int kSplitTok = 1024;  // tokens per K3a split (512 when 1024-token splits leave CUs idle)
 constexpr int kChunk = 128;      // components per K3b workgroup
+
+constexpr int kMaxExact = 1024;
+constexpr int kRowThreads = 256;  // threads of a row workgroup (the exact tail in K3b, the merge in K3c)
+
+struct RowMergeArgs {
+  const int32_t* cu_seqlens;
+  const int32_t* cu_exact;
+  const float* tile_max;
+  const float* tile_sum;
+  const float* mean_v;
+  const float* key_exact;
+  const float* value_exact;
+  const float* mask;
+  const void* query;
+  const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
+  float* ex;              // [batch * R_total][D + 2] per row: Me, Le, then ve[D] (the exact tail, row_exact)
+  void* out;              // [batch][q_len][Hq][D], out_dtype
+  float scaling;
+  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
+  int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
+};
 
 struct K2Args {
   const uint16_t* coef;  // decoded key coefficients, MFMA fragment order over slots
@@ -1119,27 +1140,6 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 // recent window, new tokens; computed beside K3b, row_exact) in one softmax
 // and writes the row's output.
 // ---------------------------------------------------------------------------
-constexpr int kMaxExact = 1024;
-constexpr int kRowThreads = 256;  // threads of a row workgroup (the exact tail in K3b, the merge in K3c)
-
-struct RowMergeArgs {
-  const int32_t* cu_seqlens;
-  const int32_t* cu_exact;
-  const float* tile_max;
-  const float* tile_sum;
-  const float* mean_v;
-  const float* key_exact;
-  const float* value_exact;
-  const float* mask;
-  const void* query;
-  const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
-  float* ex;              // [batch * R_total][D + 2] per row: Me, Le, then ve[D] (the exact tail, K3b)
-  void* out;              // [batch][q_len][Hq][D], out_dtype
-  float scaling;
-  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
-  int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
-};
-
 constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
 
 constexpr int kChunkLoads = 8;  // chunk partials per thread issued in the first round
@@ -1365,6 +1365,8 @@ struct K3aArgs {
   int total_wg, per_xcd;  // workgroups, and consecutive workgroup indices per XCD
 };
 
+constexpr int kK3WaveTok = 128;  // tokens per K3a wave
+
 // ---------------------------------------------------------------------------
 // K1 for the value side: every token's value codes (all hot planes) as 8-bit
 // codes, transposed to [G][n_slots/16][64][16] so that an MFMA operand (one
@@ -1535,14 +1537,15 @@ __global__ __launch_bounds__(kTileTok) void split_merge_kernel(K2MergeArgs a) {
 // (exact in fp16), the second a per-row scalar.  Wave w of the 8 takes tokens
 // w*128 .. +128 of the split in 16-token steps; the waves' sums meet in LDS.
 // ---------------------------------------------------------------------------
-constexpr int kK3Waves = 8;
-constexpr int kK3WaveTok = kSplitTok / kK3Waves;  // 128
-
-__global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a) {
-  __shared__ float red[kK3Waves][32][65];
-  __shared__ float ored[kK3Waves][32];
+// WAVES waves of 128 tokens: a split of 1024 tokens (8 waves) or, when 1024-token splits would leave
+// CUs idle (small contexts), 512 (4 waves: twice the workgroups, each with half the loads).
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
+  constexpr int SPLIT = WAVES * kK3WaveTok;
+  __shared__ float red[WAVES][32][65];
+  __shared__ float ored[WAVES][32];
   __shared__ float Mrow[32];
-  __shared__ __attribute__((aligned(16))) float2 saff[kK3Waves][kK3WaveTok];  // (scale, offset) of each wave's tokens
+  __shared__ __attribute__((aligned(16))) float2 saff[WAVES][kK3WaveTok];  // (scale, offset) of each wave's tokens
 
   // consecutive workgroup indices on one XCD: the group workgroups of a split share its
   // probability rows, which that XCD's L2 then fetches once
@@ -1551,16 +1554,16 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   const int rbk = bid % a.row_blocks;
   const int g = (bid / a.row_blocks) % a.G;
   const int sp = bid / (a.row_blocks * a.G);
-  const int2 bs = find_tile(a.cu_seqlens, a.batch, a.n_total, kSplitTok, sp);
+  const int2 bs = find_tile(a.cu_seqlens, a.batch, a.n_total, SPLIT, sp);
   const int b = bs.x;
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
-  const int tok0 = sr.x + bs.y * kSplitTok;
-  const int count = min(kSplitTok, sr.y - tok0);
+  const int tok0 = sr.x + bs.y * SPLIT;
+  const int count = min(SPLIT, sr.y - tok0);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
   const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
-  const long slot0 = (long)(tb0 + bs.y * (kSplitTok / kTileTok)) * kTileTok;  // first slot of the split
+  const long slot0 = (long)(tb0 + bs.y * (SPLIT / kTileTok)) * kTileTok;  // first slot of the split
   const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
   const int my_row = rbk * 32 + l32;
   const bool row_ok = my_row < a.R_total;
@@ -1572,12 +1575,13 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
   // value codes for all 8 steps.
   const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
   const int mrow = rbk * 32 + ((tid >> 3) & 31), msub = tid & 7;  // 8 lanes per row (waves 4-7 repeat 0-3)
+  static_assert(WAVES >= 4, "the row maxima take 256 threads");
   const float* tmrow = a.tile_max + (long)min(mrow, a.R_total - 1) * a.ntiles + tb0;
   float tmv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) tmv[i] = tmrow[min(msub + 8 * i, ntb - 1)];
   // this wave's 128 tokens lie in one tile; its maximum for this lane's row
-  const int tile = tb0 + bs.y * (kSplitTok / kTileTok) + wt0 / kTileTok;
+  const int tile = tb0 + bs.y * (SPLIT / kTileTok) + wt0 / kTileTok;
   const float mt_raw = a.tile_max[(long)min(my_row, a.R_total - 1) * a.ntiles + tile];
   const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
   const float4 aff2 = *(const float4*)(aff + wt0 + 2 * lane);
@@ -1658,12 +1662,12 @@ __global__ __launch_bounds__(kK3Waves * 64) void value_weights_kernel(K3aArgs a)
     for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v] * sdown;
   if (lhi == 0) ored[wave][l32] = osum;
   __syncthreads();
-  for (int e = tid; e < 32 * 64; e += kK3Waves * 64) {
+  for (int e = tid; e < 32 * 64; e += WAVES * 64) {
     const int r = e >> 6, k = e & 63;
     const int row = rbk * 32 + r;
     float s = 0.0f, o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kK3Waves; ++w) {
+    for (int w = 0; w < WAVES; ++w) {
       s += red[w][r][k];
       o += ored[w][r];
     }
@@ -1685,6 +1689,7 @@ struct K3bArgs {
   const uint16_t* value_basis;
   float* out_part;
   int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
+  int split_tok;   // tokens per K3a split
   int n_exact_wg;  // leading workgroups that compute the exact tail of one output row each (row_exact)
 };
 
@@ -1711,9 +1716,9 @@ void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
   const int b = bid / (nds * a.nchunks * a.Hkv);
   const int tid = threadIdx.x;
   const int RH = (a.Hq / a.Hkv) * a.q_len;
-  const int sp0 = tiles_before(a.cu_seqlens, b, kSplitTok);
+  const int sp0 = tiles_before(a.cu_seqlens, b, a.split_tok);
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
-  const int nsp = (sr.y - sr.x + kSplitTok - 1) / kSplitTok;
+  const int nsp = (sr.y - sr.x + a.split_tok - 1) / a.split_tok;
   const int D = a.D;
   const int npair = D / 2;
   const int dp = tid & 31, part = tid >> 5;
@@ -1803,7 +1808,7 @@ __global__ __launch_bounds__(kRowThreads) void finish_kernel(RowMergeArgs a) {
 // Workspace layout and argument checks.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int ntiles, nsplits, R_total, nchunks, n_total, n_slots;
+  int ntiles, nsplits, split_tok, R_total, nchunks, n_total, n_slots;
   int ksplit;
   size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, exact, split_scores,
       total;
@@ -1832,15 +1837,22 @@ inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
 Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   Layout L{};
   L.ntiles = 0;
-  L.nsplits = 0;
-  for (int b = 0; b < a->batch; ++b) {
-    const int len = a->cu_seqlens_host[b + 1] - a->cu_seqlens_host[b];
-    L.ntiles += (len + kTileTok - 1) / kTileTok;
-    L.nsplits += (len + kSplitTok - 1) / kSplitTok;
+  L.R_total = a->q_heads * a->q_len;
+  // K3a splits of 1024 tokens, or of 512 when 1024 would give fewer workgroups than CUs
+  auto count_splits = [&](int tok) {
+    int n = 0;
+    for (int b = 0; b < a->batch; ++b) n += (a->cu_seqlens_host[b + 1] - a->cu_seqlens_host[b] + tok - 1) / tok;
+    return n;
+  };
+  for (int b = 0; b < a->batch; ++b) L.ntiles += (a->cu_seqlens_host[b + 1] - a->cu_seqlens_host[b] + kTileTok - 1) / kTileTok;
+  L.split_tok = kSplitTok;
+  L.nsplits = count_splits(kSplitTok);
+  if ((long)L.nsplits * (a->rank / 64) * ((L.R_total + 31) / 32) < kCUs) {
+    L.split_tok = kSplitTok / 2;
+    L.nsplits = count_splits(L.split_tok);
   }
   L.n_total = a->cu_seqlens_host[a->batch];
   L.n_slots = L.ntiles * kTileTok + kSplitTok;
-  L.R_total = a->q_heads * a->q_len;
   L.nchunks = a->rank / kChunk;
   size_t off = 0;
   L.coef = off;
@@ -1891,6 +1903,58 @@ int check_attend(const dkv_attend_args_t* a, const char* what) {
   DKV_REQUIRE(a->cu_seqlens_host[0] == 0, DKV_ESHAPE, "%s: cu_seqlens[0] must be 0", what);
   for (int b = 0; b < a->batch; ++b)
     DKV_REQUIRE(a->cu_seqlens_host[b + 1] >= a->cu_seqlens_host[b], DKV_ESHAPE, "%s: cu_seqlens not monotone", what);
+  return DKV_OK;
+}
+
+// The arguments of the exact tail (row_exact, extra K3b workgroups) and the merge (K3c): one
+// workgroup per (sequence, output row).
+RowMergeArgs row_merge_args(const dkv_attend_args_t* a, const Layout& L, char* ws, int E_total) {
+  RowMergeArgs m{};
+  m.cu_seqlens = a->cu_seqlens;
+  m.cu_exact = a->cu_exact;
+  m.tile_max = (const float*)(ws + L.tile_max);
+  m.tile_sum = (const float*)(ws + L.tile_sum);
+  m.ntiles = L.ntiles;
+  m.mean_v = a->mean_v;
+  m.key_exact = a->key_exact;
+  m.value_exact = a->value_exact;
+  m.mask = a->mask;
+  m.query = a->query;
+  m.out_part = (const float*)(ws + L.out_part);
+  m.ex = (float*)(ws + L.exact);
+  m.out = a->out;
+  m.out_dtype = a->out_dtype;
+  m.nchunks = L.nchunks;
+  m.scaling = a->scaling;
+  m.batch = a->batch;
+  m.n_total = L.n_total;
+  m.e0_single = 0;  // cu_exact[0] == 0 (check_exact)
+  m.e_single = a->cu_exact ? a->cu_exact_host[1] - a->cu_exact_host[0] : 0;
+  m.layer = a->layer;
+  m.Hkv = a->kv_heads;
+  m.Hq = a->q_heads;
+  m.q_len = a->q_len;
+  m.D = a->head_dim;
+  m.R_total = L.R_total;
+  m.E_total = E_total;
+  m.query_dtype = a->query_dtype;
+  return m;
+}
+
+// The exact tokens of a decode: offsets, pointers and the per-sequence limit; E_total gets their total.
+int check_exact(const dkv_attend_args_t* a, int& E_total, const char* what) {
+  DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "%s: mask is only supported for batch == 1", what);
+  DKV_REQUIRE(!a->cu_exact || (a->key_exact && a->value_exact), DKV_EINVAL, "%s: exact keys/values missing", what);
+  E_total = 0;
+  if (a->cu_exact) {
+    DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "%s: cu_exact needs cu_exact_host", what);
+    DKV_REQUIRE(a->cu_exact_host[0] == 0, DKV_ESHAPE, "%s: cu_exact[0] must be 0", what);
+    for (int b = 0; b < a->batch; ++b) {
+      const int e = a->cu_exact_host[b + 1] - a->cu_exact_host[b];
+      DKV_REQUIRE(e >= 0 && e <= kMaxExact, DKV_ESHAPE, "%s: %d exact tokens (max %d)", what, e, kMaxExact);
+    }
+    E_total = a->cu_exact_host[a->batch];
+  }
   return DKV_OK;
 }
 
@@ -2045,20 +2109,7 @@ static int check_values(const dkv_attend_args_t* a, int& E_total) {
               "dkv_attend_values: K/V group mismatch");
   DKV_REQUIRE(a->value_basis && a->mean_v && a->out, DKV_EINVAL, "dkv_attend_values: null value/out pointer");
   DKV_REQUIRE(a->out_dtype >= DKV_F32 && a->out_dtype <= DKV_BF16, DKV_EINVAL, "dkv_attend_values: bad out dtype");
-  DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "dkv_attend_values: mask is only supported for batch == 1");
-  DKV_REQUIRE(!a->cu_exact || (a->key_exact && a->value_exact), DKV_EINVAL,
-              "dkv_attend_values: exact keys/values missing");
-  E_total = 0;
-  if (a->cu_exact) {
-    DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "dkv_attend_values: cu_exact needs cu_exact_host");
-    DKV_REQUIRE(a->cu_exact_host[0] == 0, DKV_ESHAPE, "dkv_attend_values: cu_exact[0] must be 0");
-    for (int b = 0; b < a->batch; ++b) {
-      const int e = a->cu_exact_host[b + 1] - a->cu_exact_host[b];
-      DKV_REQUIRE(e >= 0 && e <= kMaxExact, DKV_ESHAPE, "dkv_attend_values: %d exact tokens (max %d)", e, kMaxExact);
-    }
-    E_total = a->cu_exact_host[a->batch];
-  }
-  return DKV_OK;
+  return check_exact(a, E_total, "dkv_attend_values");
 }
 
 extern "C" int dkv_attend_scores(const dkv_attend_args_t* a, void* workspace, size_t workspace_bytes, void* stream) {
@@ -2101,41 +2152,17 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.row_blocks = (L.R_total + 31) / 32;
     k.total_wg = L.nsplits * k.row_blocks * G;
     k.per_xcd = (k.total_wg + 7) / 8;
-    hipLaunchKernelGGL(value_weights_kernel, dim3(8u * (unsigned)k.per_xcd), dim3(kK3Waves * 64), 0, st, k);
+    if (L.split_tok == kSplitTok)
+      hipLaunchKernelGGL(value_weights_kernel<kSplitTok / kK3WaveTok>, dim3(8u * (unsigned)k.per_xcd),
+                         dim3(kSplitTok / kK3WaveTok * 64), 0, st, k);
+    else
+      hipLaunchKernelGGL(value_weights_kernel<kSplitTok / 2 / kK3WaveTok>, dim3(8u * (unsigned)k.per_xcd),
+                         dim3(kSplitTok / 2 / kK3WaveTok * 64), 0, st, k);
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
   }
-  // row arguments: the exact tail (extra K3b workgroups) and the merge (K3c), one workgroup per
-  // (sequence, output row)
-  RowMergeArgs m{};
-  m.cu_seqlens = a->cu_seqlens;
-  m.cu_exact = a->cu_exact;
-  m.tile_max = (const float*)(ws + L.tile_max);
-  m.tile_sum = (const float*)(ws + L.tile_sum);
-  m.ntiles = L.ntiles;
-  m.mean_v = a->mean_v;
-  m.key_exact = a->key_exact;
-  m.value_exact = a->value_exact;
-  m.mask = a->mask;
-  m.query = a->query;
-  m.out_part = (const float*)(ws + L.out_part);
-  m.ex = (float*)(ws + L.exact);
-  m.out = a->out;
-  m.out_dtype = a->out_dtype;
-  m.nchunks = L.nchunks;
-  m.scaling = a->scaling;
-  m.batch = a->batch;
-  m.n_total = L.n_total;
-  m.e0_single = 0;  // cu_exact[0] == 0 (check_values)
-  m.e_single = a->cu_exact ? a->cu_exact_host[1] - a->cu_exact_host[0] : 0;
-  m.layer = a->layer;
-  m.Hkv = a->kv_heads;
-  m.Hq = a->q_heads;
-  m.q_len = a->q_len;
-  m.D = a->head_dim;
-  m.R_total = L.R_total;
-  m.E_total = E_total;
-  m.query_dtype = a->query_dtype;
+  // the exact tail (extra K3b workgroups) and the merge (K3c), one workgroup per (sequence, output row)
+  const RowMergeArgs m = row_merge_args(a, L, ws, E_total);
   K3bArgs kb{};
   kb.cu_seqlens = a->cu_seqlens;
   kb.w_part = (const float*)(ws + L.w_part);
@@ -2151,6 +2178,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.rank = a->rank;
   kb.R_total = L.R_total;
   kb.nchunks = L.nchunks;
+  kb.split_tok = L.split_tok;
   kb.n_exact_wg = a->batch * L.R_total;
   const long k3b_blocks = kb.n_exact_wg + (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
   if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
