@@ -35,6 +35,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "dkv_device.h"
 #include "dkv_host.h"
@@ -1545,7 +1546,11 @@ __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
   __shared__ float red[WAVES][32][65];
   __shared__ float ored[WAVES][32];
   __shared__ float Mrow[32];
-  __shared__ __attribute__((aligned(16))) float2 saff[WAVES][kK3WaveTok];  // (scale, offset) of each wave's tokens
+  // each wave's tokens: scale * 2^e as fp16 and the offset as fp32 (both 0 past the split's tokens),
+  // and the wave's factor f = exp(tile max - row max) of each of the block's rows
+  __shared__ __attribute__((aligned(16))) half_t sw[WAVES][kK3WaveTok];
+  __shared__ __attribute__((aligned(16))) float sofs[WAVES][kK3WaveTok];
+  __shared__ __attribute__((aligned(16))) float sf[WAVES][32];
 
   // consecutive workgroup indices on one XCD: the group workgroups of a split share its
   // probability rows, which that XCD's L2 then fetches once
@@ -1615,7 +1620,13 @@ __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
     sexp = min(max(15 - ex, -126), 126);
   }
   const float sup = ldexpf(1.0f, sexp), sdown = ldexpf(1.0f, -sexp);
-  *(float4*)&saff[wave][2 * lane] = make_float4(aff2.x * sup, aff2.y, aff2.z * sup, aff2.w);
+  {
+    const bool ok0 = ta < count, ok1 = ta + 1 < count;
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    const half2_t w2 = {ok0 ? (half_t)(aff2.x * sup) : (half_t)0.0f, ok1 ? (half_t)(aff2.z * sup) : (half_t)0.0f};
+    *(half2_t*)&sw[wave][2 * lane] = w2;
+    *(float2*)&sofs[wave][2 * lane] = make_float2(ok0 ? aff2.y : 0.0f, ok1 ? aff2.w : 0.0f);
+  }
   {
     float m = -INFINITY;
 #pragma unroll
@@ -1635,31 +1646,57 @@ __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
   float osum = 0.0f;
 
   // K2 left p~ = exp(s - tile max) in fp16; the tile's factor f = exp(tile max - row max) turns
-  // p~ into p = exp(s - row max).
+  // p~ into p = exp(s - row max).  The wave's tokens lie in one tile, so f is constant over them
+  // and multiplies the wave's sums once, after the MFMAs: the A operand is p~ * (scale * 2^e), one
+  // packed fp16 product per token pair.
   const float f = (mt == -INFINITY) ? 0.0f : __expf(mt - my_M);
+  if (lhi == 0) sf[wave][l32] = f;
   // every load above stayed inside the slot buffers (they extend a whole split past the last
-  // tile); slots past the split's tokens get p = 0 by selection, whatever they hold
+  // tile); slots past the split's tokens get p = 0 by selection, whatever they hold.  Only the
+  // wave holding a split's last token has such slots among its own; it runs a masked copy of the
+  // steps, and a wave entirely past them runs none.
+  auto steps = [&](auto masked) {
 #pragma unroll
-  for (int st = 0; st < STEPS; ++st) {
-    const int t8 = wt0 + st * 16 + lhi * 8;  // this lane's 8 tokens: t8 .. t8+7 (split-relative)
-    half8 pa;
+    for (int st = 0; st < STEPS; ++st) {
+      __builtin_amdgcn_sched_barrier(0);  // one step's LDS reads at a time
+      const half8 wv = *(const half8*)&sw[wave][st * 16 + lhi * 8];
+      const float4 o0 = *(const float4*)&sofs[wave][st * 16 + lhi * 8];
+      const float4 o1 = *(const float4*)&sofs[wave][st * 16 + lhi * 8 + 4];
+      const float ofs[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+      half8 pv = pt[st];
+      if constexpr (decltype(masked)::value) {
+        const int t8 = wt0 + st * 16 + lhi * 8;  // this lane's 8 tokens: t8 .. t8+7 (split-relative)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bool ok = t8 + e < count;
-      const float2 af = saff[wave][st * 16 + lhi * 8 + e];
-      const float p = (float)pt[st][e] * f;
-      pa[e] = ok ? (half_t)(p * af.x) : (half_t)0.0f;
-      osum += ok ? p * af.y : 0.0f;
+        for (int e = 0; e < 8; ++e) pv[e] = t8 + e < count ? pv[e] : (half_t)0.0f;
+      }
+      const half8 pa = pv * wv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) osum += (float)pv[e] * ofs[e];
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0[st].x, c0[st].y), acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1[st].x, c1[st].y), acc[1], 0, 0, 0);
     }
-    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c0[st].x, c0[st].y), acc[0], 0, 0, 0);
-    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa, codes_to_half8(c1[st].x, c1[st].y), acc[1], 0, 0, 0);
+  };
+  if (wt0 + kK3WaveTok <= count)
+    steps(std::false_type{});
+  else if (wt0 < count)
+    steps(std::true_type{});
+  osum = sum_xor32(osum) * f;
+  // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3); each row's f, and 2^-sexp, which
+  // undoes the operand scaling (the wave wrote sf itself: its LDS accesses run in order)
+  __builtin_amdgcn_wave_barrier();
+  float fr[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 f4 = *(const float4*)&sf[wave][8 * i + 4 * lhi];
+    fr[4 * i] = f4.x * sdown;
+    fr[4 * i + 1] = f4.y * sdown;
+    fr[4 * i + 2] = f4.z * sdown;
+    fr[4 * i + 3] = f4.w * sdown;
   }
-  osum = sum_xor32(osum);
-  // acc[nb][v]: component nb*32 + l32, row 8*(v/4) + 4*lhi + (v&3); 2^-sexp undoes the operand scaling
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v] * sdown;
+    for (int v = 0; v < 16; ++v) red[wave][8 * (v >> 2) + 4 * lhi + (v & 3)][nb * 32 + l32] = acc[nb][v] * fr[v];
   if (lhi == 0) ored[wave][l32] = osum;
   __syncthreads();
   for (int e = tid; e < 32 * 64; e += WAVES * 64) {
