@@ -36,6 +36,7 @@
 
 #include <mutex>
 #include <type_traits>
+#include <utility>
 
 #include "dkv_device.h"
 #include "dkv_host.h"
@@ -1127,6 +1128,281 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// K2, one KV head per workgroup: decoding contexts whose 256-row workgroups
+// (256 / D heads each) would leave CUs idle, but whose (tile, head) pairs fill
+// them.  The workgroup covers the tile's 256 tokens and the head's D basis
+// rows over every 64-component group, so no partial scores are merged
+// afterwards and the tile statistics, probabilities and their layouts are the
+// 256-row kernel's.  Wave w takes the tile's 32-token block w: its coefficient
+// operands come straight from the decoded buffer (four 16-byte loads per lane
+// and group) and the head's basis blocks [D][64] go global -> registers ->
+// LDS (D / 64 16-byte loads per thread and group), with the loads of four
+// groups in flight.  One group per barrier: group g's basis block goes to LDS
+// block g & 1, whose previous readers (group g - 2) finished before the
+// barrier of group g - 1.  Consecutive workgroup ids (one XCD) are the heads
+// of one tile, which read the same coefficients.
+// ---------------------------------------------------------------------------
+
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>), in order
+template <class Fn, int... Is>
+DKV_DEVICE void static_for_seq(Fn&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class Fn>
+DKV_DEVICE void static_for(Fn&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int D>
+__global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) {
+  constexpr int DB = D / 32;        // 32-row blocks of the head
+  constexpr int HALF_BLK = DB / 2;  // RoPE partner offset in blocks
+  constexpr int HALF_D = D / 2;
+  constexpr int BQ = D / 64;        // basis loads per thread and group: [D][64] fp16 = D * 8 x 16 B
+  constexpr int RING = 4;           // groups whose loads are in flight
+  constexpr int NW = kK2Threads / 64;
+  constexpr int BLK = D * kStride;  // halves per LDS basis block
+  static_assert(NW * 32 == kTileTok, "one 32-token block per wave");
+  static_assert(kSmallRows * D <= kK2Threads, "one query element per thread");
+  __shared__ __attribute__((aligned(16))) half_t lds[2 * BLK];  // two basis blocks
+  __shared__ __attribute__((aligned(16))) float stat_m[NW][kSmallRows];
+  __shared__ __attribute__((aligned(16))) float stat_s[NW][kSmallRows];
+  __shared__ __attribute__((aligned(16))) float q_s[kSmallRows * D];  // rows past RH are 0
+
+  const int lin = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (lin >= a.total_wg) return;
+  const int tile = lin / a.Hkv, h = lin % a.Hkv;
+  const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
+  const int b = bt.x;
+  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
+  const int tok0 = sr.x + bt.y * kTileTok;
+  const int count = min(kTileTok, sr.y - tok0);
+  const int G = a.G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int gq = a.Hq / a.Hkv;
+  const int RH = gq * a.q_len;
+  const int n = wave * 32 + l32;  // the lane's token in the tile
+
+  // First round, before the main loop's loads: the lane's position (clamped into the RoPE tables;
+  // past the tile's end, its last token's), one query element per thread and the key mean rows.
+  // Their LDS copies are written once the main loop's first loads are out.
+  const int pos = min(max(a.positions[tok0 + min(n, count - 1)], 0), a.rope_rows - 1);
+  const int qr = tid / D, qd = tid % D;
+  const bool q_ok = qr < RH;
+  const int qrc = min(qr, RH - 1);
+  // the query element as raw bits from two unconditional 16-bit loads (a float's halves, or the same
+  // 16-bit element twice), converted after the main loop's loads are out: loads under a type switch
+  // made the conversion wait for the value before anything else was issued
+  const long qi = (((long)b * a.Hq + h * gq + qrc / a.q_len) * a.q_len + qrc % a.q_len) * D + qd;
+  const bool q32 = a.query_dtype == DKV_F32;
+  const uint16_t* qp = (const uint16_t*)a.query + (q32 ? 2 * qi : qi);
+  const uint32_t qlo_bits = qp[0], qhi_bits = qp[q32 ? 1 : 0];
+  // acc[rb][v]: basis row rb * 32 + 8 (v / 4) + 4 lhi + (v & 3) of the lane's token, from the key mean
+  const float* mean_rows = a.mean_k + ((long)a.layer * a.Hkv + h) * D + 4 * lhi;
+  floatx16 acc[DB];
+#pragma unroll
+  for (int rb = 0; rb < DB; ++rb)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float4 m4 = *(const float4*)(mean_rows + rb * 32 + 8 * v4);
+      acc[rb][4 * v4 + 0] = m4.x;
+      acc[rb][4 * v4 + 1] = m4.y;
+      acc[rb][4 * v4 + 2] = m4.z;
+      acc[rb][4 * v4 + 3] = m4.w;
+    }
+
+  const half8* coef_frag = (const half8*)a.coef + ((long)(tile * 8 + wave) * 4) * 64 + lane;
+  const long coef_group_stride = (long)(a.n_slots / 32) * 4 * 64;  // in half8 units
+  const uint4* basis_head =
+      (const uint4*)(a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h * D * 64) + tid;
+  const long basis_group_stride = (long)a.Hkv * D * 64 / 8;  // in uint4 units
+
+  half8 af[RING][4];  // coefficient operands of the groups in flight, per 16-component step
+  // basis pieces of the groups in flight: one vector per slot (as arrays, the compiler kept them
+  // in scratch memory)
+  typedef uint32_t BasisVec __attribute__((ext_vector_type(4 * BQ)));
+  BasisVec bq0, bq1, bq2, bq3, bq4, bq5, bq6, bq7;
+  auto bq_slot = [&](auto slot) -> BasisVec& {
+    constexpr int s = decltype(slot)::value;
+    static_assert(s < RING, "basis slot");
+    if constexpr (s == 0) return bq0;
+    else if constexpr (s == 1) return bq1;
+    else if constexpr (s == 2) return bq2;
+    else if constexpr (s == 3) return bq3;
+    else if constexpr (s == 4) return bq4;
+    else if constexpr (s == 5) return bq5;
+    else if constexpr (s == 6) return bq6;
+    else return bq7;
+  };
+  auto issue_basis = [&](int g, auto slot) {
+    BasisVec v;
+#pragma unroll
+    for (int i = 0; i < BQ; ++i) {
+      const uint4 t = basis_head[(long)g * basis_group_stride + i * kK2Threads];
+      v[4 * i] = t.x;
+      v[4 * i + 1] = t.y;
+      v[4 * i + 2] = t.z;
+      v[4 * i + 3] = t.w;
+    }
+    bq_slot(slot) = v;
+  };
+  auto issue_coef = [&](int g, auto slot) {
+    constexpr int s = decltype(slot)::value;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) af[s][ks] = coef_frag[(long)g * coef_group_stride + ks * 64];
+  };
+  auto store_basis = [&](auto slot) {  // slot s -> LDS block s & 1
+    constexpr int s = decltype(slot)::value;
+    half_t* Bt = lds + (s & 1) * BLK;
+    const BasisVec v = bq_slot(slot);
+#pragma unroll
+    for (int i = 0; i < BQ; ++i) {
+      const int e = tid + i * kK2Threads;
+      *(uint4*)(Bt + (e >> 3) * kStride + (e & 7) * 8) = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    }
+  };
+  // the lane's RoPE rows (pair j of dimension pairs rb * 32 + 8 v4 + 4 lhi + e, rb < HALF_BLK), as
+  // 16-byte loads issued with the last groups
+  float4 cw[HALF_BLK][4], sw[HALF_BLK][4];
+  auto issue_rope = [&]() {
+    const float* crow = a.rope_cos + (long)pos * HALF_D + 4 * lhi;
+    const float* srow = a.rope_sin + (long)pos * HALF_D + 4 * lhi;
+#pragma unroll
+    for (int rb = 0; rb < HALF_BLK; ++rb)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        cw[rb][v4] = *(const float4*)(crow + rb * 32 + 8 * v4);
+        sw[rb][v4] = *(const float4*)(srow + rb * 32 + 8 * v4);
+      }
+  };
+  auto write_query = [&]() {
+    if (tid < kSmallRows * D) {
+      const float qv = q32 ? __uint_as_float(qlo_bits | qhi_bits << 16)
+                           : a.query_dtype == DKV_F16 ? half_bits_to_float((uint16_t)qlo_bits)
+                                                      : bf16_bits_to_float((uint16_t)qlo_bits);
+      q_s[tid] = q_ok ? qv : 0.0f;
+    }
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  // one group per barrier: its basis block into LDS block g & 1 (that block's previous readers, two
+  // groups back, finished before the last barrier), a barrier, the slot's next basis loads, the
+  // MFMAs (operands read from LDS), then the slot's next coefficient loads (the MFMAs have read them)
+  auto group = [&](int g, auto slot, auto load_next) {
+    constexpr int sl = decltype(slot)::value;
+    store_basis(slot);
+    __syncthreads();
+    if constexpr (decltype(load_next)::value) issue_basis(g + RING, slot);
+    const half_t* Bt = lds + (sl & 1) * BLK;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      half8 ao[DB];
+#pragma unroll
+      for (int rb = 0; rb < DB; ++rb) ao[rb] = lds_half8(Bt + (rb * 32 + l32) * kStride + ks * 16 + lhi * 8);
+#pragma unroll
+      for (int rb = 0; rb < DB; ++rb)
+        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ao[rb], af[sl][ks], acc[rb], 0, 0, 0);
+    }
+    if constexpr (decltype(load_next)::value) issue_coef(g + RING, slot);
+  };
+  // the first RING groups' loads in group order (left to itself, the scheduler issued group 0's
+  // basis last, and the loop's first wait then covered every load in flight)
+  static_for<RING>([&](auto s) {
+    issue_basis(decltype(s)::value, s);
+    issue_coef(decltype(s)::value, s);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  write_query();
+  // G is a multiple of RING (k2_head_form); the last RING groups load nothing more
+  for (int g0 = 0; g0 < G - RING; g0 += RING) static_for<RING>([&](auto s) { group(g0 + decltype(s)::value, s, T{}); });
+  issue_rope();
+  static_for<RING>([&](auto s) { group(G - RING + decltype(s)::value, s, F{}); });
+
+  // ---- epilogue: RoPE on the lane's dimension pairs (d and d + D/2 sit in the same lane), then the
+  // dot with every query row slot (rows past RH are zero) in fp32; the two dimension halves of a
+  // token combine with one shuffle
+  float rlo[HALF_BLK][4][4], rhi[HALF_BLK][4][4];
+#pragma unroll
+  for (int rb = 0; rb < HALF_BLK; ++rb)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const float cv[4] = {cw[rb][v4].x, cw[rb][v4].y, cw[rb][v4].z, cw[rb][v4].w};
+      const float sv[4] = {sw[rb][v4].x, sw[rb][v4].y, sw[rb][v4].z, sw[rb][v4].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float klo = acc[rb][v4 * 4 + e];
+        const float khi = acc[rb + HALF_BLK][v4 * 4 + e];
+        rlo[rb][v4][e] = klo * cv[e] - khi * sv[e];
+        rhi[rb][v4][e] = khi * cv[e] + klo * sv[e];
+      }
+    }
+  float xs[kSmallRows], mx[kSmallRows], sm[kSmallRows];
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r) {
+    float part = 0.0f;
+#pragma unroll
+    for (int rb = 0; rb < HALF_BLK; ++rb)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int j = rb * 32 + 8 * v4 + 4 * lhi;  // pair index, 0 .. D/2-1
+        const float4 qlo = *(const float4*)(q_s + r * D + j);
+        const float4 qhi = *(const float4*)(q_s + r * D + j + HALF_D);
+        part += qlo.x * rlo[rb][v4][0] + qlo.y * rlo[rb][v4][1] + qlo.z * rlo[rb][v4][2] + qlo.w * rlo[rb][v4][3] +
+                qhi.x * rhi[rb][v4][0] + qhi.y * rhi[rb][v4][1] + qhi.z * rhi[rb][v4][2] + qhi.w * rhi[rb][v4][3];
+      }
+    const float full = sum_xor32(part);  // the lane's and its partner's dimension halves
+    xs[r] = n < count ? full * a.scaling : -INFINITY;
+  }
+  // each wave's (max, sum exp) over its 32 tokens, then the tile's over the 8 waves
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r) mx[r] = max32(xs[r]);
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r) sm[r] = mx[r] == -INFINITY ? 0.0f : sum32(__expf(xs[r] - mx[r]));
+  if (lane == 0) {
+    *(float4*)&stat_m[wave][0] = make_float4(mx[0], mx[1], mx[2], mx[3]);
+    *(float4*)&stat_s[wave][0] = make_float4(sm[0], sm[1], sm[2], sm[3]);
+  }
+  static_assert(kSmallRows == 4, "statistics move as float4");
+  __syncthreads();
+  float4 wm[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) wm[w] = *(const float4*)&stat_m[w][0];
+  float Mt[kSmallRows];
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, r == 0 ? wm[w].x : r == 1 ? wm[w].y : r == 2 ? wm[w].z : wm[w].w);
+    Mt[r] = M;
+  }
+  if (tid < RH) {
+    const int r = tid;
+    const float M = r == 0 ? Mt[0] : r == 1 ? Mt[1] : r == 2 ? Mt[2] : Mt[3];
+    float S = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float mw = stat_m[w][r];
+        if (mw != -INFINITY) S += stat_s[w][r] * __expf(mw - M);
+      }
+    }
+    const long o = (long)(h * RH + r) * a.ntiles + tile;
+    a.tile_max[o] = M;
+    a.tile_sum[o] = S;
+  }
+  // probabilities relative to the tile maximum, fp16; every slot of the tile is written (0 past
+  // the tile's tokens); the two lanes of a token write alternate rows
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r) {
+    if (r >= RH) break;
+    if ((r & 1) != lhi) continue;
+    const float p = (xs[r] == -INFINITY) ? 0.0f : __expf(xs[r] - Mt[r]);
+    a.probs[prob_index((long)h * RH + r, (long)tile * kTileTok + n, a.Hq * a.q_len)] = f16_bits(p);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Softmax statistics of the compressed part of sequence b, row `row`.
 // ---------------------------------------------------------------------------
 DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
@@ -1855,10 +2131,20 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 constexpr int kCUs = 256;
 
-// K2 rank split for decodes with few workgroups: the largest power of two that keeps the
+// One KV head per K2 workgroup (keys_scores_head_kernel) for decodes whose 256-row workgroups
+// would leave CUs idle while their (tile, head) pairs fill every CU.
+inline bool k2_head_form(const dkv_attend_args_t* a, int ntiles) {
+  if ((a->q_heads / a->kv_heads) * a->q_len > kSmallRows) return false;
+  if (a->rank % 256 != 0) return false;  // whole rings of four groups
+  const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
+  return wg < kCUs && (long)ntiles * a->kv_heads >= kCUs;
+}
+
+// K2 rank split for decodes with few workgroups otherwise: the largest power of two that keeps the
 // workgroups within one per CU and gives every slice an even number of 64-component groups.
 inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
   if ((a->q_heads / a->kv_heads) * a->q_len > kSmallRows) return 1;
+  if (k2_head_form(a, ntiles)) return 1;
   const int G = a->rank / 64;
   const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
   int k = 1;
@@ -2059,6 +2345,16 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
     mg.ksplit = L.ksplit;
     hipLaunchKernelGGL(split_merge_kernel, dim3((unsigned)((long)L.ntiles * L.R_total)), dim3(kTileTok), 0, st, mg);
     return dkv::check_launch("split_merge");
+  }
+  if (!scoring && k2_head_form(a, L.ntiles)) {  // decoding, one KV head per workgroup
+    k.total_wg = L.ntiles * a->kv_heads;
+    k.per_xcd = (k.total_wg + 7) / 8;
+    const dim3 hgrid(8 * k.per_xcd);
+    if (a->head_dim == 128)
+      hipLaunchKernelGGL(keys_scores_head_kernel<128>, hgrid, dim3(kK2Threads), 0, st, k);
+    else
+      hipLaunchKernelGGL(keys_scores_head_kernel<64>, hgrid, dim3(kK2Threads), 0, st, k);
+    return dkv::check_launch("keys_scores (one head per workgroup)");
   }
   // probabilities: the value side's blocked layout when decoding, row-major [R][ntiles * 256] for
   // question scoring (read by the importance kernel)

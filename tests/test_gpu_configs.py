@@ -1,9 +1,10 @@
 """The two other decode workloads at their real sizes, against the oracle.
 
-- 1b-8k-2pct: Llama-3.2-1B shape, 8,192 tokens at 2 %, bf16 query, all 16 layers.  Its 64 K2
-  workgroups leave CUs idle, so the decode runs the 4-way rank split
-  (``keys_scores_kernel<64, true, true>``) and ``split_merge_kernel``: this is their real-size
-  check.
+- 1b-8k-2pct: Llama-3.2-1B shape, 8,192 tokens at 2 %, bf16 query, all 16 layers.  Its 64
+  256-row K2 workgroups would leave CUs idle, so the decode runs one KV head per workgroup
+  (``keys_scores_head_kernel<64>``, 32 tiles x 8 heads): this is its real-size check.
+- The head form at head_dim 128 (a 3B-shaped 9,000-token context) and over a ragged batch of
+  1B-shaped conversations.
 - 3b-ragged-32: 32 Llama-3.2-3B-shaped conversations of U[2K, 16K] tokens at 3 % in one packed
   buffer, one fused varlen decode step.  The reference decodes one conversation at a time
   (scripts/dimmer.py:195-197), so the pin is the oracle per conversation: the shortest, the
@@ -41,11 +42,11 @@ def test_1b_8k_2pct_all_layers_match_oracle():
     import workloads
     from helpers import assert_close, assert_sensitive, mean_base, workload_oracle
 
-    print("[case] 1b-8k-2pct: 16-layer decode step, rank-split K2 (peaked queries)", flush=True)
+    print("[case] 1b-8k-2pct: 16-layer decode step, one KV head per K2 workgroup (peaked queries)", flush=True)
     w = workloads.build_decode("1b-8k-2pct", device=DEV, keep_host_basis=True, query_scale=PEAKED)
     s = w.shape
     tiles = -(-w.middle // 256)
-    assert tiles * (s.kv_heads // (256 // s.head_dim)) * 2 <= 256, "expected a rank-split decode"
+    assert tiles * (s.kv_heads // (256 // s.head_dim)) < 256 <= tiles * s.kv_heads, "expected the head form"
     w.step()
     torch.cuda.synchronize()
     first = w.outs.clone()
@@ -61,6 +62,57 @@ def test_1b_8k_2pct_all_layers_match_oracle():
         assert_close(w.outs[layer].float().cpu().numpy(), ref, what=f"{what} (bf16 out)", rel_fro=1e9)
         err, fro = assert_close(_fp32_outputs(w, layer), ref, what=what, base=base)
         print(f"  {what}: max abs err {err:.2e}, rel fro {fro:.2e} (uniform attention {gap:.2e} away)", flush=True)
+
+
+@pytest.mark.parametrize("case", ["3b-shape-9000", "1b-ragged-5"])
+def test_head_form_k2_matches_oracle(case):
+    """``keys_scores_head_kernel`` (one KV head per K2 workgroup) at head_dim 128, and over a ragged
+    batch whose tiles belong to several conversations: every layer and (ragged) conversation against
+    the oracle, with the uniform-attention sensitivity check; eager steps deterministic and a graph
+    replay equal to them."""
+    import synth
+    import workloads
+    from helpers import assert_close, assert_sensitive, mean_base, workload_oracle
+
+    if case == "3b-shape-9000":
+        shape = synth.ModelShape(2, 8, 128, 24, 2048)
+        w = workloads.build_decode("3b-shape-9000", shape=shape, tokens=9000, budget=0.03, budget_shape=synth.SHAPE_3B,
+                                   device=DEV, query_dtype=torch.bfloat16, keep_host_basis=True, query_scale=PEAKED)
+        convs = [0]
+    else:
+        shape = synth.ModelShape(2, 8, 64, 32, 1024)
+        # a two-layer model's own budget: 25 % of its 4 KB per token leaves the compressed tokens
+        # about 3.3 planes on average
+        w = workloads.build_ragged(count=5, lo=1000, hi=3000, budget=0.25, seed=77, device=DEV, shape=shape,
+                                   query_scale=PEAKED, keep_host_basis=True)
+        convs = list(range(5))
+    cu = w.context.cu_host.numpy()
+    tiles = int(sum(-(-int(cu[b + 1] - cu[b]) // 256) for b in range(len(cu) - 1)))
+    print(f"[case] head-form K2: {case}, {tiles} tiles x {shape.kv_heads} heads (peaked queries)", flush=True)
+    assert tiles * (shape.kv_heads // (256 // shape.head_dim)) < 256 <= tiles * shape.kv_heads, "expected the head form"
+    w.step()
+    torch.cuda.synchronize()
+    eager = w.outs.clone()
+    w.step()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, w.outs)
+    graph = w.capture()
+    w.outs.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(w.outs, eager), "graph replay differs from the eager step"
+    coef = {k: w.streams[k].dequantize(dtype=torch.float32).cpu().numpy() for k in ("key", "value")}
+    for layer in range(shape.layers):
+        out32 = _fp32_outputs(w, layer)
+        for b in convs:
+            ref = workload_oracle(w, coef, layer, b)
+            base = mean_base(shape, w.tables.mean_v[layer].cpu().numpy(), ref.shape)
+            what = f"{case} b={b} layer {layer}"
+            gap = assert_sensitive(ref, workload_oracle(w, coef, layer, b, query_zero=True), base, what=what)
+            err, fro = assert_close(out32[b:b + 1], ref, what=what, base=base)
+            print(f"  {what}: max abs err {err:.2e}, rel fro {fro:.2e} (uniform attention {gap:.2e} away)",
+                  flush=True)
 
 
 def test_3b_ragged_32_matches_per_conversation_oracle():
