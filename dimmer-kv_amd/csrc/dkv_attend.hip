@@ -17,7 +17,9 @@
 //                      score against the GQA query rows in registers, write
 //                      fp16 probabilities relative to the tile maximum and
 //                      per-tile (max, sum exp) statistics.  The rebuilt keys
-//                      never reach memory.
+//                      never reach memory.  Decodes whose (tile, head group)
+//                      workgroups would leave CUs idle run one workgroup per
+//                      (tile, KV head) instead (keys_scores_head).
 //   K3a value_weights: per (1024-token split, 64-component group, 32 rows):
 //                      p @ value codes on MFMA plus sum(p * offset) ->
 //                      coefficient-space partial sums.
@@ -88,10 +90,6 @@ struct K2Args {
   // question scoring: (max, sum exp) of every row over each 64-token quarter of a tile, [R][ntiles * 4]
   float* sub_max;
   float* sub_sum;
-  // rank split (decoding with few workgroups): each workgroup rebuilds its keys from g_per_split
-  // of the 64-component groups and writes partial scores [ksplit][R_total][ntiles * 256]
-  float* split_scores;
-  int ksplit, g_per_split;
 };
 
 DKV_DEVICE uint16_t f16_bits(float v) {
@@ -425,11 +423,10 @@ DKV_DEVICE void stage_rope_rows(const K2Args& a, float* cs, float* sn, const int
   __syncthreads();
 }
 
-template <int D, bool SPLIT, bool ROWMAJOR>
+template <int D, bool ROWMAJOR>
 DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
                                            float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
-                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs,
-                                           int split) {
+                                           int tile, int h0, int b, int RH, const int* pos_s, const float* qs) {
   constexpr int HPW = 256 / D;
   constexpr int DB = D / 32;
   constexpr int HALF_BLK = DB / 2;
@@ -508,14 +505,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
         const int n = tq * 64 + tb * 32 + l32;
         x[tb] = n < count ? full * a.scaling : -INFINITY;
         xs[hw][r][tb] = x[tb];
-        if constexpr (SPLIT) {  // RoPE and the dot are linear in the key: partial scores add up
-          if (tb == lhi && n < count)
-            a.split_scores[((long)split * a.Hq * a.q_len + h * RH + r) * ((long)a.ntiles * kTileTok) +
-                           (long)tile * kTileTok + n] = x[tb];
-          continue;
-        }
       }
-      if constexpr (SPLIT) continue;
       if constexpr (ROWMAJOR) {  // question scoring: this wave's quarter (64 tokens), written at once
         const float mq = max32(fmaxf(x[0], x[1]));
         const float e0 = mq == -INFINITY ? 0.0f : __expf(x[0] - mq);
@@ -541,7 +531,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
       }
     }
   }
-  if constexpr (SPLIT || ROWMAJOR) return;  // the merge kernel, or the loop above, wrote everything
+  if constexpr (ROWMAJOR) return;  // the loop above wrote everything
   __syncthreads();
   if (tid < HPW * kSmallRows) {
     const int hl = tid / kSmallRows, r = tid % kSmallRows;
@@ -590,7 +580,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 // [256][64] are fetched into registers one group ahead and stored into a
 // double-buffered, padded LDS tile; 32x32x16 fp16 MFMAs accumulate the keys.
 // ---------------------------------------------------------------------------
-template <int D, bool SMALL, bool SPLIT = false, bool ROWMAJOR = false>
+template <int D, bool SMALL, bool ROWMAJOR = false>
 __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   constexpr int HPW = 256 / D;      // heads per workgroup
   constexpr int DB = D / 32;        // 32-row blocks per head
@@ -605,10 +595,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int lin = (bid & 7) * a.per_xcd + (bid >> 3);
   if (lin >= a.total_wg) return;
   const int nhg = a.Hkv / HPW;
-  // with a rank split, consecutive ids (one XCD) are the head groups of one (tile, split): they
-  // read the same coefficient groups
-  const int tile = SPLIT ? lin / (nhg * a.ksplit) : lin / nhg, hg = lin % nhg;
-  const int split = SPLIT ? (lin / nhg) % a.ksplit : 0;
+  const int tile = lin / nhg, hg = lin % nhg;  // consecutive ids (one XCD): the head groups of a tile
   const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
   const int b = bt.x;
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
@@ -616,8 +603,6 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int count = min(kTileTok, sr.y - tok0);
   const int h0 = hg * HPW;
   const int G = a.G;
-  const int gb = SPLIT ? split * a.g_per_split : 0;  // this workgroup's groups: gb .. ge - 1
-  const int ge = SPLIT ? gb + a.g_per_split : G;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tq = wave & 3, hs = wave >> 2;
@@ -655,8 +640,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
-      // the key mean enters once: in the first rank slice only
-      const float4 m4 = split == 0 ? *(const float4*)(mean_rows + j * 32 + 8 * v4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 m4 = *(const float4*)(mean_rows + j * 32 + 8 * v4);
       acc[0][j][4 * v4 + 0] = acc[1][j][4 * v4 + 0] = m4.x;
       acc[0][j][4 * v4 + 1] = acc[1][j][4 * v4 + 1] = m4.y;
       acc[0][j][4 * v4 + 2] = acc[1][j][4 * v4 + 2] = m4.z;
@@ -719,18 +703,18 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // wave of a SIMD runs MFMAs while the other does its memory work.
   // sched_barrier keeps the compiler from moving loads into the MFMA
   // segments; a wave in its MFMA segment runs at raised priority.
-  DKV_K2_ISSUE_A(gb, af0);
-  DKV_K2_ISSUE_B(gb);
+  DKV_K2_ISSUE_A(0, af0);
+  DKV_K2_ISSUE_B(0);
   DKV_K2_FINISH(0);
-  DKV_K2_ISSUE_B(gb + 1);
-  DKV_K2_ISSUE_A(gb + 1, af1);
+  DKV_K2_ISSUE_B(1);
+  DKV_K2_ISSUE_A(1, af1);
   __syncthreads();
   if (hs == 1) __builtin_amdgcn_s_barrier();
-  // ge - gb is even (the rank is a multiple of 256; a slice an even count).  The last two groups run
+  // G is even (the rank is a multiple of 256).  The last two groups run
   // after the loop, which loads nothing more: loads past the end would only repeat the last group and
   // hold up the epilogue's loads behind them (a branch around them in the loop costs more: the
   // compiler then waits for every load at the join).
-  for (int g = gb; g < ge - 2; g += 2) {
+  for (int g = 0; g < G - 2; g += 2) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     DKV_K2_MFMA(0, af0);
@@ -777,8 +761,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   const int gq = a.Hq / a.Hkv;
   if constexpr (SMALL) {
-    keys_scores_small_epilogue<D, SPLIT, ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s,
-                                                   q_s, split);
+    keys_scores_small_epilogue<D, ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s);
     return;
   } else {
 
@@ -1753,59 +1736,6 @@ DKV_DEVICE half8 codes_to_half8(uint32_t lo, uint32_t hi) {
 }
 
 // ---------------------------------------------------------------------------
-// K2 merge (rank split only): one workgroup per (tile, output row) adds the
-// slices' partial scores of the tile's tokens in slice order, then writes the
-// tile's softmax statistics and the fp16 probabilities relative to the tile
-// maximum, as the unsplit decode epilogue does.
-// ---------------------------------------------------------------------------
-struct K2MergeArgs {
-  const int32_t* cu_seqlens;
-  const float* split_scores;  // [ksplit][R_total][ntiles * 256]
-  uint16_t* probs;
-  float* tile_max;
-  float* tile_sum;
-  int batch, n_total, ntiles, R_total, ksplit;
-};
-
-__global__ __launch_bounds__(kTileTok) void split_merge_kernel(K2MergeArgs a) {
-  __shared__ float red[2][kTileTok / 64];
-  const int tile = blockIdx.x / a.R_total, row = blockIdx.x % a.R_total;
-  const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
-  const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, bt.x);
-  const int count = min(kTileTok, sr.y - (sr.x + bt.y * kTileTok));
-  const int n = threadIdx.x, lane = n & 63, wave = n >> 6;
-  const long slice = (long)a.R_total * a.ntiles * kTileTok;
-  const float* src = a.split_scores + ((long)row * a.ntiles + tile) * kTileTok + min(n, count - 1);
-  float x = 0.0f;
-  for (int s0 = 0; s0 < a.ksplit; s0 += 8) {  // the loads of 8 slices go out together
-    float v[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = src[min(s0 + k, a.ksplit - 1) * slice];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x += s0 + k < a.ksplit ? v[k] : 0.0f;
-  }
-  if (n >= count) x = -INFINITY;
-  const float m = wave_max(x);
-  if (lane == 0) red[0][wave] = m;
-  __syncthreads();
-  float M = red[0][0];
-#pragma unroll
-  for (int w = 1; w < kTileTok / 64; ++w) M = fmaxf(M, red[0][w]);
-  const float pr = (x == -INFINITY) ? 0.0f : __expf(x - M);
-  const float sm = wave_sum(pr);
-  if (lane == 0) red[1][wave] = sm;
-  __syncthreads();
-  if (n == 0) {
-    float S = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kTileTok / 64; ++w) S += red[1][w];
-    a.tile_max[(long)row * a.ntiles + tile] = M;
-    a.tile_sum[(long)row * a.ntiles + tile] = S;
-  }
-  a.probs[prob_index(row, (long)tile * kTileTok + n, a.R_total)] = f16_bits(pr);
-}
-
-// ---------------------------------------------------------------------------
 // K3a: w[row][k] = sum_t p[row][t] * value[t][k] for one token split, one
 // 64-component group and one block of 32 rows, with p = exp(s - M_row).
 // value = code * scale + offset, so
@@ -2122,9 +2052,7 @@ __global__ __launch_bounds__(kRowThreads) void finish_kernel(RowMergeArgs a) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int ntiles, nsplits, split_tok, R_total, nchunks, n_total, n_slots;
-  int ksplit;
-  size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, exact, split_scores,
-      total;
+  size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, exact, total;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -2132,28 +2060,17 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 constexpr int kCUs = 256;
 
 // One KV head per K2 workgroup (keys_scores_head_kernel) for decodes whose 256-row workgroups
-// would leave CUs idle while their (tile, head) pairs fill every CU.
+// would leave CUs idle: D / 256 as many rows per workgroup, 256 / D times the workgroups, each
+// the same length, and no partial results to merge.
 inline bool k2_head_form(const dkv_attend_args_t* a, int ntiles) {
   if ((a->q_heads / a->kv_heads) * a->q_len > kSmallRows) return false;
   if (a->rank % 256 != 0) return false;  // whole rings of four groups
   const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
-  return wg < kCUs && (long)ntiles * a->kv_heads >= kCUs;
-}
-
-// K2 rank split for decodes with few workgroups otherwise: the largest power of two that keeps the
-// workgroups within one per CU and gives every slice an even number of 64-component groups.
-inline int k2_split(const dkv_attend_args_t* a, int ntiles) {
-  if ((a->q_heads / a->kv_heads) * a->q_len > kSmallRows) return 1;
-  if (k2_head_form(a, ntiles)) return 1;
-  const int G = a->rank / 64;
-  const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
-  int k = 1;
-  while (wg * k * 2 <= kCUs && G % (4 * k) == 0) k *= 2;
-  return k;
+  return wg < kCUs;
 }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][probabilities][tile statistics]
-// [split partials][chunk partials][exact-tail results][K2 rank-slice partial scores].
+// [split partials][chunk partials][exact-tail results].
 // The decoded areas are indexed by token slot (256 per tile, see slot_token).
 // `values` false: no value-decode areas (question scoring decodes and reads the keys alone), so
 // every later area starts right after the key operands.
@@ -2196,9 +2113,6 @@ Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   off += align256((size_t)L.nchunks * a->batch * L.R_total * a->head_dim * 4);
   L.exact = off;
   off += align256((size_t)a->batch * L.R_total * (a->head_dim + 2) * 4);
-  L.ksplit = k2_split(a, L.ntiles);
-  L.split_scores = off;
-  if (L.ksplit > 1) off += align256((size_t)L.ksplit * L.R_total * L.ntiles * kTileTok * 4);
   L.total = off;
   return L;
 }
@@ -2319,33 +2233,6 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   // decoding (at most kSmallRows query rows per KV head) and question scoring are separate
   // instantiations, so neither epilogue's registers weigh on the other's main loop
   const bool small = (a->q_heads / a->kv_heads) * a->q_len <= kSmallRows;
-  if (!scoring && L.ksplit > 1) {  // decoding with few workgroups: rank slices, then the merge
-    k.ksplit = L.ksplit;
-    k.g_per_split = k.G / L.ksplit;
-    k.split_scores = (float*)(ws + L.split_scores);
-    k.total_wg *= L.ksplit;
-    k.per_xcd = (k.total_wg + 7) / 8;
-    const dim3 sgrid(8 * k.per_xcd);
-    if (a->head_dim == 128)
-      hipLaunchKernelGGL((keys_scores_kernel<128, true, true>), sgrid, dim3(kK2Threads), 0, st, k);
-    else
-      hipLaunchKernelGGL((keys_scores_kernel<64, true, true>), sgrid, dim3(kK2Threads), 0, st, k);
-    int rc = dkv::check_launch("keys_scores (rank slices)");
-    if (rc) return rc;
-    K2MergeArgs mg{};
-    mg.cu_seqlens = a->cu_seqlens;
-    mg.split_scores = k.split_scores;
-    mg.probs = k.probs;
-    mg.tile_max = k.tile_max;
-    mg.tile_sum = k.tile_sum;
-    mg.batch = a->batch;
-    mg.n_total = L.n_total;
-    mg.ntiles = L.ntiles;
-    mg.R_total = L.R_total;
-    mg.ksplit = L.ksplit;
-    hipLaunchKernelGGL(split_merge_kernel, dim3((unsigned)((long)L.ntiles * L.R_total)), dim3(kTileTok), 0, st, mg);
-    return dkv::check_launch("split_merge");
-  }
   if (!scoring && k2_head_form(a, L.ntiles)) {  // decoding, one KV head per workgroup
     k.total_wg = L.ntiles * a->kv_heads;
     k.per_xcd = (k.total_wg + 7) / 8;
@@ -2362,20 +2249,20 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
     if (small && !scoring)
       hipLaunchKernelGGL((keys_scores_kernel<128, true>), grid, dim3(kK2Threads), 0, st, k);
     else if (small)
-      hipLaunchKernelGGL((keys_scores_kernel<128, true, false, true>), grid, dim3(kK2Threads), 0, st, k);
+      hipLaunchKernelGGL((keys_scores_kernel<128, true, true>), grid, dim3(kK2Threads), 0, st, k);
     else if (!scoring)
       hipLaunchKernelGGL((keys_scores_kernel<128, false>), grid, dim3(kK2Threads), 0, st, k);
     else
-      hipLaunchKernelGGL((keys_scores_kernel<128, false, false, true>), grid, dim3(kK2Threads), 0, st, k);
+      hipLaunchKernelGGL((keys_scores_kernel<128, false, true>), grid, dim3(kK2Threads), 0, st, k);
   } else {
     if (small && !scoring)
       hipLaunchKernelGGL((keys_scores_kernel<64, true>), grid, dim3(kK2Threads), 0, st, k);
     else if (small)
-      hipLaunchKernelGGL((keys_scores_kernel<64, true, false, true>), grid, dim3(kK2Threads), 0, st, k);
+      hipLaunchKernelGGL((keys_scores_kernel<64, true, true>), grid, dim3(kK2Threads), 0, st, k);
     else if (!scoring)
       hipLaunchKernelGGL((keys_scores_kernel<64, false>), grid, dim3(kK2Threads), 0, st, k);
     else
-      hipLaunchKernelGGL((keys_scores_kernel<64, false, false, true>), grid, dim3(kK2Threads), 0, st, k);
+      hipLaunchKernelGGL((keys_scores_kernel<64, false, true>), grid, dim3(kK2Threads), 0, st, k);
   }
   return dkv::check_launch("keys_scores");
 }

@@ -8,9 +8,9 @@ The decode queries are peaked (N(0, 100^2) entries, score spread of order 1 over
 tokens): with the unit-variance queries of the benchmark the attention is nearly uniform
 and its output nearly the value mean, so the check would barely depend on the scores.  Each
 checked layer first shows that uniform attention (the oracle with a zero query) misses the
-bar by a wide margin.  These are the cases that run the unsplit decode instantiations of
+bar by a wide margin.  These are the cases that run the 256-row decode instantiations of
 K2: ``keys_scores_kernel<128, true>`` here, ``<64, true>`` in the 33K-token 1B case (at
-least 129 token tiles, so no rank split)."""
+least 129 token tiles; fewer 256-row workgroups than CUs would take one KV head per workgroup)."""
 
 from __future__ import annotations
 
@@ -206,15 +206,15 @@ def test_3b_16k_dkvtc_decode_matches_oracle():
 
 def test_1b_33k_unsplit_head_dim_64_matches_oracle():
     """Llama-3.2-1B shape (head_dim 64), two layers, 33,004 tokens: 129 token tiles x 2 head groups
-    = 258 K2 workgroups, more than one per CU, so the decode runs the unsplit
-    ``keys_scores_kernel<64, true>`` (the rank split only starts at <= 128 workgroups)."""
+    = 258 K2 workgroups, at least one per CU, so the decode runs the 256-row
+    ``keys_scores_kernel<64, true>`` (below 256 it takes one KV head per workgroup)."""
     import synth
     import workloads
     from helpers import mean_base
 
     shape = synth.ModelShape(2, 8, 64, 32, 1024)
     tokens = 33_004
-    print(f"[case] 1B shape, 2 layers, {tokens} tokens: unsplit K2 at head_dim 64 (peaked queries)", flush=True)
+    print(f"[case] 1B shape, 2 layers, {tokens} tokens: 256-row K2 at head_dim 64 (peaked queries)", flush=True)
     w = workloads.build_decode("1b-33k", shape=shape, tokens=tokens, device=DEV, keep_host_basis=True,
                                query_dtype=torch.bfloat16, query_scale=PEAKED)
     tiles = -(-w.middle // 256)
