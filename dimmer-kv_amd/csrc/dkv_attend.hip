@@ -1409,125 +1409,136 @@ constexpr int kChunkLoads = 8;  // chunk partials per thread issued in the first
 // Le = sum_e exp(s_e - Me) and ve[d] = sum_e exp(s_e - Me) v_e[d], written to ex[wg] as (Me, Le, ve).
 // It needs only the query and the exact tokens, so it runs beside K3b's chunk workgroups (their
 // registers and LDS leave room on every CU) instead of on the finish kernel's critical path.
-template <int NT>
+//
+// One wave does it all, with no barrier: the query, the keys of the first kExactKR * 16 tokens and
+// the values of the first kExactVR * (256 / D) go out in one round (every load unconditional, with
+// clamped indices: a load under a per-element condition is a branch and a wait each).  Scores: four
+// lanes per token, 32 dimensions each, 16 tokens per round, reduced with two lane exchanges; the
+// weights go through LDS (a wave's LDS accesses run in order); values: a lane holds 4 consecutive
+// dimensions of one token slot (D / 4 lanes per token), the slots combined with lane exchanges.
+constexpr int kExactKR = 3;   // key rounds (16 tokens each) loaded in the first round
+constexpr int kExactVR = 20;  // value loads (16 bytes per lane) in the first round
+
 __device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
-  constexpr int NW = NT / 64;
-  float* q = smem;               // [128] the query row
-  float* se = q + 128;           // [kMaxExact] exact scores, then weights
-  float* wred = se + kMaxExact;  // [2][NW] per-wave maxima and sums
-  float* buf = wred + 2 * NW;    // [NT] per-thread exact value sums
+  const int lane = threadIdx.x;
+  if (lane >= 64) return;  // one wave
+  float* q = smem;          // [128] the query row
+  float* se = q + 128;      // [kMaxExact] exact scores, then weights
   const int row = wg % a.R_total;
   const int b = wg / a.R_total;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.D;
   const int gq = a.Hq / a.Hkv;
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
   const int e0 = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
   const int E = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
-  const int d = tid % D, part = tid / D, parts = NT / D;
-  // Every global load goes out in one round before any value is used: each dependent round trip
-  // to memory costs microseconds here, and this work is nothing but them.  Loads under a
-  // per-element condition compile to one branch and one wait per load, so they are
-  // unconditional (clamped indices) or under one uniform branch: the query element, a quarter key
-  // row (token tid / 4, 32 dimensions), the exact values.
-  const long qidx = (((long)b * a.Hq + qh) * a.q_len + qi) * D + d;
-  const uint32_t qword = load_query_word(a.query, qidx, a.query_dtype);
-  const int kj = tid >> 2, ks = tid & 3;
+  const long qbase = (((long)b * a.Hq + qh) * a.q_len + qi) * D;
+  const uint32_t qw0 = load_query_word(a.query, qbase + min(lane, D - 1), a.query_dtype);
+  const uint32_t qw1 = load_query_word(a.query, qbase + min(lane + 64, D - 1), a.query_dtype);
+  // scores: lane (kj, ks) takes dimensions ks * 32 .. +32 of token kj of each round
+  const int kj = lane >> 2, ks = lane & 3;
   const bool kslice = ks * 32 < D;
-  float4 k4[8];
-  float vv[kExactVB];
-  float mval = 0.0f;
+  const float* krow0 = a.key_exact + ((long)h * a.E_total + e0) * D + min(ks * 32, D - 32);
+  // values: lane (tp, dq) holds dimensions 4 dq .. 4 dq + 3 of token slot tp
+  const int lpt = D / 4;  // lanes per token
+  const int tpi = 64 / lpt;  // tokens per value load
+  const int dq = lane % lpt, tp = lane / lpt;
+  const float* vrow0 = a.value_exact + ((long)h * a.E_total + e0) * D + 4 * dq;
+  float4 k4[kExactKR][8];
+  float mv[kExactKR];
+  float4 v4[kExactVR];
   if (E > 0) {
-    const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + min(kj, E - 1)) * D +
-                                       min(ks * 32, D - 32));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) k4[i] = kr[i];
+    for (int r = 0; r < kExactKR; ++r) {
+      const float4* kr = (const float4*)(krow0 + (long)min(r * 16 + kj, E - 1) * D);
 #pragma unroll
-    for (int i = 0; i < kExactVB; ++i)
-      vv[i] = a.value_exact[((long)h * a.E_total + e0 + min(part + i * parts, E - 1)) * D + d];
-    if (a.mask) mval = a.mask[(long)qi * E + min(kj, E - 1)];
-  } else {
+      for (int i = 0; i < 8; ++i) k4[r][i] = kr[i];
+      mv[r] = a.mask ? a.mask[(long)qi * E + min(r * 16 + kj, E - 1)] : 0.0f;
+    }
 #pragma unroll
-    for (int i = 0; i < kExactVB; ++i) vv[i] = 0.0f;
+    for (int i = 0; i < kExactVR; ++i) v4[i] = *(const float4*)(vrow0 + (long)min(tp + i * tpi, E - 1) * D);
   }
-  if (tid < D) q[tid] = query_word_value(qword, qidx, a.query_dtype);
-  __syncthreads();
-  // scores: four lanes per token, 32 dimensions each, NT / 4 tokens per pass
-  float me = -INFINITY;
-  constexpr int TPP = NT / 4;
-  const int Epad = (E + TPP - 1) / TPP * TPP;
-  for (int j = kj; j < Epad; j += TPP) {
-    if (j != kj && j < E) {
-      const float4* kr = (const float4*)(a.key_exact + ((long)h * a.E_total + e0 + j) * D + min(ks * 32, D - 32));
+  if (lane < D) q[lane] = query_word_value(qw0, qbase + lane, a.query_dtype);
+  if (lane + 64 < D) q[lane + 64] = query_word_value(qw1, qbase + lane + 64, a.query_dtype);
+  float ex_m = -INFINITY, ex_l = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (E > 0) {
+    float4 qv[8];  // this lane's 32 query dimensions
 #pragma unroll
-      for (int i = 0; i < 8; ++i) k4[i] = kr[i];
-      if (a.mask) mval = a.mask[(long)qi * E + j];
-    }
-    float dot = 0.0f;
-    if (kslice) {
-      const float* qr = q + ks * 32;
+    for (int i = 0; i < 8; ++i) qv[i] = *(const float4*)(q + min(ks * 32, D - 32) + 4 * i);
+    auto score = [&](const float4 (&kk)[8], float mval, int j) {
+      float dot = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dot += qr[4 * i] * k4[i].x + qr[4 * i + 1] * k4[i].y + qr[4 * i + 2] * k4[i].z + qr[4 * i + 3] * k4[i].w;
-    }
-    dot += lane_xor1(dot);
-    dot += lane_xor2(dot);
-    if (j < E) {
+      for (int i = 0; i < 8; ++i) dot += qv[i].x * kk[i].x + qv[i].y * kk[i].y + qv[i].z * kk[i].z + qv[i].w * kk[i].w;
+      dot = kslice ? dot : 0.0f;
+      dot += lane_xor1(dot);
+      dot += lane_xor2(dot);
       const float sc = dot * a.scaling + mval;
-      if (ks == 0) se[j] = sc;
-      me = fmaxf(me, sc);
+      if (ks == 0 && j < E) se[j] = sc;
+      return j < E ? sc : -INFINITY;
+    };
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kExactKR; ++r) m = fmaxf(m, score(k4[r], mv[r], r * 16 + kj));
+    for (int j0 = kExactKR * 16; j0 < E; j0 += 16) {  // more than kExactKR * 16 exact tokens
+      float4 kk[8];
+      const float4* kr = (const float4*)(krow0 + (long)min(j0 + kj, E - 1) * D);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) kk[i] = kr[i];
+      const float mval = a.mask ? a.mask[(long)qi * E + min(j0 + kj, E - 1)] : 0.0f;
+      m = fmaxf(m, score(kk, mval, j0 + kj));
+    }
+    ex_m = wave_max(m);
+    float l = 0.0f;
+    for (int j = lane; j < E; j += 64) {
+      const float s = se[j];
+      const float w = (ex_m == -INFINITY || s == -INFINITY) ? 0.0f : __expf(s - ex_m);
+      se[j] = w;
+      l += w;
+    }
+    ex_l = wave_sum(l);
+    // weighted values: every weight read is unconditional (clamped), the select drops the products
+    // of slots past the exact tokens
+#pragma unroll
+    for (int i = 0; i < kExactVR; ++i) {
+      const int t = tp + i * tpi;
+      const float w = t < E ? se[min(t, kMaxExact - 1)] : 0.0f;
+      acc.x += w * v4[i].x;
+      acc.y += w * v4[i].y;
+      acc.z += w * v4[i].z;
+      acc.w += w * v4[i].w;
+    }
+    for (int t0 = kExactVR * tpi; t0 < E; t0 += tpi) {  // tokens past the first round's values
+      const int t = t0 + tp;
+      const float4 vv = *(const float4*)(vrow0 + (long)min(t, E - 1) * D);
+      const float w = t < E ? se[min(t, kMaxExact - 1)] : 0.0f;
+      acc.x += w * vv.x;
+      acc.y += w * vv.y;
+      acc.z += w * vv.z;
+      acc.w += w * vv.w;
     }
   }
-  me = wave_max(me);
-  if (lane == 0) wred[wave] = me;
-  __syncthreads();
-  float Me = wred[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) Me = fmaxf(Me, wred[w]);
-  float le = 0.0f;
-  for (int j = tid; j < E; j += NT) {
-    const float wgt = (Me == -INFINITY || se[j] == -INFINITY) ? 0.0f : __expf(se[j] - Me);
-    se[j] = wgt;
-    le += wgt;
+  // the token slots' sums: lanes dq, dq + lpt, ... (D = 128: two slots; D = 64: four)
+  if (lpt == 16) {
+    acc.x = sum_xor16(acc.x);
+    acc.y = sum_xor16(acc.y);
+    acc.z = sum_xor16(acc.z);
+    acc.w = sum_xor16(acc.w);
   }
-  le = wave_sum(le);
-  if (lane == 0) wred[NW + wave] = le;
-  __syncthreads();
-  // exact values: thread (d, part) takes tokens part, part + parts, ...; every weight read is
-  // unconditional (a read under a per-element condition is a branch and a wait each), the select
-  // drops the products of slots past the exact tokens, whatever they hold
-  float ve = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kExactVB; ++i) {
-    const int j = part + i * parts;
-    const float prod = se[min(j, kMaxExact - 1)] * vv[i];
-    ve += j < E ? prod : 0.0f;
-  }
-  for (int j0 = part + kExactVB * parts; j0 < E; j0 += 8 * parts) {
-    float v8[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v8[i] = a.value_exact[((long)h * a.E_total + e0 + min(j0 + i * parts, E - 1)) * D + d];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int j = j0 + i * parts;
-      if (j < E) ve += se[j] * v8[i];
-    }
-  }
-  buf[tid] = ve;
-  __syncthreads();
+  acc.x = sum_xor32(acc.x);
+  acc.y = sum_xor32(acc.y);
+  acc.z = sum_xor32(acc.z);
+  acc.w = sum_xor32(acc.w);
   float* ex = a.ex + (long)wg * (D + 2);
-  if (tid < D) {
-    float ves = 0.0f;
-    for (int p = 0; p < parts; ++p) ves += buf[p * D + tid];
-    ex[2 + tid] = ves;
+  if (tp == 0) {  // ex + 2 + 4 dq is 8-byte aligned only
+    ex[2 + 4 * dq] = acc.x;
+    ex[3 + 4 * dq] = acc.y;
+    ex[4 + 4 * dq] = acc.z;
+    ex[5 + 4 * dq] = acc.w;
   }
-  if (tid == 0) {
-    float Le = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) Le += wred[NW + w];
-    ex[0] = Me;
-    ex[1] = Le;
+  if (lane == 0) {
+    ex[0] = ex_m;
+    ex[1] = ex_l;
   }
 }
 
@@ -1945,8 +1956,8 @@ template <int NR>
 __global__ __launch_bounds__(kRowThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
   if ((int)blockIdx.x < a.n_exact_wg) {  // the exact tail of output row blockIdx.x
-    __shared__ float xsm[128 + kMaxExact + 2 * (kRowThreads / 64) + kRowThreads];
-    row_exact<kRowThreads>(ex, blockIdx.x, xsm);
+    __shared__ __attribute__((aligned(16))) float xsm[128 + kMaxExact];
+    row_exact(ex, blockIdx.x, xsm);
     return;
   }
   __shared__ __attribute__((aligned(16))) float W[NR][kChunk];  // the pass's summed weights
