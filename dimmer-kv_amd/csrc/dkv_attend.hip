@@ -1205,18 +1205,14 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
   // basis pieces of the groups in flight: one vector per slot (as arrays, the compiler kept them
   // in scratch memory)
   typedef uint32_t BasisVec __attribute__((ext_vector_type(4 * BQ)));
-  BasisVec bq0, bq1, bq2, bq3, bq4, bq5, bq6, bq7;
+  static_assert(RING == 4, "four basis slots");
+  BasisVec bq0, bq1, bq2, bq3;
   auto bq_slot = [&](auto slot) -> BasisVec& {
     constexpr int s = decltype(slot)::value;
-    static_assert(s < RING, "basis slot");
     if constexpr (s == 0) return bq0;
     else if constexpr (s == 1) return bq1;
     else if constexpr (s == 2) return bq2;
-    else if constexpr (s == 3) return bq3;
-    else if constexpr (s == 4) return bq4;
-    else if constexpr (s == 5) return bq5;
-    else if constexpr (s == 6) return bq6;
-    else return bq7;
+    else return bq3;
   };
   auto issue_basis = [&](int g, auto slot) {
     BasisVec v;
