@@ -89,9 +89,15 @@ def test_dequantize_codes_exhaustive():
     ("3b2", 700, (1,), 120.0, 5, "float32"),        # q_len > 1 with a causal exact part
     ("3b2", 700, (0,), 120.0, 5, "bfloat16"),       # many-row epilogue, per query type
     ("1b", 900, (2,), 150.0, 3, "float16"),
+    # one KV head per K2 workgroup with 1, 2 and 4 query rows per KV head (GQA groups of 1 and 2)
+    ("mha64", 700, (0, 1), 120.0, 1, "float32"),
+    ("mha64", 700, (1,), 120.0, 4, "bfloat16"),
+    ("gq2_128", 900, (0,), 120.0, 1, "float16"),
+    ("gq2_128", 700, (1,), 120.0, 2, "float32"),
 ])
 def test_attend_matches_oracle(shape_name, tokens, layers, query_scale, q_len, qdtype):
-    shape = synth.SHAPE_1B if shape_name == "1b" else synth.ModelShape(2, 8, 128, 24, 2048)
+    shape = {"1b": synth.SHAPE_1B, "3b2": synth.ModelShape(2, 8, 128, 24, 2048),
+             "mha64": synth.ModelShape(2, 8, 64, 8, 1024), "gq2_128": synth.ModelShape(2, 8, 128, 16, 2048)}[shape_name]
     print(f"[case] attend {shape_name} T={tokens} scale={query_scale} q_len={q_len} {qdtype}", flush=True)
     case = build_case(shape, tokens, seed=1234, query_scale=query_scale, q_len=q_len,
                       query_dtype=getattr(torch, qdtype))
