@@ -108,6 +108,18 @@ def test_kvtc_methods_on_cpu(name):
     budget = methods.budget_of(name)
     assert out.used_bytes <= int(budget * tokens * 2 * codec.exact_bytes)
     start, end = codec.last_span
+    # bytes counted = exact tokens + every kept (token, stream) at its rung's oracle size
+    want_bytes = (tokens - (end - start)) * 2 * codec.exact_bytes
+    for kind in ("key", "value"):
+        rungs = codec.streams[kind].rungs
+        for level in codec.last_choice[kind].tolist():
+            if level >= 0:
+                want_bytes += (codec.exact_bytes if level == len(rungs)
+                               else kvtc_ref.rung_bytes(rungs[level].numpy(), 64))
+    assert out.used_bytes == want_bytes
+    assert abs(sum(out.histogram.values()) - 1.0) < 1e-12
+    assert set(out.histogram) <= {"evict", "exact"} | {f"{s / codec.exact_bytes:.3f}" for kind in ("key", "value")
+                                                       for s in codec.streams[kind].rung_bytes}
     for layer in range(shape.layers):
         assert torch.equal(out.keys[layer][..., :start, :], keys[layer][..., :start, :])
         assert torch.equal(out.values[layer][..., end:, :], values[layer][..., end:, :])
