@@ -25,12 +25,13 @@
 //                      coefficient-space partial sums.
 //   K3b basis_apply  : sum the partials over the splits and multiply once by
 //                      the value basis of the KV head (per 128-component
-//                      chunk and 64-dimension slice); beside them, one
-//                      workgroup per output row computes the exact tail
-//                      (sinks, recent window, new tokens): its scores, their
-//                      maximum and exponential sum, and the weighted values.
+//                      chunk and 64-dimension slice); beside them, four
+//                      one-wave workgroups per output row compute the exact
+//                      tail (sinks, recent window, new tokens), a share of
+//                      its tokens each: scores, their maximum and
+//                      exponential sum, and the weighted values.
 //   K3c finish       : per output row, merge the tiles' softmax statistics
-//                      (Mc, Lc) with the exact tail's (Me, Le, ve) in one
+//                      (Mc, Lc) with the exact tail's shares (Me, Le, ve) in one
 //                      softmax: out = (ec (sum of chunk partials + Lc mean_v)
 //                      + ee ve) / (ec Lc + ee Le), ec and ee taking Mc and Me
 //                      to the common maximum.
@@ -65,7 +66,7 @@ struct RowMergeArgs {
   const float* mask;
   const void* query;
   const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
-  float* ex;              // [batch * R_total][D + 2] per row: Me, Le, then ve[D] (the exact tail, row_exact)
+  float* ex;              // [batch * R_total][kExactParts][D + 2] per row and share: Me, Le, then ve[D] (row_exact)
   void* out;              // [batch][q_len][Hq][D], out_dtype
   float scaling;
   int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
@@ -1396,60 +1397,72 @@ DKV_DEVICE int tiles_before(const int32_t* cu, int b, int tile) {
 // recent window, new tokens; computed beside K3b, row_exact) in one softmax
 // and writes the row's output.
 // ---------------------------------------------------------------------------
-constexpr int kExactVB = 32;  // exact tokens per thread whose values are loaded in the first round
-
 constexpr int kChunkLoads = 8;  // chunk partials per thread issued in the first round
 
-// The exact tail of one output row (workgroup wg = b * R_total + row), in extra workgroups of K3b:
-// the row's scores against its sequence's exact tokens (mask added), their maximum Me,
-// Le = sum_e exp(s_e - Me) and ve[d] = sum_e exp(s_e - Me) v_e[d], written to ex[wg] as (Me, Le, ve).
-// It needs only the query and the exact tokens, so it runs beside K3b's chunk workgroups (their
-// registers and LDS leave room on every CU) instead of on the finish kernel's critical path.
+// The exact tail of output row wg = b * R_total + row, in extra workgroups of K3b: the row's scores
+// against its sequence's exact tokens (mask added), their maximum Me, Le = sum_e exp(s_e - Me) and
+// ve[d] = sum_e exp(s_e - Me) v_e[d].  It needs only the query and the exact tokens, so it runs
+// beside K3b's chunk workgroups (their registers and LDS leave room on every CU) instead of on the
+// finish kernel's critical path.
 //
-// One wave does it all, with no barrier: the query, the keys of the first kExactKR * 16 tokens and
-// the values of the first kExactVR * (256 / D) go out in one round (every load unconditional, with
-// clamped indices: a load under a per-element condition is a branch and a wait each).  Scores: four
-// lanes per token, 32 dimensions each, 16 tokens per round, reduced with two lane exchanges; the
-// weights go through LDS (a wave's LDS accesses run in order); values: a lane holds 4 consecutive
-// dimensions of one token slot (D / 4 lanes per token), the slots combined with lane exchanges.
-constexpr int kExactKR = 3;   // key rounds (16 tokens each) loaded in the first round
-constexpr int kExactVR = 20;  // value loads (16 bytes per lane) in the first round
+// The exact tokens are cut into kExactParts contiguous shares, each taken by one wave of its own
+// workgroup (the workgroups' loads then spread over kExactParts CUs): share `part` writes its
+// (Me, Le, ve) to ex[wg * kExactParts + part], and the finish kernel merges the shares.  A wave's
+// query, keys of its first kExactKR * 8 tokens and values of its first kExactVR * (256 / D) go
+// out in one round (every load unconditional, with clamped indices: a load under a per-element
+// condition is a branch and a wait each).  Scores: eight lanes
+// per token, 8 tokens per round; lane ks holds the key's 16-byte pieces ks, ks + 8, ..., so each
+// load of a round reads whole 128-byte lines; the dot products are reduced with three lane
+// exchanges.  The weights go through the wave's own LDS area (a wave's LDS accesses run in order);
+// values: a lane holds 4 consecutive dimensions of one token slot (D / 4 lanes per token), the
+// slots combined with lane exchanges.
+constexpr int kExactParts = 4;                        // token shares (workgroups) per output row
+constexpr int kExactShare = kMaxExact / kExactParts;  // most tokens of one share
+constexpr int kExactLds = 128 + kExactShare;          // floats: the query and the share's weights
+constexpr int kExactKR = 2;  // key rounds (8 tokens each) loaded in the first round
+constexpr int kExactKI = 4;  // key loads (16 bytes per lane) per round at D = 128 (2 at D = 64)
+constexpr int kExactVR = 8;  // value loads (16 bytes per lane) in the first round
 
-__device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
+__device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) {
   const int lane = threadIdx.x;
   if (lane >= 64) return;  // one wave
   float* q = smem;          // [128] the query row
-  float* se = q + 128;      // [kMaxExact] exact scores, then weights
+  float* se = q + 128;      // [kExactShare] this share's scores, then weights
   const int row = wg % a.R_total;
   const int b = wg / a.R_total;
   const int D = a.D;
   const int gq = a.Hq / a.Hkv;
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
-  const int e0 = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
-  const int E = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e0 : 0;
+  const int e_seq = a.batch == 1 ? a.e0_single : a.cu_exact ? a.cu_exact[b] : 0;
+  const int E_seq = a.batch == 1 ? a.e_single : a.cu_exact ? a.cu_exact[b + 1] - e_seq : 0;
+  const int per = (E_seq + kExactParts - 1) / kExactParts;
+  const int j0s = min(part * per, E_seq);  // this share: sequence-relative tokens j0s .. j0s + E - 1
+  const int E = min(per, E_seq - j0s);
+  const int e0 = e_seq + j0s;
   const long qbase = (((long)b * a.Hq + qh) * a.q_len + qi) * D;
   const uint32_t qw0 = load_query_word(a.query, qbase + min(lane, D - 1), a.query_dtype);
   const uint32_t qw1 = load_query_word(a.query, qbase + min(lane + 64, D - 1), a.query_dtype);
-  // scores: lane (kj, ks) takes dimensions ks * 32 .. +32 of token kj of each round
-  const int kj = lane >> 2, ks = lane & 3;
-  const bool kslice = ks * 32 < D;
-  const float* krow0 = a.key_exact + ((long)h * a.E_total + e0) * D + min(ks * 32, D - 32);
+  // scores: lane (kj, ks) takes dimensions 4 ks + 32 i .. +4 (i < D / 32) of token kj of each round
+  const int kj = lane >> 3, ks = lane & 7;
+  const int ni = D / 32;
+  const float* krow0 = a.key_exact + ((long)h * a.E_total + e0) * D + 4 * ks;
+  const float* mrow0 = a.mask ? a.mask + (long)qi * E_seq + j0s : nullptr;
   // values: lane (tp, dq) holds dimensions 4 dq .. 4 dq + 3 of token slot tp
   const int lpt = D / 4;  // lanes per token
   const int tpi = 64 / lpt;  // tokens per value load
   const int dq = lane % lpt, tp = lane / lpt;
   const float* vrow0 = a.value_exact + ((long)h * a.E_total + e0) * D + 4 * dq;
-  float4 k4[kExactKR][8];
+  float4 k4[kExactKR][kExactKI];
   float mv[kExactKR];
   float4 v4[kExactVR];
   if (E > 0) {
 #pragma unroll
     for (int r = 0; r < kExactKR; ++r) {
-      const float4* kr = (const float4*)(krow0 + (long)min(r * 16 + kj, E - 1) * D);
+      const float* kr = krow0 + (long)min(r * 8 + kj, E - 1) * D;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) k4[r][i] = kr[i];
-      mv[r] = a.mask ? a.mask[(long)qi * E + min(r * 16 + kj, E - 1)] : 0.0f;
+      for (int i = 0; i < kExactKI; ++i) k4[r][i] = *(const float4*)(kr + 32 * min(i, ni - 1));
+      mv[r] = mrow0 ? mrow0[min(r * 8 + kj, E - 1)] : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < kExactVR; ++i) v4[i] = *(const float4*)(vrow0 + (long)min(tp + i * tpi, E - 1) * D);
@@ -1459,29 +1472,30 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
   float ex_m = -INFINITY, ex_l = 0.0f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (E > 0) {
-    float4 qv[8];  // this lane's 32 query dimensions
+    float4 qv[kExactKI];  // this lane's query dimensions
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qv[i] = *(const float4*)(q + min(ks * 32, D - 32) + 4 * i);
-    auto score = [&](const float4 (&kk)[8], float mval, int j) {
+    for (int i = 0; i < kExactKI; ++i) qv[i] = *(const float4*)(q + 4 * ks + 32 * min(i, ni - 1));
+    auto score = [&](const float4 (&kk)[kExactKI], float mval, int j) {
       float dot = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dot += qv[i].x * kk[i].x + qv[i].y * kk[i].y + qv[i].z * kk[i].z + qv[i].w * kk[i].w;
-      dot = kslice ? dot : 0.0f;
-      dot += lane_xor1(dot);
-      dot += lane_xor2(dot);
+      for (int i = 0; i < kExactKI; ++i) {
+        const float d4 = qv[i].x * kk[i].x + qv[i].y * kk[i].y + qv[i].z * kk[i].z + qv[i].w * kk[i].w;
+        dot += i < ni ? d4 : 0.0f;
+      }
+      dot = sum8(dot);
       const float sc = dot * a.scaling + mval;
       if (ks == 0 && j < E) se[j] = sc;
       return j < E ? sc : -INFINITY;
     };
     float m = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < kExactKR; ++r) m = fmaxf(m, score(k4[r], mv[r], r * 16 + kj));
-    for (int j0 = kExactKR * 16; j0 < E; j0 += 16) {  // more than kExactKR * 16 exact tokens
-      float4 kk[8];
-      const float4* kr = (const float4*)(krow0 + (long)min(j0 + kj, E - 1) * D);
+    for (int r = 0; r < kExactKR; ++r) m = fmaxf(m, score(k4[r], mv[r], r * 8 + kj));
+    for (int j0 = kExactKR * 8; j0 < E; j0 += 8) {  // more than kExactKR * 8 tokens in the share
+      float4 kk[kExactKI];
+      const float* kr = krow0 + (long)min(j0 + kj, E - 1) * D;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) kk[i] = kr[i];
-      const float mval = a.mask ? a.mask[(long)qi * E + min(j0 + kj, E - 1)] : 0.0f;
+      for (int i = 0; i < kExactKI; ++i) kk[i] = *(const float4*)(kr + 32 * min(i, ni - 1));
+      const float mval = mrow0 ? mrow0[min(j0 + kj, E - 1)] : 0.0f;
       m = fmaxf(m, score(kk, mval, j0 + kj));
     }
     ex_m = wave_max(m);
@@ -1494,11 +1508,11 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
     }
     ex_l = wave_sum(l);
     // weighted values: every weight read is unconditional (clamped), the select drops the products
-    // of slots past the exact tokens
+    // of slots past the share's tokens
 #pragma unroll
     for (int i = 0; i < kExactVR; ++i) {
       const int t = tp + i * tpi;
-      const float w = t < E ? se[min(t, kMaxExact - 1)] : 0.0f;
+      const float w = t < E ? se[min(t, kExactShare - 1)] : 0.0f;
       acc.x += w * v4[i].x;
       acc.y += w * v4[i].y;
       acc.z += w * v4[i].z;
@@ -1507,7 +1521,7 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
     for (int t0 = kExactVR * tpi; t0 < E; t0 += tpi) {  // tokens past the first round's values
       const int t = t0 + tp;
       const float4 vv = *(const float4*)(vrow0 + (long)min(t, E - 1) * D);
-      const float w = t < E ? se[min(t, kMaxExact - 1)] : 0.0f;
+      const float w = t < E ? se[min(t, kExactShare - 1)] : 0.0f;
       acc.x += w * vv.x;
       acc.y += w * vv.y;
       acc.z += w * vv.z;
@@ -1525,7 +1539,7 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, float* smem) {
   acc.y = sum_xor32(acc.y);
   acc.z = sum_xor32(acc.z);
   acc.w = sum_xor32(acc.w);
-  float* ex = a.ex + (long)wg * (D + 2);
+  float* ex = a.ex + ((long)wg * kExactParts + part) * (D + 2);
   if (tp == 0) {  // ex + 2 + 4 dq is 8-byte aligned only
     ex[2 + 4 * dq] = acc.x;
     ex[3 + 4 * dq] = acc.y;
@@ -1569,9 +1583,15 @@ __device__ void row_merge(const RowMergeArgs& a, int wg, float* smem) {
       s4[k] = ts[t];
     }
   }
-  const float* ex = a.ex + (long)wg * (D + 2);
-  const float2 mle = *(const float2*)ex;  // (Me, Le)
-  const float ve = ex[2 + d];
+  // the exact tail's shares (row_exact): (Me, Le) and ve[d] of each
+  const float* ex = a.ex + (long)wg * kExactParts * (D + 2);
+  float2 mlp[kExactParts];
+  float vep[kExactParts];
+#pragma unroll
+  for (int p = 0; p < kExactParts; ++p) {
+    mlp[p] = *(const float2*)(ex + p * (D + 2));
+    vep[p] = ex[p * (D + 2) + 2 + d];
+  }
   // thread (d, part) sums the chunk partials part, part + parts, ... of output d
   const long rows_all = (long)a.batch * a.R_total;
   const float* cp = a.out_part + (long)wg * D + d;
@@ -1610,7 +1630,16 @@ __device__ void row_merge(const RowMergeArgs& a, int wg, float* smem) {
   if (tid < D) {
     float csum = 0.0f;
     for (int p = 0; p < parts; ++p) csum += cbuf[p * D + tid];
-    const float Mc = bc[0], Lc = bc[1], Me = mle.x, Le = mle.y;
+    float Me = -INFINITY, Le = 0.0f, ve = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kExactParts; ++p) Me = fmaxf(Me, mlp[p].x);
+#pragma unroll
+    for (int p = 0; p < kExactParts; ++p) {
+      const float f = mlp[p].x == -INFINITY ? 0.0f : __expf(mlp[p].x - Me);
+      Le += mlp[p].y * f;
+      ve += vep[p] * f;
+    }
+    const float Mc = bc[0], Lc = bc[1];
     const float M = fmaxf(Mc, Me);
     const float ec = (M == -INFINITY || Mc == -INFINITY) ? 0.0f : __expf(Mc - M);
     const float ee = (M == -INFINITY || Me == -INFINITY) ? 0.0f : __expf(Me - M);
@@ -1940,7 +1969,7 @@ struct K3bArgs {
   float* out_part;
   int batch, n_total, layer, Hkv, Hq, q_len, D, rank, R_total, nchunks;
   int split_tok;   // tokens per K3a split
-  int n_exact_wg;  // leading workgroups that compute the exact tail of one output row each (row_exact)
+  int n_exact_wg;  // leading workgroups that compute a share of one output row's exact tail each (row_exact)
 };
 
 constexpr int kK3bParts = 8;                  // component parts of a chunk
@@ -1951,9 +1980,9 @@ constexpr int kK3bDims = 64;                  // dimensions per workgroup
 template <int NR>
 __global__ __launch_bounds__(kRowThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
-  if ((int)blockIdx.x < a.n_exact_wg) {  // the exact tail of output row blockIdx.x
-    __shared__ __attribute__((aligned(16))) float xsm[128 + kMaxExact];
-    row_exact(ex, blockIdx.x, xsm);
+  if ((int)blockIdx.x < a.n_exact_wg) {  // share blockIdx.x % kExactParts of output row blockIdx.x / kExactParts
+    __shared__ __attribute__((aligned(16))) float xsm[kExactLds];
+    row_exact(ex, blockIdx.x / kExactParts, blockIdx.x % kExactParts, xsm);
     return;
   }
   __shared__ __attribute__((aligned(16))) float W[NR][kChunk];  // the pass's summed weights
@@ -2119,7 +2148,7 @@ Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   L.out_part = off;
   off += align256((size_t)L.nchunks * a->batch * L.R_total * a->head_dim * 4);
   L.exact = off;
-  off += align256((size_t)a->batch * L.R_total * (a->head_dim + 2) * 4);
+  off += align256((size_t)a->batch * L.R_total * kExactParts * (a->head_dim + 2) * 4);
   L.total = off;
   return L;
 }
@@ -2406,7 +2435,7 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.R_total = L.R_total;
   kb.nchunks = L.nchunks;
   kb.split_tok = L.split_tok;
-  kb.n_exact_wg = a->batch * L.R_total;
+  kb.n_exact_wg = a->batch * L.R_total * kExactParts;
   const long k3b_blocks = kb.n_exact_wg + (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
   if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
     hipLaunchKernelGGL(basis_apply_kernel<4>, dim3((unsigned)k3b_blocks), dim3(kRowThreads), 0, st, kb, m);

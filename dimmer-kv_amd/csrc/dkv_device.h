@@ -366,6 +366,11 @@ DKV_DEVICE float max8(float v) {
   v = fmaxf(v, lane_xor2(v));
   return fmaxf(v, lane_half_mirror(v));
 }
+DKV_DEVICE float sum8(float v) {
+  v += lane_xor1(v);
+  v += lane_xor2(v);
+  return v + lane_half_mirror(v);
+}
 DKV_DEVICE float max16(float v) { v = max8(v); return fmaxf(v, lane_mirror(v)); }
 DKV_DEVICE float sum16(float v) {
   v += lane_xor1(v);
