@@ -2508,9 +2508,11 @@ DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
   const int qh = row0 / a.q_len, qi0 = row0 % a.q_len;
   const int h = qh / gq;
   const int nkeys_max = a.E + qi0 + RPW;  // row i sees exact context tokens + question keys 0..qi0 + i
+  // lane kh of a key holds its 16-byte pieces kh, kh + KL, ...: the KL lanes of a key read one
+  // contiguous run per load instead of one cache line each
   auto key_half = [&](int j) {
     return (const float4*)(j < a.E ? a.key_exact + ((long)h * a.E + j) * D
-                                   : a.key_question + ((long)h * a.q_len + (j - a.E)) * D) + kh * U;
+                                   : a.key_question + ((long)h * a.q_len + (j - a.E)) * D) + kh;
   };
   // first round: quarter statistics (one per row and thread), query words, the first pass of keys
   float mt[RPW], st[RPW];
@@ -2540,7 +2542,7 @@ DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
   {
     const float4* kr = key_half(min(kj, nkeys_max - 1));
 #pragma unroll
-    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+    for (int u = 0; u < U; ++u) k4[u] = kr[u * KL];
   }
   __builtin_amdgcn_sched_barrier(0);
   // compressed part: the thread's quarters of each row
@@ -2581,7 +2583,7 @@ DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
         float dot = 0.0f;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const float4 q4 = *(const float4*)&q[i][kh * (D / KL) + 4 * u];
+          const float4 q4 = *(const float4*)&q[i][4 * (kh + KL * u)];
           dot += q4.x * k4[u].x + q4.y * k4[u].y + q4.z * k4[u].z + q4.w * k4[u].w;
         }
         dot += lane_xor1(dot);  // the key's KL lanes (each sum is the same in all of them)
@@ -2598,7 +2600,7 @@ DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
   for (int j0 = kStatKeys; j0 < nkeys_max; j0 += kStatKeys) {  // more exact keys than one pass holds
     const float4* kr = key_half(min(j0 + kj, nkeys_max - 1));
 #pragma unroll
-    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+    for (int u = 0; u < U; ++u) k4[u] = kr[u * KL];
     float sc[RPW];
     scores(sc);
 #pragma unroll
@@ -2624,7 +2626,7 @@ DKV_DEVICE void row_stats_rows(const RowStatsArgs& a, int wg) {
   for (int j0 = kStatKeys; j0 < nkeys_max; j0 += kStatKeys) {
     const float4* kr = key_half(min(j0 + kj, nkeys_max - 1));
 #pragma unroll
-    for (int u = 0; u < U; ++u) k4[u] = kr[u];
+    for (int u = 0; u < U; ++u) k4[u] = kr[u * KL];
     float sc[RPW];
     scores(sc);
 #pragma unroll
