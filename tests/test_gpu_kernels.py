@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import synth
-from helpers import assert_close, build_case, gpu_attend, gpu_context, oracle_attend, value_mean_base
+from helpers import assert_close, assert_sensitive, build_case, gpu_attend, gpu_context, oracle_attend, value_mean_base
 from oracle import packing_ref, progressive_ref as pr
 
 pytestmark = pytest.mark.gpu
@@ -107,6 +107,34 @@ def test_attend_matches_oracle(shape_name, tokens, layers, query_scale, q_len, q
         got = gpu_attend(case, ctx, layer)
         err, fro = assert_close(got, ref, what=f"layer {layer}", base=value_mean_base(case, layer))
         print(f"  layer {layer}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("shape_name,tokens,sinks,recent,q_len", [
+    ("3b2", 600, 0, 2, 1),      # 3 exact tokens: one per share, the fourth share empty
+    ("3b2", 900, 4, 300, 1),    # 305: every share past its first round of keys and of values
+    ("1b", 1400, 4, 1000, 1),   # 1,005 of the 1,024 allowed: 252 per share
+    ("1b", 800, 2, 200, 3),     # 205 with a causal mask across the shares
+])
+def test_attend_exact_tail_lengths(shape_name, tokens, sinks, recent, q_len):
+    """The exact tail's token shares (four per output row, merged by the finish kernel) at lengths
+    the 37-token default never reaches; with a long tail, zeroing its values must move the oracle's
+    output far past the bar, so the tail is what the check sees."""
+    shape = {"1b": synth.SHAPE_1B, "3b2": synth.ModelShape(2, 8, 128, 24, 2048)}[shape_name]
+    print(f"[case] exact tail {shape_name} T={tokens} sinks={sinks} recent={recent} q_len={q_len}", flush=True)
+    case = build_case(shape, tokens, seed=4321, query_scale=20.0, q_len=q_len, sinks=sinks, recent=recent)
+    ctx, _, _ = gpu_context(case)
+    layer = shape.layers - 1
+    ref = oracle_attend(case, layer)
+    got = gpu_attend(case, ctx, layer)
+    base = value_mean_base(case, layer)
+    err, fro = assert_close(got, ref, what=f"exact tail E={case.key_exact.shape[2]}", base=base)
+    print(f"  E={case.key_exact.shape[2]}: max abs err {err:.2e}, rel fro {fro:.2e}", flush=True)
+    if recent >= 100:
+        from dataclasses import replace
+
+        zeroed = oracle_attend(replace(case, value_exact=torch.zeros_like(case.value_exact)), layer)
+        gap = assert_sensitive(ref, zeroed, base, what="exact values zeroed")
+        print(f"  zeroed exact values move the output by {gap:.2e} (relative)", flush=True)
 
 
 def test_attend_special_cases():
