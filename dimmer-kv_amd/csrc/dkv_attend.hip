@@ -1356,20 +1356,22 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
     for (int w = 0; w < NW; ++w) M = fmaxf(M, r == 0 ? wm[w].x : r == 1 ? wm[w].y : r == 2 ? wm[w].z : wm[w].w);
     Mt[r] = M;
   }
-  if (tid < RH) {
-    const int r = tid;
+  // the tile's sum of exponentials per row, in wave 0: lane (w, r) = (lane / 4 % 8, lane % 4) scales
+  // wave w's sum of row r to the tile maximum, and three lane exchanges add the eight waves
+  if (wave == 0) {
+    static_assert(NW == 8, "eight waves: lanes 4 w + r, w < 8");
+    const int w = (lane >> 2) & 7, r = lane & 3;
     const float M = r == 0 ? Mt[0] : r == 1 ? Mt[1] : r == 2 ? Mt[2] : Mt[3];
-    float S = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float mw = stat_m[w][r];
-        if (mw != -INFINITY) S += stat_s[w][r] * __expf(mw - M);
-      }
+    const float mw = stat_m[w][r];
+    float S = (M == -INFINITY || mw == -INFINITY) ? 0.0f : stat_s[w][r] * __expf(mw - M);
+    S += __shfl_xor(S, 4);
+    S += __shfl_xor(S, 8);
+    S += __shfl_xor(S, 16);
+    if (lane < RH) {
+      const long o = (long)(h * RH + lane) * a.ntiles + tile;
+      a.tile_max[o] = M;
+      a.tile_sum[o] = S;
     }
-    const long o = (long)(h * RH + r) * a.ntiles + tile;
-    a.tile_max[o] = M;
-    a.tile_sum[o] = S;
   }
   // probabilities relative to the tile maximum, fp16; every slot of the tile is written (0 past
   // the tile's tokens); the two lanes of a token write alternate rows
