@@ -424,7 +424,41 @@ DKV_DEVICE void stage_rope_rows(const K2Args& a, float* cs, float* sn, const int
   __syncthreads();
 }
 
-template <int D, bool ROWMAJOR>
+// One RoPE table (cos or sin, [rope_rows][D/2] floats) of the tile's 256 tokens straight into LDS
+// (global_load_lds: no registers), unpadded and swizzled: token n's 16-byte piece c sits at piece
+// n * NC + (c ^ (n % NC)) of dst (NC = D/8 pieces per token), which keeps the epilogue's reads of a
+// piece across 32 consecutive tokens on distinct banks.  Each wave instruction fills 64 consecutive
+// pieces (1 KB); lane l takes piece S0 + l and loads whichever source piece the swizzle puts
+// there.  Positions come from pos_s (past the tile's tokens, its last token's, so every row is a
+// real table row).  The caller waits for the loads (vmcnt) and synchronises before reading.
+template <int D>
+DKV_DEVICE void dma_rope_table(const float* __restrict__ table, const int* pos_s, float* dst) {
+  constexpr int HALF_D = D / 2;
+  constexpr int NC = HALF_D / 4;                       // 16-byte pieces per token
+  constexpr int PER_WAVE = kTileTok * NC / 64 / (kK2Threads / 64);  // instructions per wave
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int S0 = (wave * PER_WAVE + i) * 64;
+    const int sl = S0 + lane;
+    const int n = sl / NC, c = (sl % NC) ^ (n % NC);
+    __builtin_amdgcn_global_load_lds(table + (long)pos_s[n] * HALF_D + 4 * c, dst + 4 * S0, 16, 0, 0);
+  }
+}
+
+// The swizzled piece of dma_rope_table holding floats 4c .. 4c + 3 of token n.
+template <int D>
+DKV_DEVICE int rope_piece(int n, int c) {
+  constexpr int NC = D / 8;
+  return n * NC + (c ^ (n % NC));
+}
+
+// DMA (decoding): the cos rows were loaded into LDS at byte offset kDmaCosOffset during the main
+// loop's last groups (dma_rope_table); the sin rows go to offset 0 here, and the reads follow the
+// swizzled layout.  Otherwise both are staged by stage_rope_rows.
+constexpr int kDmaCosOffset = 2 * kTileTok * kStride * 2;  // bytes: past the two basis blocks
+
+template <int D, bool ROWMAJOR, bool DMA = false>
 DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4], half_t* lds_h,
                                            float (*stat_m)[4][32], float (*stat_s)[4][32], int tok0, int count,
                                            int tile, int h0, int b, int RH, const int* pos_s, const float* qs) {
@@ -433,14 +467,20 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
   constexpr int HALF_BLK = DB / 2;
   constexpr int HALF_D = D / 2;
   constexpr int CSTR = HALF_D + 4;  // floats per staged RoPE row (keeps b128 reads conflict-free)
-  float* cs = (float*)lds_h;                 // [256][CSTR] cos
-  float* sn = cs + kTileTok * CSTR;          // [256][CSTR] sin
+  float* cs = DMA ? (float*)((char*)lds_h + kDmaCosOffset) : (float*)lds_h;  // cos: [256][CSTR] or swizzled
+  float* sn = DMA ? (float*)lds_h : cs + kTileTok * CSTR;                    // sin
   // pos_s (the tile's positions) and qs ([HPW][kSmallRows][D] query rows) were staged at kernel start
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tq = wave & 3, hs = wave >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  stage_rope_rows<D>(a, cs, sn, pos_s, count);
+  if constexpr (DMA) {
+    dma_rope_table<D>(a.rope_sin, pos_s, sn);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's table loads (cos and sin) have landed
+    __syncthreads();
+  } else {
+    stage_rope_rows<D>(a, cs, sn, pos_s, count);
+  }
 
   // part[hw][r][tb]: partial q . k over this lane's dimensions, head hw of the wave
   constexpr int HPWAVE = HPW / 2;
@@ -469,8 +509,9 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
 #pragma unroll
       for (int tb = 0; tb < 2; ++tb) {
         const int n = tq * 64 + tb * 32 + l32;
-        const float4 c4 = *(const float4*)(cs + n * CSTR + j);
-        const float4 s4 = *(const float4*)(sn + n * CSTR + j);
+        const int o = DMA ? 4 * rope_piece<D>(n, j / 4) : n * CSTR + j;
+        const float4 c4 = *(const float4*)(cs + o);
+        const float4 s4 = *(const float4*)(sn + o);
         const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
         const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
         float rlo[4], rhi[4];
@@ -744,6 +785,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   DKV_K2_FINISH(1);
+  // decoding: the tile's cos rows go straight to LDS past the basis blocks while the last MFMAs run
+  if constexpr (SMALL && !ROWMAJOR) dma_rope_table<D>(a.rope_cos, pos_s, (float*)((char*)lds + kDmaCosOffset));
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_setprio(1);
@@ -762,7 +805,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 
   const int gq = a.Hq / a.Hkv;
   if constexpr (SMALL) {
-    keys_scores_small_epilogue<D, ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH, pos_s, q_s);
+    keys_scores_small_epilogue<D, ROWMAJOR, !ROWMAJOR>(a, acc, lds, stat_m, stat_s, tok0, count, tile, h0, b, RH,
+                                                       pos_s, q_s);
     return;
   } else {
 
