@@ -785,8 +785,9 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   DKV_K2_FINISH(1);
-  // decoding: the tile's cos rows go straight to LDS past the basis blocks while the last MFMAs run
-  if constexpr (SMALL && !ROWMAJOR) dma_rope_table<D>(a.rope_cos, pos_s, (float*)((char*)lds + kDmaCosOffset));
+  // the tile's cos rows go straight to LDS past the basis blocks while the last MFMAs run (every
+  // epilogue but the few-row scoring one, which stages its rows itself)
+  if constexpr (!(SMALL && ROWMAJOR)) dma_rope_table<D>(a.rope_cos, pos_s, (float*)((char*)lds + kDmaCosOffset));
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_setprio(1);
@@ -811,7 +812,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   } else {
 
   // ---- epilogue 1 (many query rows): RoPE in registers, straight into MFMA key fragments.  The
-  // tile's cos / sin rows are staged in LDS with coalesced loads; each lane rotates the
+  // tile's cos / sin rows are in LDS (dma_rope_table: cos during the last groups, sin here); each lane rotates the
   // (d, d + D/2) pairs it holds in fp32 and rounds them to fp16.  Lane (l32, lhi) then holds, for
   // its token, 4 of the 8 dimensions of every 8-dimension chunk c (offset 4 lhi); the key fragment
   // of k-step ks needs chunk 2 ks + lhi whole, which one permlane32 swap per dword of the chunk pair
@@ -819,12 +820,13 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // 32-63 keep their chunk 2 ks + 1 half and get lanes 0-31's.
   constexpr int HPWAVE = HPW / 2;  // heads handled by each wave in the epilogue
   constexpr int KS = D / 16;       // MFMA k-steps over the head dimension
-  constexpr int CSTR = D / 2 + 4;  // staged RoPE row stride (floats), as stage_rope_rows lays it out
   half8 kf[HPWAVE][KS][2];
   {
-    float* cs = (float*)lds;
-    float* sn = cs + kTileTok * CSTR;
-    stage_rope_rows<D>(a, cs, sn, pos_s, count);
+    const float* cs = (const float*)((const char*)lds + kDmaCosOffset);
+    float* sn = (float*)lds;
+    dma_rope_table<D>(a.rope_sin, pos_s, sn);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's table loads (cos and sin) have landed
+    __syncthreads();
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
       const int n = tq * 64 + tb * 32 + l32;
@@ -837,8 +839,9 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
 #pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) {
           const int d0 = (rb % DB) * 32 + 8 * v4 + 4 * lhi;
-          const float4 c4 = *(const float4*)(cs + n * CSTR + d0);
-          const float4 s4 = *(const float4*)(sn + n * CSTR + d0);
+          const int o = 4 * rope_piece<D>(n, d0 / 4);
+          const float4 c4 = *(const float4*)(cs + o);
+          const float4 s4 = *(const float4*)(sn + o);
           const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
           const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
           uint32_t lo[2], hi[2];
