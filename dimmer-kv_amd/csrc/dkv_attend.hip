@@ -651,18 +651,42 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const int RH = (a.Hq / a.Hkv) * a.q_len;
 
-  // the epilogue's positions (clamped into the RoPE tables; past the tile's end, its last token's)
-  // and the decode epilogue's query rows are fetched now, behind the main loop
-  if (tid < kTileTok) pos_s[tid] = min(max(a.positions[tok0 + min(tid, count - 1)], 0), a.rope_rows - 1);
+  // First round, ahead of the main loop's loads: the epilogue's positions (clamped into the RoPE
+  // tables; past the tile's end, its last token's) and the decode epilogue's query rows, as raw bits
+  // from unconditional loads (rows past RH read row RH - 1 and are written as 0).  They reach LDS once
+  // the main loop's first loads are out: storing each as it arrives, or converting under a type
+  // switch, made every later load wait for it.
+  const int pos_raw = a.positions[tok0 + min(tid % kTileTok, count - 1)];
+  constexpr int QE = SMALL ? HPW * kSmallRows * D / kK2Threads : 1;  // query elements per thread
+  static_assert(!SMALL || QE * kK2Threads == HPW * kSmallRows * D, "whole rounds of query elements");
+  const bool q32 = a.query_dtype == DKV_F32;
+  uint32_t qlo_bits[QE], qhi_bits[QE];
   if constexpr (SMALL) {
     const int gq = a.Hq / a.Hkv;
-    for (int e = tid; e < HPW * RH * D; e += kK2Threads) {
-      const int hl = e / (RH * D), r = (e / D) % RH, d = e % D;
+#pragma unroll
+    for (int i = 0; i < QE; ++i) {
+      const int e = tid + i * kK2Threads;
+      const int hl = e / (kSmallRows * D), r = min((e / D) % kSmallRows, RH - 1), d = e % D;
       const int qh = (h0 + hl) * gq + r / a.q_len, qi = r % a.q_len;
-      q_s[(hl * kSmallRows + r) * D + d] = load_as_float(a.query, (((long)b * a.Hq + qh) * a.q_len + qi) * D + d,
-                                                         a.query_dtype);
+      const long idx = (((long)b * a.Hq + qh) * a.q_len + qi) * D + d;
+      const uint16_t* qp = (const uint16_t*)a.query + (q32 ? 2 * idx : idx);
+      qlo_bits[i] = qp[0];
+      qhi_bits[i] = qp[q32 ? 1 : 0];
     }
   }
+  auto write_first_round = [&]() {
+    if (tid < kTileTok) pos_s[tid] = min(max(pos_raw, 0), a.rope_rows - 1);
+    if constexpr (SMALL) {
+#pragma unroll
+      for (int i = 0; i < QE; ++i) {
+        const int e = tid + i * kK2Threads;
+        const float qv = q32 ? __uint_as_float(qlo_bits[i] | qhi_bits[i] << 16)
+                             : a.query_dtype == DKV_F16 ? half_bits_to_float((uint16_t)qlo_bits[i])
+                                                        : bf16_bits_to_float((uint16_t)qlo_bits[i]);
+        q_s[e] = (e / D) % kSmallRows < RH ? qv : 0.0f;
+      }
+    }
+  };
 
   // Coefficient operands come straight from the decoded buffer (one 16-byte
   // load per lane per MFMA operand); the basis block [256][64] goes global ->
@@ -745,11 +769,20 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
   // wave of a SIMD runs MFMAs while the other does its memory work.
   // sched_barrier keeps the compiler from moving loads into the MFMA
   // segments; a wave in its MFMA segment runs at raised priority.
-  DKV_K2_ISSUE_A(0, af0);
+  // prologue: group 0's basis first (the LDS store waits for it alone), its coefficient operands in
+  // k-step order (the first MFMAs wait for the first two), group 1's operands, then group 1's basis
+  // (its registers are free once group 0's block is stored)
   DKV_K2_ISSUE_B(0);
+  {
+    const half8* src_ = coef_frag;
+    af0[0] = src_[0 * 64]; af0[4] = src_[4 * 64]; af0[1] = src_[1 * 64]; af0[5] = src_[5 * 64];
+    af0[2] = src_[2 * 64]; af0[6] = src_[6 * 64]; af0[3] = src_[3 * 64]; af0[7] = src_[7 * 64];
+  }
+  DKV_K2_ISSUE_A(1, af1);
+  __builtin_amdgcn_sched_barrier(0);
+  write_first_round();
   DKV_K2_FINISH(0);
   DKV_K2_ISSUE_B(1);
-  DKV_K2_ISSUE_A(1, af1);
   __syncthreads();
   if (hs == 1) __builtin_amdgcn_s_barrier();
   // G is even (the rank is a multiple of 256).  The last two groups run
