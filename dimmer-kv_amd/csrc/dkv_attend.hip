@@ -69,7 +69,8 @@ struct RowMergeArgs {
   float* ex;              // [batch * R_total][kExactParts][D + 2] per row and share: Me, Le, then ve[D] (row_exact)
   void* out;              // [batch][q_len][Hq][D], out_dtype
   float scaling;
-  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, ntiles, nchunks, out_dtype;
+  // nstats: softmax-statistics entries per row (ntiles, or 2 * ntiles for 128-token entries)
+  int batch, n_total, layer, Hkv, Hq, q_len, D, R_total, E_total, query_dtype, nstats, nchunks, out_dtype;
   int e0_single, e_single;  // with one sequence: its first exact token and exact-token count
 };
 
@@ -91,6 +92,7 @@ struct K2Args {
   // question scoring: (max, sum exp) of every row over each 64-token quarter of a tile, [R][ntiles * 4]
   float* sub_max;
   float* sub_sum;
+  int nstats;  // softmax-statistics entries per row: ntiles, or 2 * ntiles with 128-token entries
 };
 
 DKV_DEVICE uint16_t f16_bits(float v) {
@@ -589,7 +591,7 @@ DKV_DEVICE void keys_scores_small_epilogue(const K2Args& a, floatx16 (&acc)[2][4
           if (mq != -INFINITY) S += stat_s[hl][q][r] * __expf(mq - M);
         }
       }
-      const long o = (long)((h0 + hl) * RH + r) * a.ntiles + tile;
+      const long o = (long)((h0 + hl) * RH + r) * a.nstats + tile;
       a.tile_max[o] = M;
       a.tile_sum[o] = S;
     }
@@ -1143,7 +1145,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_kernel(K2Args a) {
               if (mq != -INFINITY) S += stat_s[hl][q][rr] * __expf(mq - M);
             }
           }
-          const long o = (long)((h0 + hl) * RH + row) * a.ntiles + tile;
+          const long o = (long)((h0 + hl) * RH + row) * a.nstats + tile;
           a.tile_max[o] = M;
           a.tile_sum[o] = S;
         }
@@ -1217,17 +1219,23 @@ DKV_DEVICE void static_for(Fn&& f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-template <int D>
-__global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) {
+// NW waves of 32 tokens: the whole tile (8), or half of it (4) when short contexts leave CUs idle
+// even with one workgroup per (tile, head); the softmax statistics then cover the workgroup's 128
+// tokens (entry 2 * tile + half).
+template <int D, int NW>
+__global__ __launch_bounds__(NW * 64) void keys_scores_head_kernel(K2Args a) {
+  constexpr int NT = NW * 64;       // threads
+  constexpr int TT = NW * 32;       // tokens of the workgroup
+  constexpr int PARTS = kTileTok / TT;
   constexpr int DB = D / 32;        // 32-row blocks of the head
   constexpr int HALF_BLK = DB / 2;  // RoPE partner offset in blocks
   constexpr int HALF_D = D / 2;
-  constexpr int BQ = D / 64;        // basis loads per thread and group: [D][64] fp16 = D * 8 x 16 B
+  constexpr int BQ = D * 8 / NT;    // basis loads per thread and group: [D][64] fp16 = D * 8 x 16 B
   constexpr int RING = 4;           // groups whose loads are in flight
-  constexpr int NW = kK2Threads / 64;
   constexpr int BLK = D * kStride;  // halves per LDS basis block
-  static_assert(NW * 32 == kTileTok, "one 32-token block per wave");
-  static_assert(kSmallRows * D <= kK2Threads, "one query element per thread");
+  constexpr int QE = (kSmallRows * D + NT - 1) / NT;  // query elements per thread
+  static_assert(NW == 8 || NW == 4, "a tile or half of it");
+  static_assert(BQ * NT == D * 8, "whole rounds of basis loads");
   __shared__ __attribute__((aligned(16))) half_t lds[2 * BLK];  // two basis blocks
   __shared__ __attribute__((aligned(16))) float stat_m[NW][kSmallRows];
   __shared__ __attribute__((aligned(16))) float stat_s[NW][kSmallRows];
@@ -1235,7 +1243,8 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
 
   const int lin = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (lin >= a.total_wg) return;
-  const int tile = lin / a.Hkv, h = lin % a.Hkv;
+  const int tp = lin / a.Hkv, h = lin % a.Hkv;  // tp = PARTS * tile + part: the statistics entry
+  const int tile = tp / PARTS, part = tp % PARTS;
   const int2 bt = find_tile(a.cu_seqlens, a.batch, a.n_total, kTileTok, tile);
   const int b = bt.x;
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
@@ -1246,22 +1255,26 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
   const int l32 = lane & 31, lhi = lane >> 5;
   const int gq = a.Hq / a.Hkv;
   const int RH = gq * a.q_len;
-  const int n = wave * 32 + l32;  // the lane's token in the tile
+  const int n = part * TT + wave * 32 + l32;  // the lane's token in the tile
 
   // First round, before the main loop's loads: the lane's position (clamped into the RoPE tables;
   // past the tile's end, its last token's), one query element per thread and the key mean rows.
   // Their LDS copies are written once the main loop's first loads are out.
   const int pos = min(max(a.positions[tok0 + min(n, count - 1)], 0), a.rope_rows - 1);
-  const int qr = tid / D, qd = tid % D;
-  const bool q_ok = qr < RH;
-  const int qrc = min(qr, RH - 1);
-  // the query element as raw bits from two unconditional 16-bit loads (a float's halves, or the same
-  // 16-bit element twice), converted after the main loop's loads are out: loads under a type switch
-  // made the conversion wait for the value before anything else was issued
-  const long qi = (((long)b * a.Hq + h * gq + qrc / a.q_len) * a.q_len + qrc % a.q_len) * D + qd;
+  // the query elements as raw bits from two unconditional 16-bit loads each (a float's halves, or the
+  // same 16-bit element twice), converted after the main loop's loads are out: loads under a type
+  // switch made the conversion wait for the value before anything else was issued
   const bool q32 = a.query_dtype == DKV_F32;
-  const uint16_t* qp = (const uint16_t*)a.query + (q32 ? 2 * qi : qi);
-  const uint32_t qlo_bits = qp[0], qhi_bits = qp[q32 ? 1 : 0];
+  uint32_t qlo_bits[QE], qhi_bits[QE];
+#pragma unroll
+  for (int i = 0; i < QE; ++i) {
+    const int e = min(tid + i * NT, kSmallRows * D - 1);
+    const int qrc = min(e / D, RH - 1), qd = e % D;
+    const long qi = (((long)b * a.Hq + h * gq + qrc / a.q_len) * a.q_len + qrc % a.q_len) * D + qd;
+    const uint16_t* qp = (const uint16_t*)a.query + (q32 ? 2 * qi : qi);
+    qlo_bits[i] = qp[0];
+    qhi_bits[i] = qp[q32 ? 1 : 0];
+  }
   // acc[rb][v]: basis row rb * 32 + 8 (v / 4) + 4 lhi + (v & 3) of the lane's token, from the key mean
   const float* mean_rows = a.mean_k + ((long)a.layer * a.Hkv + h) * D + 4 * lhi;
   floatx16 acc[DB];
@@ -1276,7 +1289,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
       acc[rb][4 * v4 + 3] = m4.w;
     }
 
-  const half8* coef_frag = (const half8*)a.coef + ((long)(tile * 8 + wave) * 4) * 64 + lane;
+  const half8* coef_frag = (const half8*)a.coef + ((long)(tile * 8 + part * NW + wave) * 4) * 64 + lane;
   const long coef_group_stride = (long)(a.n_slots / 32) * 4 * 64;  // in half8 units
   const uint4* basis_head =
       (const uint4*)(a.key_basis + (long)a.layer * G * a.Hkv * D * 64 + (long)h * D * 64) + tid;
@@ -1299,7 +1312,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
     BasisVec v;
 #pragma unroll
     for (int i = 0; i < BQ; ++i) {
-      const uint4 t = basis_head[(long)g * basis_group_stride + i * kK2Threads];
+      const uint4 t = basis_head[(long)g * basis_group_stride + i * NT];
       v[4 * i] = t.x;
       v[4 * i + 1] = t.y;
       v[4 * i + 2] = t.z;
@@ -1318,7 +1331,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
     const BasisVec v = bq_slot(slot);
 #pragma unroll
     for (int i = 0; i < BQ; ++i) {
-      const int e = tid + i * kK2Threads;
+      const int e = tid + i * NT;
       *(uint4*)(Bt + (e >> 3) * kStride + (e & 7) * 8) = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
     }
   };
@@ -1337,11 +1350,13 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
       }
   };
   auto write_query = [&]() {
-    if (tid < kSmallRows * D) {
-      const float qv = q32 ? __uint_as_float(qlo_bits | qhi_bits << 16)
-                           : a.query_dtype == DKV_F16 ? half_bits_to_float((uint16_t)qlo_bits)
-                                                      : bf16_bits_to_float((uint16_t)qlo_bits);
-      q_s[tid] = q_ok ? qv : 0.0f;
+#pragma unroll
+    for (int i = 0; i < QE; ++i) {
+      const int e = tid + i * NT;
+      const float qv = q32 ? __uint_as_float(qlo_bits[i] | qhi_bits[i] << 16)
+                           : a.query_dtype == DKV_F16 ? half_bits_to_float((uint16_t)qlo_bits[i])
+                                                      : bf16_bits_to_float((uint16_t)qlo_bits[i]);
+      if (e < kSmallRows * D) q_s[e] = e / D < RH ? qv : 0.0f;
     }
   };
   using T = std::true_type;
@@ -1414,7 +1429,7 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
     const float full = sum_xor32(part);  // the lane's and its partner's dimension halves
     xs[r] = n < count ? full * a.scaling : -INFINITY;
   }
-  // each wave's (max, sum exp) over its 32 tokens, then the tile's over the 8 waves
+  // each wave's (max, sum exp) over its 32 tokens, then the workgroup's over its NW waves
 #pragma unroll
   for (int r = 0; r < kSmallRows; ++r) mx[r] = max32(xs[r]);
 #pragma unroll
@@ -1436,25 +1451,23 @@ __global__ __launch_bounds__(kK2Threads) void keys_scores_head_kernel(K2Args a) 
     for (int w = 0; w < NW; ++w) M = fmaxf(M, r == 0 ? wm[w].x : r == 1 ? wm[w].y : r == 2 ? wm[w].z : wm[w].w);
     Mt[r] = M;
   }
-  // the tile's sum of exponentials per row, in wave 0: lane (w, r) = (lane / 4 % 8, lane % 4) scales
-  // wave w's sum of row r to the tile maximum, and three lane exchanges add the eight waves
+  // the workgroup's sum of exponentials per row, in wave 0: lane (w, r) = (lane / 4 % NW, lane % 4)
+  // scales wave w's sum of row r to the maximum, and lane exchanges add the NW waves
   if (wave == 0) {
-    static_assert(NW == 8, "eight waves: lanes 4 w + r, w < 8");
-    const int w = (lane >> 2) & 7, r = lane & 3;
+    const int w = (lane >> 2) % NW, r = lane & 3;
     const float M = r == 0 ? Mt[0] : r == 1 ? Mt[1] : r == 2 ? Mt[2] : Mt[3];
     const float mw = stat_m[w][r];
     float S = (M == -INFINITY || mw == -INFINITY) ? 0.0f : stat_s[w][r] * __expf(mw - M);
-    S += __shfl_xor(S, 4);
-    S += __shfl_xor(S, 8);
-    S += __shfl_xor(S, 16);
+#pragma unroll
+    for (int m = 4; m < 4 * NW; m <<= 1) S += __shfl_xor(S, m);
     if (lane < RH) {
-      const long o = (long)(h * RH + lane) * a.ntiles + tile;
+      const long o = (long)(h * RH + lane) * a.nstats + tp;
       a.tile_max[o] = M;
       a.tile_sum[o] = S;
     }
   }
-  // probabilities relative to the tile maximum, fp16; every slot of the tile is written (0 past
-  // the tile's tokens); the two lanes of a token write alternate rows
+  // probabilities relative to the workgroup's maximum, fp16; every slot of its tokens is written (0
+  // past the tile's tokens); the two lanes of a token write alternate rows
 #pragma unroll
   for (int r = 0; r < kSmallRows; ++r) {
     if (r >= RH) break;
@@ -1639,7 +1652,8 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) 
 //   out = (e_c * (sum of the chunk partials) + e_c * L_c * mean_v + e_e * ve) / (e_c * L_c + e_e * L_e),
 //   e_c = exp(M_c - M), e_e = exp(M_e - M), M = max(M_c, M_e).
 // All its loads (tile statistics, the exact results, the chunk partials, the mean) go out in one round.
-template <int NT>
+// PER_TILE: softmax-statistics entries per tile (1, or 2 for 128-token entries).
+template <int NT, int PER_TILE>
 __device__ void row_merge(const RowMergeArgs& a, int wg, float* smem) {
   float* bc = smem;      // [2] the compressed part's (max, sum)
   float* cbuf = bc + 2;  // [NT] per-thread chunk-partial sums
@@ -1651,11 +1665,13 @@ __device__ void row_merge(const RowMergeArgs& a, int wg, float* smem) {
   const int qh = row / a.q_len, qi = row % a.q_len;
   const int h = qh / gq;
   const int d = tid % D, part = tid / D, parts = NT / D;
-  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
+  // the sequence's statistics entries: PER_TILE per tile (an entry past its tokens holds (-inf, 0))
+  constexpr int per_tile = PER_TILE;
+  const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok) * per_tile;
   const int2 sr = seq_range(a.cu_seqlens, a.batch, a.n_total, b);
-  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
-  const float* tm = ntb > 0 ? a.tile_max + (long)row * a.ntiles + tb0 : a.mean_v;
-  const float* ts = ntb > 0 ? a.tile_sum + (long)row * a.ntiles + tb0 : a.mean_v;
+  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok * per_tile;
+  const float* tm = ntb > 0 ? a.tile_max + (long)row * a.nstats + tb0 : a.mean_v;
+  const float* ts = ntb > 0 ? a.tile_sum + (long)row * a.nstats + tb0 : a.mean_v;
   float m4[4], s4[4];
   if (wave == 0) {
 #pragma unroll
@@ -1739,7 +1755,8 @@ struct K3aArgs {
   const uint16_t* probs;  // fp16 exp(score - tile max), [n_slots/16][R][16] (prob_index)
   const float* tile_max;
   float* w_part;
-  int batch, R_total, n_total, n_slots, ntiles, G, rank, nsplits, row_blocks;
+  // nstats: softmax-statistics entries per row (ntiles, or 2 * ntiles for 128-token entries)
+  int batch, R_total, n_total, n_slots, nstats, G, rank, nsplits, row_blocks;
   int total_wg, per_xcd;  // workgroups, and consecutive workgroup indices per XCD
 };
 
@@ -1864,7 +1881,8 @@ DKV_DEVICE half8 codes_to_half8(uint32_t lo, uint32_t hi) {
 // ---------------------------------------------------------------------------
 // WAVES waves of 128 tokens: a split of 1024 tokens (8 waves) or, when 1024-token splits would leave
 // CUs idle (small contexts), 512 (4 waves: twice the workgroups, each with half the loads).
-template <int WAVES>
+// PER_TILE: softmax-statistics entries per tile (1, or 2 for 128-token entries).
+template <int WAVES, int PER_TILE>
 __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
   constexpr int SPLIT = WAVES * kK3WaveTok;
   __shared__ float red[WAVES][32][65];
@@ -1893,6 +1911,8 @@ __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const int tb0 = tiles_before(a.cu_seqlens, b, kTileTok);
   const long slot0 = (long)(tb0 + bs.y * (SPLIT / kTileTok)) * kTileTok;  // first slot of the split
+  constexpr int per_tile = PER_TILE;
+  const int sb0 = tb0 * per_tile;              // the sequence's first statistics entry
   const int wt0 = wave * kK3WaveTok;  // first token of this wave, relative to tok0
   const int my_row = rbk * 32 + l32;
   const bool row_ok = my_row < a.R_total;
@@ -1902,16 +1922,17 @@ __global__ __launch_bounds__(WAVES * 64) void value_weights_kernel(K3aArgs a) {
   // the bulk is in flight), this wave's tile maximum, then the affine pairs of its 128 tokens
   // (one 16-byte load per lane, staged in LDS for the broadcast reads), its probability rows and
   // value codes for all 8 steps.
-  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok;
+  const int ntb = (sr.y - sr.x + kTileTok - 1) / kTileTok * per_tile;  // the sequence's entries
   const int mrow = rbk * 32 + ((tid >> 3) & 31), msub = tid & 7;  // 8 lanes per row (waves 4-7 repeat 0-3)
   static_assert(WAVES >= 4, "the row maxima take 256 threads");
-  const float* tmrow = a.tile_max + (long)min(mrow, a.R_total - 1) * a.ntiles + tb0;
+  const float* tmrow = a.tile_max + (long)min(mrow, a.R_total - 1) * a.nstats + sb0;
   float tmv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) tmv[i] = tmrow[min(msub + 8 * i, ntb - 1)];
-  // this wave's 128 tokens lie in one tile; its maximum for this lane's row
-  const int tile = tb0 + bs.y * (SPLIT / kTileTok) + wt0 / kTileTok;
-  const float mt_raw = a.tile_max[(long)min(my_row, a.R_total - 1) * a.ntiles + tile];
+  // this wave's 128 tokens lie in one statistics entry; its maximum for this lane's row (a wave
+  // past the sequence's tokens reads a clamped entry and discards it)
+  const int tile = min(sb0 + (bs.y * SPLIT + wt0) / (kTileTok / PER_TILE), a.nstats - 1);
+  const float mt_raw = a.tile_max[(long)min(my_row, a.R_total - 1) * a.nstats + tile];
   const float2* aff = a.vaff + (long)g * a.n_slots + slot0;
   const float4 aff2 = *(const float4*)(aff + wt0 + 2 * lane);
   // step st covers slots slot0 + wt0 + 16 st .. +16 (one 16-slot block): the wave's probability
@@ -2160,9 +2181,10 @@ void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
   }
 }
 
+template <int PER_TILE>
 __global__ __launch_bounds__(kRowThreads) void finish_kernel(RowMergeArgs a) {
   __shared__ float smem[2 + kRowThreads];
-  row_merge<kRowThreads>(a, blockIdx.x, smem);
+  row_merge<kRowThreads, PER_TILE>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -2170,6 +2192,7 @@ __global__ __launch_bounds__(kRowThreads) void finish_kernel(RowMergeArgs a) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int ntiles, nsplits, split_tok, R_total, nchunks, n_total, n_slots;
+  int stat_tok, nstats;  // tokens per softmax-statistics entry (256, or 128 with K2's half-tile workgroups), entries per row
   size_t coef, vcodes, vaff, probs, tile_max, tile_sum, w_part, out_part, exact, total;
 };
 
@@ -2185,6 +2208,13 @@ inline bool k2_head_form(const dkv_attend_args_t* a, int ntiles) {
   if (a->rank % 256 != 0) return false;  // whole rings of four groups
   const long wg = (long)ntiles * (a->kv_heads / (256 / a->head_dim));
   return wg < kCUs;
+}
+
+// Tokens per one-head K2 workgroup: half a tile (four waves) when twice the workgroups still fit one
+// wave of the CUs (short contexts: each workgroup's main loop is then half as long), else a tile.
+// The softmax statistics follow: one entry per workgroup's tokens.
+inline int k2_head_tokens(const dkv_attend_args_t* a, int ntiles) {
+  return k2_head_form(a, ntiles) && 2L * ntiles * a->kv_heads <= kCUs ? kTileTok / 2 : kTileTok;
 }
 
 // Workspace: [decoded key coefficients][decoded value codes][value affine][probabilities][tile statistics]
@@ -2212,6 +2242,8 @@ Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   L.n_total = a->cu_seqlens_host[a->batch];
   L.n_slots = L.ntiles * kTileTok + kSplitTok;
   L.nchunks = a->rank / kChunk;
+  L.stat_tok = k2_head_tokens(a, L.ntiles);
+  L.nstats = L.ntiles * (kTileTok / L.stat_tok);
   size_t off = 0;
   L.coef = off;
   off += align256((size_t)L.n_slots * a->rank * 2);
@@ -2222,9 +2254,9 @@ Layout make_layout(const dkv_attend_args_t* a, bool values = true) {
   L.probs = off;
   off += align256((size_t)L.R_total * L.n_slots * 2);
   L.tile_max = off;
-  off += align256((size_t)L.R_total * L.ntiles * 4);
+  off += align256((size_t)L.R_total * L.nstats * 4);
   L.tile_sum = off;
-  off += align256((size_t)L.R_total * L.ntiles * 4);
+  off += align256((size_t)L.R_total * L.nstats * 4);
   L.w_part = off;
   off += align256((size_t)L.nsplits * L.R_total * a->rank * 4);
   L.out_part = off;
@@ -2269,7 +2301,7 @@ RowMergeArgs row_merge_args(const dkv_attend_args_t* a, const Layout& L, char* w
   m.cu_exact = a->cu_exact;
   m.tile_max = (const float*)(ws + L.tile_max);
   m.tile_sum = (const float*)(ws + L.tile_sum);
-  m.ntiles = L.ntiles;
+  m.nstats = L.nstats;
   m.mean_v = a->mean_v;
   m.key_exact = a->key_exact;
   m.value_exact = a->value_exact;
@@ -2343,6 +2375,7 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   k.G = dkv::stream_groups(a->key);
   k.n_total = L.n_total;
   k.ntiles = L.ntiles;
+  k.nstats = L.nstats;
   k.query_dtype = a->query_dtype;
   const int HPW = 256 / a->head_dim;
   k.total_wg = L.ntiles * (a->kv_heads / HPW);
@@ -2352,13 +2385,18 @@ int launch_keys_scores(const dkv_attend_args_t* a, const Layout& L, char* ws, hi
   // instantiations, so neither epilogue's registers weigh on the other's main loop
   const bool small = (a->q_heads / a->kv_heads) * a->q_len <= kSmallRows;
   if (!scoring && k2_head_form(a, L.ntiles)) {  // decoding, one KV head per workgroup
-    k.total_wg = L.ntiles * a->kv_heads;
+    const bool half = L.stat_tok < kTileTok;     // half a tile per workgroup (k2_head_tokens)
+    k.total_wg = L.ntiles * (half ? 2 : 1) * a->kv_heads;
     k.per_xcd = (k.total_wg + 7) / 8;
     const dim3 hgrid(8 * k.per_xcd);
-    if (a->head_dim == 128)
-      hipLaunchKernelGGL(keys_scores_head_kernel<128>, hgrid, dim3(kK2Threads), 0, st, k);
+    if (a->head_dim == 128 && half)
+      hipLaunchKernelGGL((keys_scores_head_kernel<128, 4>), hgrid, dim3(256), 0, st, k);
+    else if (a->head_dim == 128)
+      hipLaunchKernelGGL((keys_scores_head_kernel<128, 8>), hgrid, dim3(512), 0, st, k);
+    else if (half)
+      hipLaunchKernelGGL((keys_scores_head_kernel<64, 4>), hgrid, dim3(256), 0, st, k);
     else
-      hipLaunchKernelGGL(keys_scores_head_kernel<64>, hgrid, dim3(kK2Threads), 0, st, k);
+      hipLaunchKernelGGL((keys_scores_head_kernel<64, 8>), hgrid, dim3(512), 0, st, k);
     return dkv::check_launch("keys_scores (one head per workgroup)");
   }
   // probabilities: the value side's blocked layout when decoding, row-major [R][ntiles * 256] for
@@ -2483,19 +2521,24 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
     k.R_total = L.R_total;
     k.n_total = L.n_total;
     k.n_slots = L.n_slots;
-    k.ntiles = L.ntiles;
+    k.nstats = L.nstats;
     k.G = G;
     k.rank = a->rank;
     k.nsplits = L.nsplits;
     k.row_blocks = (L.R_total + 31) / 32;
     k.total_wg = L.nsplits * k.row_blocks * G;
     k.per_xcd = (k.total_wg + 7) / 8;
-    if (L.split_tok == kSplitTok)
-      hipLaunchKernelGGL(value_weights_kernel<kSplitTok / kK3WaveTok>, dim3(8u * (unsigned)k.per_xcd),
-                         dim3(kSplitTok / kK3WaveTok * 64), 0, st, k);
+    constexpr int W8 = kSplitTok / kK3WaveTok, W4 = kSplitTok / 2 / kK3WaveTok;
+    const dim3 grid(8u * (unsigned)k.per_xcd);
+    const bool whole = L.stat_tok == kTileTok;  // one statistics entry per tile
+    if (L.split_tok == kSplitTok && whole)
+      hipLaunchKernelGGL((value_weights_kernel<W8, 1>), grid, dim3(W8 * 64), 0, st, k);
+    else if (L.split_tok == kSplitTok)
+      hipLaunchKernelGGL((value_weights_kernel<W8, 2>), grid, dim3(W8 * 64), 0, st, k);
+    else if (whole)
+      hipLaunchKernelGGL((value_weights_kernel<W4, 1>), grid, dim3(W4 * 64), 0, st, k);
     else
-      hipLaunchKernelGGL(value_weights_kernel<kSplitTok / 2 / kK3WaveTok>, dim3(8u * (unsigned)k.per_xcd),
-                         dim3(kSplitTok / 2 / kK3WaveTok * 64), 0, st, k);
+      hipLaunchKernelGGL((value_weights_kernel<W4, 2>), grid, dim3(W4 * 64), 0, st, k);
     rc = dkv::check_launch("value_weights");
     if (rc) return rc;
   }
@@ -2526,7 +2569,10 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   rc = dkv::check_launch("basis_apply");
   if (rc) return rc;
   // K3c
-  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kRowThreads), 0, st, m);
+  if (L.stat_tok == kTileTok)
+    hipLaunchKernelGGL(finish_kernel<1>, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kRowThreads), 0, st, m);
+  else
+    hipLaunchKernelGGL(finish_kernel<2>, dim3((unsigned)((long)a->batch * L.R_total)), dim3(kRowThreads), 0, st, m);
   return dkv::check_launch("finish");
 }
 
