@@ -19,7 +19,8 @@
 //                      per-tile (max, sum exp) statistics.  The rebuilt keys
 //                      never reach memory.  Decodes whose (tile, head group)
 //                      workgroups would leave CUs idle run one workgroup per
-//                      (tile, KV head) instead (keys_scores_head).
+//                      (tile, KV head) instead (keys_scores_head), or per
+//                      (half tile, KV head) for the shortest contexts.
 //   K3a value_weights: per (1024-token split, 64-component group, 32 rows):
 //                      p @ value codes on MFMA plus sum(p * offset) ->
 //                      coefficient-space partial sums.
