@@ -116,6 +116,7 @@ class CompressedContext:
         self._score_workspace = None
         self._score_prepared = None
         self._cu_exact = {}
+        self._mask_cache = None  # (mask tensor, its version, keys, float32 rows) of the last forward
         self.importance = None  # float32 [n] while a question is being scored
         # Middle tokens held exactly (kvtc's exact rung), per layer float32 [Hkv, E_x, d] (keys RoPE'd);
         # they join the exact tokens of every softmax.
@@ -274,6 +275,17 @@ class CompressedContext:
         return parts
 
     # ----- attention -----
+    def _mask_rows(self, attention_mask: torch.Tensor, keys: int) -> torch.Tensor:
+        """float32 [q_len, keys]: the additive mask's rows over the exact cache.  A forward passes the
+        same mask tensor to every layer, so its conversion is kept while that tensor is (the strong
+        reference keeps its memory from being reused by another mask meanwhile)."""
+        key = (attention_mask, attention_mask._version, keys)
+        cached = self._mask_cache
+        if cached is None or cached[0] is not attention_mask or cached[1:3] != key[1:]:
+            rows = attention_mask[0, 0, :, -keys:].float().contiguous()
+            self._mask_cache = cached = (attention_mask, attention_mask._version, keys, rows)
+        return cached[3]
+
     def _exact_offsets(self, lengths: tuple[int, ...]):
         if lengths not in self._cu_exact:
             host = torch.zeros(len(lengths) + 1, dtype=torch.int32)
@@ -285,7 +297,8 @@ class CompressedContext:
                    value_exact: torch.Tensor | None = None, mask: torch.Tensor | None = None,
                    exact_lengths: tuple[int, ...] | None = None, scaling: float | None = None):
         """Build the C-ABI argument block of one layer.  query [B, Hq, q_len, d] (f32/f16/bf16);
-        out [B, q_len, Hq, d]; key/value_exact float32 [Hkv, E_total, d] (RoPE applied);
+        out [B, q_len, Hq, d]; key/value_exact [Hkv, E_total, d] (RoPE applied), both float32, float16
+        or bfloat16 (one type; the kernels convert to float32 exactly as they load);
         mask float32 [q_len, E] (B == 1)."""
         t = self.tables
         batch, q_heads, q_len, dim = query.shape
@@ -309,7 +322,10 @@ class CompressedContext:
             lengths = exact_lengths if exact_lengths is not None else (key_exact.shape[1],)
             host, dev = self._exact_offsets(tuple(int(x) for x in lengths))
             a.cu_exact, a.cu_exact_host = dev.data_ptr(), host.data_ptr()
+            if value_exact.dtype != key_exact.dtype:
+                raise ValueError(f"exact keys ({key_exact.dtype}) and values ({value_exact.dtype}) differ in type")
             a.key_exact, a.value_exact = dkv_hip.ptr(key_exact), dkv_hip.ptr(value_exact)
+            a.exact_dtype = dkv_hip.dtype_code(key_exact.dtype)
             a.mask = dkv_hip.ptr(mask) if mask is not None else None
         a.out, a.out_dtype = dkv_hip.ptr(out), dkv_hip.dtype_code(out.dtype)
         return a
@@ -347,11 +363,12 @@ class CompressedContext:
         if key is not None and key.shape[2] > 0:
             if batch != 1:
                 raise ValueError("exact caches with batch > 1 go through layer_args(exact_lengths=...)")
-            key_exact = key[0].float().contiguous()
-            value_exact = value[0].float().contiguous()
+            key_exact, value_exact = _exact_operand(key[0]), _exact_operand(value[0])
+            if self.extra is not None or key_exact.dtype != value_exact.dtype:
+                key_exact, value_exact = key_exact.float().contiguous(), value_exact.float().contiguous()
             lengths = (key.shape[2],)
             if attention_mask is not None:
-                mask = attention_mask[0, 0, :, -key.shape[2]:].float().contiguous()
+                mask = self._mask_rows(attention_mask, key.shape[2])
         if self.extra is not None:
             if batch != 1:
                 raise ValueError("a context with exact-rung tokens takes one conversation")
@@ -410,6 +427,16 @@ class CompressedContext:
             dkv_hip.attend_prepare(args, self._score_workspace, self.score_plane_cap, values=False)
             self._score_prepared = state
         dkv_hip.score_layer(args, key_question, self.importance, self._score_workspace)
+
+
+def _exact_operand(t: torch.Tensor) -> torch.Tensor:
+    """A cache's [Hkv, E, d] exact tokens as the kernels take them: float32, float16 or bfloat16 as they
+    are when contiguous and aligned for their four-element loads (a model's fp16 cache needs no
+    conversion), a float32 copy otherwise."""
+    if t.dtype in (torch.float16, torch.bfloat16, torch.float32) and t.is_contiguous():
+        if dkv_hip.addr(t) % (16 if t.dtype == torch.float32 else 8) == 0:
+            return t
+    return t.float().contiguous()
 
 
 def _stops(token: int, tokenizer) -> bool:

@@ -62,8 +62,8 @@ struct RowMergeArgs {
   const float* tile_max;
   const float* tile_sum;
   const float* mean_v;
-  const float* key_exact;
-  const float* value_exact;
+  const void* key_exact;    // [Hkv][E_total][D] in the exact tail's type (row_exact's XT)
+  const void* value_exact;
   const float* mask;
   const void* query;
   const float* out_part;  // [nchunks][batch * R_total][D] value-basis chunk partials (K3b)
@@ -1519,6 +1519,24 @@ constexpr int kExactKR = 2;  // key rounds (8 tokens each) loaded in the first r
 constexpr int kExactKI = 4;  // key loads (16 bytes per lane) per round at D = 128 (2 at D = 64)
 constexpr int kExactVR = 8;  // value loads (16 bytes per lane) in the first round
 
+// Four consecutive elements (16 bytes of f32, 8 of f16 / bf16) of an exact key or value row as floats;
+// the conversion from f16 / bf16 is exact, so every type gives the f32 path's results.
+template <int XT>
+DKV_DEVICE float4 load_exact4(const void* base, long e) {
+  if constexpr (XT == DKV_F32) {
+    return *(const float4*)((const float*)base + e);
+  } else {
+    const uint2 w = *(const uint2*)((const uint16_t*)base + e);
+    if constexpr (XT == DKV_F16)
+      return make_float4(half_bits_to_float((uint16_t)(w.x & 0xffffu)), half_bits_to_float((uint16_t)(w.x >> 16)),
+                         half_bits_to_float((uint16_t)(w.y & 0xffffu)), half_bits_to_float((uint16_t)(w.y >> 16)));
+    else
+      return make_float4(bf16_bits_to_float((uint16_t)(w.x & 0xffffu)), bf16_bits_to_float((uint16_t)(w.x >> 16)),
+                         bf16_bits_to_float((uint16_t)(w.y & 0xffffu)), bf16_bits_to_float((uint16_t)(w.y >> 16)));
+  }
+}
+
+template <int XT>
 __device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) {
   const int lane = threadIdx.x;
   if (lane >= 64) return;  // one wave
@@ -1542,26 +1560,26 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) 
   // scores: lane (kj, ks) takes dimensions 4 ks + 32 i .. +4 (i < D / 32) of token kj of each round
   const int kj = lane >> 3, ks = lane & 7;
   const int ni = D / 32;
-  const float* krow0 = a.key_exact + ((long)h * a.E_total + e0) * D + 4 * ks;
+  const long krow0 = ((long)h * a.E_total + e0) * D + 4 * ks;  // element index
   const float* mrow0 = a.mask ? a.mask + (long)qi * E_seq + j0s : nullptr;
   // values: lane (tp, dq) holds dimensions 4 dq .. 4 dq + 3 of token slot tp
   const int lpt = D / 4;  // lanes per token
   const int tpi = 64 / lpt;  // tokens per value load
   const int dq = lane % lpt, tp = lane / lpt;
-  const float* vrow0 = a.value_exact + ((long)h * a.E_total + e0) * D + 4 * dq;
+  const long vrow0 = ((long)h * a.E_total + e0) * D + 4 * dq;  // element index
   float4 k4[kExactKR][kExactKI];
   float mv[kExactKR];
   float4 v4[kExactVR];
   if (E > 0) {
 #pragma unroll
     for (int r = 0; r < kExactKR; ++r) {
-      const float* kr = krow0 + (long)min(r * 8 + kj, E - 1) * D;
+      const long kr = krow0 + (long)min(r * 8 + kj, E - 1) * D;
 #pragma unroll
-      for (int i = 0; i < kExactKI; ++i) k4[r][i] = *(const float4*)(kr + 32 * min(i, ni - 1));
+      for (int i = 0; i < kExactKI; ++i) k4[r][i] = load_exact4<XT>(a.key_exact, kr + 32 * min(i, ni - 1));
       mv[r] = mrow0 ? mrow0[min(r * 8 + kj, E - 1)] : 0.0f;
     }
 #pragma unroll
-    for (int i = 0; i < kExactVR; ++i) v4[i] = *(const float4*)(vrow0 + (long)min(tp + i * tpi, E - 1) * D);
+    for (int i = 0; i < kExactVR; ++i) v4[i] = load_exact4<XT>(a.value_exact, vrow0 + (long)min(tp + i * tpi, E - 1) * D);
   }
   if (lane < D) q[lane] = query_word_value(qw0, qbase + lane, a.query_dtype);
   if (lane + 64 < D) q[lane + 64] = query_word_value(qw1, qbase + lane + 64, a.query_dtype);
@@ -1588,9 +1606,9 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) 
     for (int r = 0; r < kExactKR; ++r) m = fmaxf(m, score(k4[r], mv[r], r * 8 + kj));
     for (int j0 = kExactKR * 8; j0 < E; j0 += 8) {  // more than kExactKR * 8 tokens in the share
       float4 kk[kExactKI];
-      const float* kr = krow0 + (long)min(j0 + kj, E - 1) * D;
+      const long kr = krow0 + (long)min(j0 + kj, E - 1) * D;
 #pragma unroll
-      for (int i = 0; i < kExactKI; ++i) kk[i] = *(const float4*)(kr + 32 * min(i, ni - 1));
+      for (int i = 0; i < kExactKI; ++i) kk[i] = load_exact4<XT>(a.key_exact, kr + 32 * min(i, ni - 1));
       const float mval = mrow0 ? mrow0[min(j0 + kj, E - 1)] : 0.0f;
       m = fmaxf(m, score(kk, mval, j0 + kj));
     }
@@ -1616,7 +1634,7 @@ __device__ void row_exact(const RowMergeArgs& a, int wg, int part, float* smem) 
     }
     for (int t0 = kExactVR * tpi; t0 < E; t0 += tpi) {  // tokens past the first round's values
       const int t = t0 + tp;
-      const float4 vv = *(const float4*)(vrow0 + (long)min(t, E - 1) * D);
+      const float4 vv = load_exact4<XT>(a.value_exact, vrow0 + (long)min(t, E - 1) * D);
       const float w = t < E ? se[min(t, kExactShare - 1)] : 0.0f;
       acc.x += w * vv.x;
       acc.y += w * vv.y;
@@ -2081,12 +2099,12 @@ constexpr int kK3bComp = kChunk / kK3bParts;  // 16 components per thread
 constexpr int kK3bDims = 64;                  // dimensions per workgroup
 
 // (at most two waves per SIMD: the exact-tail role's registers are not capped for occupancy)
-template <int NR>
+template <int NR, int XT>
 __global__ __launch_bounds__(kRowThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void basis_apply_kernel(K3bArgs a, RowMergeArgs ex) {
   if ((int)blockIdx.x < a.n_exact_wg) {  // share blockIdx.x % kExactParts of output row blockIdx.x / kExactParts
     __shared__ __attribute__((aligned(16))) float xsm[kExactLds];
-    row_exact(ex, blockIdx.x / kExactParts, blockIdx.x % kExactParts, xsm);
+    row_exact<XT>(ex, blockIdx.x / kExactParts, blockIdx.x % kExactParts, xsm);
     return;
   }
   __shared__ __attribute__((aligned(16))) float W[NR][kChunk];  // the pass's summed weights
@@ -2333,6 +2351,13 @@ RowMergeArgs row_merge_args(const dkv_attend_args_t* a, const Layout& L, char* w
 int check_exact(const dkv_attend_args_t* a, int& E_total, const char* what) {
   DKV_REQUIRE(!a->mask || a->batch == 1, DKV_ESHAPE, "%s: mask is only supported for batch == 1", what);
   DKV_REQUIRE(!a->cu_exact || (a->key_exact && a->value_exact), DKV_EINVAL, "%s: exact keys/values missing", what);
+  DKV_REQUIRE(a->exact_dtype == DKV_F32 || a->exact_dtype == DKV_F16 || a->exact_dtype == DKV_BF16, DKV_EINVAL,
+              "%s: exact_dtype %d is not DKV_F32, DKV_F16 or DKV_BF16", what, a->exact_dtype);
+  {  // row_exact reads four elements per load: 16 bytes of f32, 8 of f16 / bf16
+    const uintptr_t align = a->exact_dtype == DKV_F32 ? 16 : 8;
+    DKV_REQUIRE(!a->cu_exact || ((uintptr_t)a->key_exact % align == 0 && (uintptr_t)a->value_exact % align == 0),
+                DKV_EINVAL, "%s: exact keys/values must be %d-byte aligned", what, (int)align);
+  }
   E_total = 0;
   if (a->cu_exact) {
     DKV_REQUIRE(a->cu_exact_host, DKV_EINVAL, "%s: cu_exact needs cu_exact_host", what);
@@ -2563,10 +2588,23 @@ extern "C" int dkv_attend_values(const dkv_attend_args_t* a, void* workspace, si
   kb.split_tok = L.split_tok;
   kb.n_exact_wg = a->batch * L.R_total * kExactParts;
   const long k3b_blocks = kb.n_exact_wg + (long)a->batch * a->kv_heads * L.nchunks * (a->head_dim / kK3bDims);
-  if ((a->q_heads / a->kv_heads) * a->q_len <= 4)
-    hipLaunchKernelGGL(basis_apply_kernel<4>, dim3((unsigned)k3b_blocks), dim3(kRowThreads), 0, st, kb, m);
-  else
-    hipLaunchKernelGGL(basis_apply_kernel<8>, dim3((unsigned)k3b_blocks), dim3(kRowThreads), 0, st, kb, m);
+  const bool rows4 = (a->q_heads / a->kv_heads) * a->q_len <= 4;
+  auto k3b = [&](auto nr, auto xt) {
+    hipLaunchKernelGGL((basis_apply_kernel<decltype(nr)::value, decltype(xt)::value>), dim3((unsigned)k3b_blocks),
+                       dim3(kRowThreads), 0, st, kb, m);
+  };
+  using R4 = std::integral_constant<int, 4>;
+  using R8 = std::integral_constant<int, 8>;
+  using X32 = std::integral_constant<int, DKV_F32>;
+  using X16 = std::integral_constant<int, DKV_F16>;
+  using XB16 = std::integral_constant<int, DKV_BF16>;
+  if (a->exact_dtype == DKV_F16) {
+    if (rows4) k3b(R4{}, X16{}); else k3b(R8{}, X16{});
+  } else if (a->exact_dtype == DKV_BF16) {
+    if (rows4) k3b(R4{}, XB16{}); else k3b(R8{}, XB16{});
+  } else {
+    if (rows4) k3b(R4{}, X32{}); else k3b(R8{}, X32{});
+  }
   rc = dkv::check_launch("basis_apply");
   if (rc) return rc;
   // K3c
@@ -3105,6 +3143,8 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   int E = 0;
   if (a->cu_exact) {
     DKV_REQUIRE(a->cu_exact_host && a->key_exact, DKV_EINVAL, "dkv_score_layer: exact keys need host offsets");
+    DKV_REQUIRE(a->exact_dtype == DKV_F32, DKV_EINVAL, "dkv_score_layer: exact keys must be f32 (exact_dtype %d)",
+                a->exact_dtype);
     DKV_REQUIRE(a->cu_exact_host[0] == 0, DKV_ESHAPE, "dkv_score_layer: cu_exact[0] must be 0");
     E = a->cu_exact_host[1] - a->cu_exact_host[0];
   }
@@ -3122,7 +3162,7 @@ extern "C" int dkv_score_layer(const dkv_attend_args_t* a, const float* key_ques
   if (rc) return rc;
   RowStatsArgs e{};
   e.query = a->query;
-  e.key_exact = a->key_exact;
+  e.key_exact = (const float*)a->key_exact;
   e.key_question = key_question;
   e.sub_max = (const float*)(ws + S.sub_max[cur]);
   e.sub_sum = (const float*)(ws + S.sub_sum);

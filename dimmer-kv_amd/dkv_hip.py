@@ -68,7 +68,7 @@ class AttendArgs(ctypes.Structure):
         ("rope_cos", c_vp), ("rope_sin", c_vp), ("rope_rows", c_i32),
         ("query", c_vp), ("query_dtype", c_i32),
         ("cu_exact", c_vp), ("cu_exact_host", c_vp), ("key_exact", c_vp), ("value_exact", c_vp), ("mask", c_vp),
-        ("out", c_vp), ("out_dtype", c_i32),
+        ("out", c_vp), ("out_dtype", c_i32), ("exact_dtype", c_i32),
     ]
 
 

@@ -238,11 +238,14 @@ typedef struct dkv_attend_args {
   int32_t query_dtype;
   const int32_t* cu_exact;        /* [batch+1] with cu_exact[0] == 0, or NULL (no exact tokens) */
   const int32_t* cu_exact_host;   /* host mirror of cu_exact (<= 1024 exact tokens per sequence) */
-  const float* key_exact;         /* [Hkv][E_total][d] f32, RoPE applied */
-  const float* value_exact;       /* [Hkv][E_total][d] f32 */
+  const void* key_exact;          /* [Hkv][E_total][d] in exact_dtype, RoPE applied */
+  const void* value_exact;        /* [Hkv][E_total][d] in exact_dtype */
   const float* mask;              /* [q_len][E] additive (batch == 1 only) or NULL */
   void* out;                      /* [batch][q_len][Hq][d], out_dtype */
   int32_t out_dtype;
+  int32_t exact_dtype;            /* DKV_F32 (0), DKV_F16 or DKV_BF16: the type of key_exact and value_exact
+                                     (a model's own cache can be passed as it is; the kernels compute in f32);
+                                     dkv_score_layer takes DKV_F32 only */
 } dkv_attend_args_t;
 
 size_t dkv_attend_workspace_bytes(const dkv_attend_args_t* a);

@@ -137,6 +137,45 @@ def test_attend_exact_tail_lengths(shape_name, tokens, sinks, recent, q_len):
         print(f"  zeroed exact values move the output by {gap:.2e} (relative)", flush=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attend_exact_tail_in_cache_type(dtype):
+    """The exact tail read in the model cache's own type (exact_dtype f16 / bf16, converted to float32
+    as the kernels load it) gives the float32 path's output bit for bit, through the C ABI directly and
+    through the attention hook, which now passes an fp16 / bf16 cache on as it is."""
+    import types
+
+    shape = synth.ModelShape(2, 8, 128, 24, 2048)
+    print(f"[case] exact tail in {dtype}: 3B heads, T=900, 305 exact tokens, q_len=2", flush=True)
+    case = build_case(shape, 900, seed=4322, query_scale=20.0, q_len=2, sinks=4, recent=300)
+    ctx, _, _ = gpu_context(case)
+    layer = 1
+    q = case.queries[layer].to(DEV).contiguous()
+    ke = case.key_exact[layer].to(DEV, dtype).contiguous()
+    ve = case.value_exact[layer].to(DEV, dtype).contiguous()
+    mask = case.mask.to(DEV).contiguous()
+    outs = []
+    for k, v in ((ke, ve), (ke.float(), ve.float())):
+        out = torch.empty(1, case.q_len, shape.q_heads, shape.head_dim, device=DEV)
+        args = ctx.layer_args(layer, q, out, k, v, mask)
+        assert args.exact_dtype == (0 if k.dtype == torch.float32 else 1 if k.dtype == torch.float16 else 2)
+        ctx.run_layer(args)
+        outs.append(out)
+    # the hook: key / value as a model cache hands them over ([1, Hkv, E, d]) with an additive mask
+    module = types.SimpleNamespace(layer_idx=layer, num_key_value_groups=shape.q_heads // shape.kv_heads)
+    hook_out, _ = ctx.attend(module, q.to(dtype), ke[None], ve[None], mask[None, None], None)
+    ref_out = torch.empty(1, case.q_len, shape.q_heads, shape.head_dim, dtype=dtype, device=DEV)
+    ctx.run_layer(ctx.layer_args(layer, q.to(dtype), ref_out, ke.float(), ve.float(), mask))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]), f"{dtype} exact tail differs from its float32 copy"
+    assert torch.equal(hook_out, ref_out), "the hook's cache-type exact tail differs from the float32 path"
+    from dataclasses import replace
+
+    rounded = replace(case, key_exact=case.key_exact.to(dtype).float(), value_exact=case.value_exact.to(dtype).float())
+    ref = oracle_attend(rounded, layer)  # the oracle over the same (rounded) exact tokens
+    err, _ = assert_close(outs[0].cpu().numpy(), ref, what=f"exact tail in {dtype}", base=value_mean_base(case, layer))
+    print(f"  bit-identical to float32; max abs err vs oracle {err:.2e}", flush=True)
+
+
 def test_attend_special_cases():
     """Closed forms: all tokens at 0 planes and no exact part -> output = mean_v;
     a zero query -> the plain average of the decoded values."""

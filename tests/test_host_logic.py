@@ -198,3 +198,37 @@ def test_failed_refine_gives_back_slots_and_version():
     assert (st.refined, st.version) == (8, 4)
     assert st.settle_refine(torch.tensor([2176, 0]), 4) == 2176
     assert (st.refined, st.version) == (8, 4)
+
+
+def test_exact_operand_and_mask_rows():
+    """The hook hands the kernels a model cache's exact tokens in their own type when they are
+    contiguous and aligned for four-element loads (float32 copies otherwise), and converts the
+    additive mask once per mask tensor (again when the tensor changes in place or the key count does)."""
+    import types
+
+    from compressed_attention import CompressedContext, _exact_operand
+
+    cache = torch.randn(1, 8, 40, 64, dtype=torch.float16)
+    assert _exact_operand(cache[0]) is not None and _exact_operand(cache[0]).data_ptr() == cache.data_ptr()
+    bf = cache.to(torch.bfloat16)
+    assert _exact_operand(bf[0]).dtype == torch.bfloat16
+    strided = cache[0, :, ::2]
+    got = _exact_operand(strided)
+    assert got.dtype == torch.float32 and got.is_contiguous() and torch.equal(got, strided.float())
+    flat = torch.randn(8 * 40 * 64 + 1, dtype=torch.float16)
+    shifted = flat[1:].view(8, 40, 64)  # 2-byte offset: not aligned for 8-byte loads
+    assert _exact_operand(shifted).dtype == torch.float32
+    assert _exact_operand(torch.randn(2, 3, 4, dtype=torch.float64)).dtype == torch.float32
+
+    ctx = types.SimpleNamespace(_mask_cache=None)
+    mask = torch.zeros(1, 1, 2, 50, dtype=torch.float16)
+    mask[..., -1] = -1e4
+    rows = CompressedContext._mask_rows(ctx, mask, 40)
+    assert rows.dtype == torch.float32 and rows.shape == (2, 40) and torch.equal(rows, mask[0, 0, :, -40:].float())
+    assert CompressedContext._mask_rows(ctx, mask, 40) is rows  # every layer of one forward: converted once
+    mask[..., -2] = -1e4  # changed in place: converted again
+    again = CompressedContext._mask_rows(ctx, mask, 40)
+    assert again is not rows and float(again[0, -2]) == -1e4
+    assert CompressedContext._mask_rows(ctx, mask, 41).shape == (2, 41)
+    other = mask.clone()
+    assert CompressedContext._mask_rows(ctx, other, 41) is not CompressedContext._mask_rows(ctx, mask, 41)
