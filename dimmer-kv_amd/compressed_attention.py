@@ -117,6 +117,7 @@ class CompressedContext:
         self._score_prepared = None
         self._cu_exact = {}
         self._mask_cache = None  # (mask tensor, its version, keys, float32 rows) of the last forward
+        self._args_static = None  # (key stream, value stream, their array addresses, the shared argument fields)
         self.importance = None  # float32 [n] while a question is being scored
         # Middle tokens held exactly (kvtc's exact rung), per layer float32 [Hkv, E_x, d] (keys RoPE'd);
         # they join the exact tokens of every softmax.
@@ -305,18 +306,9 @@ class CompressedContext:
         if batch != self.batch or q_heads != self.q_heads or dim != t.head_dim:
             raise ValueError(f"query {tuple(query.shape)} does not match the context "
                              f"(batch {self.batch}, {self.q_heads} heads, head_dim {t.head_dim})")
-        a = dkv_hip.AttendArgs()
-        a.batch, a.q_len = batch, q_len
-        a.layers, a.layer, a.kv_heads, a.head_dim, a.q_heads, a.rank = (t.layers, layer, t.kv_heads, t.head_dim,
-                                                                         q_heads, t.rank)
+        a = dkv_hip.AttendArgs.from_buffer_copy(self._static_args())
+        a.q_len, a.layer, a.q_heads = q_len, layer, q_heads
         a.scaling = dim ** -0.5 if scaling is None else float(scaling)
-        a.key, a.value = self.key.c_stream(), self.value.c_stream()
-        a.cu_seqlens = self.cu.data_ptr()
-        a.cu_seqlens_host = self.cu_host.data_ptr()
-        a.positions = dkv_hip.addr(self.positions)
-        a.key_basis, a.value_basis = t.key_basis.data_ptr(), t.value_basis.data_ptr()
-        a.mean_k, a.mean_v = t.mean_k.data_ptr(), t.mean_v.data_ptr()
-        a.rope_cos, a.rope_sin, a.rope_rows = t.rope_cos.data_ptr(), t.rope_sin.data_ptr(), t.rope_cos.shape[0]
         a.query, a.query_dtype = dkv_hip.ptr(query), dkv_hip.dtype_code(query.dtype)
         if key_exact is not None and key_exact.shape[1] > 0:
             lengths = exact_lengths if exact_lengths is not None else (key_exact.shape[1],)
@@ -329,6 +321,26 @@ class CompressedContext:
             a.mask = dkv_hip.ptr(mask) if mask is not None else None
         a.out, a.out_dtype = dkv_hip.ptr(out), dkv_hip.dtype_code(out.dtype)
         return a
+
+    def _static_args(self) -> dkv_hip.AttendArgs:
+        """The fields of the argument block that every layer shares (shapes, streams, bases, tables),
+        built again only when a stream's arrays move (a refine that grows the hot blob)."""
+        ptrs = tuple(x.data_ptr() for s in (self.key, self.value) for x in (s.blob, s.tok_off, s.pieces))
+        cached = self._args_static
+        if cached is None or cached[0] is not self.key or cached[1] is not self.value or cached[2] != ptrs:
+            t = self.tables
+            a = dkv_hip.AttendArgs()
+            a.batch = self.batch
+            a.layers, a.kv_heads, a.head_dim, a.rank = t.layers, t.kv_heads, t.head_dim, t.rank
+            a.key, a.value = self.key.c_stream(), self.value.c_stream()
+            a.cu_seqlens = self.cu.data_ptr()
+            a.cu_seqlens_host = self.cu_host.data_ptr()
+            a.positions = dkv_hip.addr(self.positions)
+            a.key_basis, a.value_basis = t.key_basis.data_ptr(), t.value_basis.data_ptr()
+            a.mean_k, a.mean_v = t.mean_k.data_ptr(), t.mean_v.data_ptr()
+            a.rope_cos, a.rope_sin, a.rope_rows = t.rope_cos.data_ptr(), t.rope_sin.data_ptr(), t.rope_cos.shape[0]
+            self._args_static = cached = (self.key, self.value, ptrs, a)
+        return cached[3]
 
     def workspace(self, args) -> torch.Tensor:
         need = dkv_hip.attend_workspace_bytes(args)

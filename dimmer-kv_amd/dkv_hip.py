@@ -128,7 +128,16 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return addr(t)
 
 
+try:  # the raw handle of the current stream, without a Python stream object per call
+    from torch._C import _cuda_getCurrentRawStream as _raw_stream, _cuda_getDevice as _current_device
+except ImportError:  # pragma: no cover - older torch
+    _raw_stream = _current_device = None
+
+
 def stream_handle() -> int:
+    """The current HIP stream of the current device (what torch.cuda.current_stream().cuda_stream gives)."""
+    if _raw_stream is not None:
+        return _raw_stream(_current_device())
     return torch.cuda.current_stream().cuda_stream
 
 

@@ -137,6 +137,18 @@ def test_attend_exact_tail_lengths(shape_name, tokens, sinks, recent, q_len):
         print(f"  zeroed exact values move the output by {gap:.2e} (relative)", flush=True)
 
 
+def test_stream_handle_is_torch_current_stream():
+    """The launch stream the bindings pass (torch's raw-stream accessor) is torch's current stream,
+    also inside a ``torch.cuda.stream`` block."""
+    import dkv_hip
+
+    assert dkv_hip.stream_handle() == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert dkv_hip.stream_handle() == side.cuda_stream == torch.cuda.current_stream().cuda_stream
+    assert dkv_hip.stream_handle() == torch.cuda.current_stream().cuda_stream
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_attend_exact_tail_in_cache_type(dtype):
     """The exact tail read in the model cache's own type (exact_dtype f16 / bf16, converted to float32
