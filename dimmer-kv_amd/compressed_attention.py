@@ -288,9 +288,14 @@ class CompressedContext:
         return cached[3]
 
     def _exact_offsets(self, lengths: tuple[int, ...]):
+        """cu_exact (host and device) for these exact-tail lengths.  The tail grows by a token per decode
+        step, so only the last few are kept (a dropped device array goes back to torch's allocator in
+        stream order, after the kernels queued on the stream that read it)."""
         if lengths not in self._cu_exact:
             host = torch.zeros(len(lengths) + 1, dtype=torch.int32)
             host[1:] = torch.cumsum(torch.tensor(lengths, dtype=torch.int32), 0)
+            while len(self._cu_exact) >= 8:
+                self._cu_exact.pop(next(iter(self._cu_exact)))
             self._cu_exact[lengths] = (host, host.to(self.key.blob.device))
         return self._cu_exact[lengths]
 

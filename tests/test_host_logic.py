@@ -232,3 +232,21 @@ def test_exact_operand_and_mask_rows():
     assert CompressedContext._mask_rows(ctx, mask, 41).shape == (2, 41)
     other = mask.clone()
     assert CompressedContext._mask_rows(ctx, other, 41) is not CompressedContext._mask_rows(ctx, mask, 41)
+
+
+def test_exact_offsets_keep_the_last_few():
+    """cu_exact arrays are made once per exact-tail length and only the last eight lengths are kept
+    (a long reply adds one length per token)."""
+    import types
+
+    from compressed_attention import CompressedContext
+
+    ctx = types.SimpleNamespace(key=types.SimpleNamespace(blob=torch.zeros(1)), _cu_exact={})
+    first = CompressedContext._exact_offsets(ctx, (37,))
+    assert CompressedContext._exact_offsets(ctx, (37,)) is first
+    for n in range(38, 60):
+        host, dev = CompressedContext._exact_offsets(ctx, (n,))
+        assert host.tolist() == [0, n] and dev.tolist() == [0, n]
+    assert len(ctx._cu_exact) == 8 and (37,) not in ctx._cu_exact
+    host, _ = CompressedContext._exact_offsets(ctx, (3, 4, 5))
+    assert host.tolist() == [0, 3, 7, 12]
