@@ -16,7 +16,7 @@ import torch
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libdimmerkv_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DKV_F32, DKV_F16, DKV_BF16 = 0, 1, 2
 DKV_FMT_PLANES, DKV_FMT_LADDER = 0, 1

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define DKV_ABI_VERSION 2
+#define DKV_ABI_VERSION 3  /* 3: dkv_attend_args_t.exact_dtype; 2: dkv_stream_t.format */
 
 /* Status codes.  The Python wrapper maps them to the reference's exception
  * types: DKV_EINVAL/DKV_ESHAPE -> ValueError, DKV_EBUDGET -> AssertionError,
