@@ -150,3 +150,34 @@ def test_prepare_refuses_stream_tables_beyond_the_decode_lds_column():
     assert need > 0
     rc = lib.dkv_attend_prepare(ctypes.byref(a), ctypes.c_int32(8), fake, ctypes.c_size_t(need), None)
     assert rc == -2 and b"table has 5000 rows" in lib.dkv_last_error()
+
+
+def test_layer_refuses_bad_exact_dtype_and_misaligned_exact_tokens():
+    """exact_dtype must be DKV_F32, DKV_F16 or DKV_BF16, and the exact keys / values aligned for the
+    kernels' four-element loads (16 bytes for f32, 8 for the 16-bit types): refused on the host before
+    any device work."""
+    lib = dkv_hip.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: refused before any device work
+    order = dkv_hip.Order(32, 256, fake, fake, fake, fake)
+    stream = dkv_hip.Stream(fake, fake, fake, order, dkv_hip.DKV_FMT_PLANES, dkv_hip.Ladder())
+    cu_host = (ctypes.c_int32 * 2)(0, 1000)
+    ex_host = (ctypes.c_int32 * 2)(0, 37)
+    a = dkv_hip.AttendArgs()
+    a.batch, a.q_len, a.layers, a.layer, a.kv_heads, a.head_dim, a.q_heads, a.rank = 1, 1, 28, 0, 8, 128, 24, 2048
+    a.scaling = 128 ** -0.5
+    a.key, a.value = stream, stream
+    a.cu_seqlens = a.positions = a.key_basis = a.value_basis = a.mean_k = a.mean_v = 256
+    a.rope_cos = a.rope_sin = a.query = a.out = 256
+    a.rope_rows = 1001
+    a.cu_seqlens_host = ctypes.cast(cu_host, ctypes.c_void_p).value
+    a.cu_exact, a.cu_exact_host = 256, ctypes.cast(ex_host, ctypes.c_void_p).value
+    a.key_exact = a.value_exact = 512
+    a.exact_dtype = 7
+    assert lib.dkv_attend_layer(ctypes.byref(a), None, ctypes.c_size_t(0), None) == -1  # DKV_EINVAL
+    assert b"exact_dtype 7" in lib.dkv_last_error()
+    a.exact_dtype, a.key_exact = 0, 520  # f32 needs 16-byte alignment
+    assert lib.dkv_attend_layer(ctypes.byref(a), None, ctypes.c_size_t(0), None) == -1
+    assert b"16-byte aligned" in lib.dkv_last_error()
+    a.exact_dtype, a.value_exact = 1, 514  # f16 needs 8
+    assert lib.dkv_attend_layer(ctypes.byref(a), None, ctypes.c_size_t(0), None) == -1
+    assert b"8-byte aligned" in lib.dkv_last_error()
